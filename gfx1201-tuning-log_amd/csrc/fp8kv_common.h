@@ -1,0 +1,87 @@
+// Shared device helpers for the gfx950 (CDNA4, wave64) kernels of this library.
+//
+// Formats handled here:
+//   * e2m1 (MXFP4 element): sign | 2-bit exponent (bias 1) | 1-bit mantissa; two codes per byte,
+//     LOW nibble = even k (the Quark checkpoint layout read by h4mv/h4mv.cu:2-3).
+//   * e8m0 (MX block scale): 2^(b-127) for b in [0,254], b = 255 is NaN (OCP MX v1.0).
+//   * e4m3fn (KV cache): bias 7, no infinities, 0x7F/0xFF are NaN, max 448.
+// All conversions use the gfx950 scaled-convert instructions, which take the packed codes
+// straight from a VGPR and return bf16 pairs; e2m1 * 2^k and e4m3 values are exact in bf16.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+#define FP8KV_WAVE 64
+
+// e8m0 byte -> f32 scale.  Byte 0 is 2^-127 (an f32 subnormal), byte 255 is NaN.
+__device__ __forceinline__ float e8m0_to_f32(uint32_t b) {
+    uint32_t bits = b << 23;
+    bits = (b == 0u) ? 0x00400000u : bits;
+    bits = (b == 255u) ? 0x7fc00000u : bits;
+    return __uint_as_float(bits);
+}
+
+// Two e2m1 codes held in byte `sel` (0..3) of `w` -> (lo nibble, hi nibble) as bf16, times `scale`.
+template <int SEL>
+__device__ __forceinline__ bf16x2_t fp4x2_to_bf16x2(uint32_t w, float scale) {
+    return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, SEL);
+}
+
+// Four e2m1 bytes (8 codes) of one dword -> 8 bf16 (an MFMA A/B fragment), times `scale`.
+__device__ __forceinline__ bf16x8_t fp4x8_to_bf16x8(uint32_t w, float scale) {
+    bf16x2_t p0 = fp4x2_to_bf16x2<0>(w, scale);
+    bf16x2_t p1 = fp4x2_to_bf16x2<1>(w, scale);
+    bf16x2_t p2 = fp4x2_to_bf16x2<2>(w, scale);
+    bf16x2_t p3 = fp4x2_to_bf16x2<3>(w, scale);
+    bf16x8_t r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+// Two e4m3fn bytes held in the low (HI=false) or high (HI=true) 16 bits of `w` -> bf16 pair.
+template <bool HI>
+__device__ __forceinline__ bf16x2_t fp8x2_to_bf16x2(uint32_t w) {
+    return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
+}
+
+// Eight e4m3fn bytes (two dwords, byte order = element order) -> bf16x8.
+__device__ __forceinline__ bf16x8_t fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+    bf16x2_t a = fp8x2_to_bf16x2<false>(lo);
+    bf16x2_t b = fp8x2_to_bf16x2<true>(lo);
+    bf16x2_t c = fp8x2_to_bf16x2<false>(hi);
+    bf16x2_t d = fp8x2_to_bf16x2<true>(hi);
+    bf16x8_t r;
+    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+    r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+    return r;
+}
+
+// f32 -> bf16 bits, round to nearest even (NaN stays NaN): v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    bf2 v;
+    v[0] = (__bf16)lo;
+    v[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ f32x4_t mfma16x16x32_bf16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// Non-temporal 16-byte global load: weight and KV streams are read exactly once per launch.
+__device__ __forceinline__ u32x4_t load_nt_16(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+}
+__device__ __forceinline__ u32x4_t load_16(const void* p) {
+    return *reinterpret_cast<const u32x4_t*>(p);
+}

@@ -1,0 +1,67 @@
+"""ctypes binding of libfp8kv_amd.so (declarations: include/fp8kv_amd.h).
+
+The library path is FP8KV_AMD_LIB if set, else the in-tree build next to this package.
+Loading fails loudly: there is no CPU or Python fallback for any kernel.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from .build import LIB_PATH
+
+_c_vp = ctypes.c_void_p
+_c_i = ctypes.c_int
+_c_i64 = ctypes.c_int64
+_c_f = ctypes.c_float
+_c_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes).  Mirrors include/fp8kv_amd.h.
+SIGNATURES: dict[str, tuple] = {
+    "fp8kv_status_string": (ctypes.c_char_p, [_c_i]),
+    "fp8kv_last_status": (_c_i, []),
+    # reference ABI, h4mv/h4mv.cu:106-107 / h4mv/fp8kv_hipw4.py:21-23
+    "h4mv_launch": (None, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
+    "h4mv_launch_status": (_c_i, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class Fp8kvError(RuntimeError):
+    """A C-ABI entry point returned a non-zero status."""
+
+    def __init__(self, fn: str, status: int, msg: str):
+        super().__init__(f"{fn} failed: status {status} ({msg})")
+        self.status = status
+
+
+def lib_path() -> str:
+    return os.environ.get("FP8KV_AMD_LIB") or LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and type the library; raises if it is missing."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = lib_path()
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} is missing: build it with fp8kv_amd.build.build() (no fallback path exists)")
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def check(fn_name: str, status: int) -> None:
+    if status != 0:
+        msg = load().fp8kv_status_string(status).decode()
+        raise Fp8kvError(fn_name, status, msg)

@@ -1,0 +1,61 @@
+"""Build libfp8kv_amd.so (all HIP kernels + the C ABI) for gfx950 with hipcc, in-tree.
+
+Usage: ``python -m fp8kv_amd.build`` (with gfx1201-tuning-log_amd/ on sys.path) or
+``fp8kv_amd.build.build()``.  The library lands next to the package directory, which is where
+``fp8kv_amd._lib`` looks for it (override with FP8KV_AMD_LIB).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))   # gfx1201-tuning-log_amd/
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+CSRC = os.path.join(PKG_ROOT, "csrc")
+INCLUDE = os.path.join(REPO_ROOT, "include")
+LIB_NAME = "libfp8kv_amd.so"
+LIB_PATH = os.path.join(PKG_ROOT, LIB_NAME)
+
+SOURCES = ["h4mv.hip"]
+
+# Packed-fp32 VALU forms are disabled for every HIP file built here (the compiler would otherwise
+# emit v_pk_{add,mul,fma}_f32 from ordinary float code).
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise FileNotFoundError("hipcc not found (set HIPCC)")
+
+
+def build(out: str = LIB_PATH, verbose: bool = False) -> str:
+    """Compile every source in SOURCES into one shared library; atomic replace of ``out``."""
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    fd, tmp = tempfile.mkstemp(prefix=".fp8kv_amd_", suffix=".so", dir=os.path.dirname(out))
+    os.close(fd)
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), file=sys.stderr)
+    try:
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-6000:]}")
+        os.chmod(tmp, 0o755)
+        os.replace(tmp, out)
+    finally:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+    return out
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,188 @@
+"""GPU parity of the MXFP4 W4A16 matvec (h4mv_launch) against the CPU oracle.
+
+Bar: rel-to-max error (h4mv/h4mv_test.py:74) < 2e-3; the one-hot and integer probes are exact.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from fp8kv_amd import _lib, ops, workloads
+from oracle import matvec
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 2e-3
+
+
+def _run(case, M=None, dev=DEV):
+    X = case["X"] if M is None else case["X"][:M]
+    y = ops.h4mv(X.to(dev).contiguous(), case["W"].to(dev), case["St"].to(dev))
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+def _oracle(case, M=None):
+    X = case["X"] if M is None else case["X"][:M]
+    return matvec.w4mv(case["W"].numpy(), case["St"].numpy(), X.float().numpy())
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 16])
+def test_one_hot_probes_exact(M):
+    """h4mv/h4mv_test.py:38-52 on every k of a group, for M rows (M = 16 beyond the reference)."""
+    N, K = 4, 32
+    St = torch.full((N, 1), 127, dtype=torch.uint8, device=DEV)
+    for k in range(32):
+        W = torch.zeros(N, K // 2, dtype=torch.uint8, device=DEV)
+        W[:, k // 2] = 2 if k % 2 == 0 else (2 << 4)
+        X = torch.zeros(M, K, dtype=torch.bfloat16, device=DEV)
+        X[:, k] = 1.0
+        y = ops.h4mv(X, W, St)
+        torch.cuda.synchronize()
+        assert torch.equal(y.float().cpu(), torch.ones(M, N)), f"k={k} M={M}: {y[0].tolist()}"
+
+
+def test_one_hot_probes_across_groups_and_rows():
+    """Distinct value per (row, group) so a wrong group/row/scale pairing cannot cancel out."""
+    N, K, M = 37, 512, 3
+    G = K // 32
+    rng = np.random.default_rng(4)
+    St = rng.integers(120, 135, (N, G), dtype=np.uint8)
+    for k in [0, 1, 31, 32, 63, 200, 255, 256, 480, 511]:
+        codes = np.zeros((N, K), dtype=np.uint8)
+        codes[:, k] = rng.integers(1, 16, N).astype(np.uint8)
+        from oracle.formats import pack_e2m1
+        W = pack_e2m1(codes)
+        X = np.zeros((M, K), dtype=np.float32)
+        X[:, k] = [1.0, -2.0, 0.5][:M]
+        case = {"W": torch.from_numpy(W), "St": torch.from_numpy(St),
+                "X": torch.from_numpy(X).to(torch.bfloat16)}
+        assert np.array_equal(_run(case), _oracle(case)), f"k={k}"
+
+
+def test_integer_full_row_exact():
+    """w4-hip-demo/probe_w4hip.py:33-47 (scale 127, x = (k mod 7) - 3): exact in fp32."""
+    g = torch.Generator().manual_seed(0)
+    N, K = 8, 4096
+    W = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, generator=g)
+    St = torch.full((N, K // 32), 127, dtype=torch.uint8)
+    X = (torch.arange(K) % 7 - 3).to(torch.bfloat16)[None, :]
+    case = {"W": W, "St": St, "X": X}
+    ref = _oracle(case)
+    y = _run(case)
+    # |sum| < 2^8 here, so bf16 holds it only to 8 bits: compare to the bf16-rounded exact value.
+    assert np.array_equal(y, torch.from_numpy(ref).to(torch.bfloat16).float().numpy())
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_baseline_config1(M):
+    """cfg1: K=4096, N=28672 (fused gate+up), codes uniform, scales 2^-8..2^-4, x ~ N(0,1)."""
+    case = workloads.w4_case(N=28672, K=4096, M=8, seed=100)
+    err = matvec.rel_to_max_error(_run(case, M), _oracle(case, M))
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("N,K,M", [
+    (1, 32, 1), (8, 32, 3), (17, 96, 2), (100, 160, 7), (4096, 3584, 8), (3584, 3072, 8),
+    (3584, 18944, 1), (37888, 3584, 8), (33, 4096, 16), (1000, 4128, 5),
+])
+def test_shapes(N, K, M):
+    case = workloads.w4_case(N=N, K=K, M=M, seed=N + K + M)
+    err = matvec.rel_to_max_error(_run(case), _oracle(case))
+    assert err < TOL, err
+
+
+def test_wide_scale_range():
+    """Scale bytes far from 127 on both sides; each band is checked against its own maximum."""
+    case = workloads.w4_case(N=96, K=256, M=2, seed=9)
+    St = case["St"].clone()
+    St[:32] = 60                       # 2^-67
+    St[32:64] = 150                    # 2^23
+    St[64:] = torch.randint(60, 151, (32, 8), generator=torch.Generator().manual_seed(1),
+                            dtype=torch.uint8)
+    case["St"] = St
+    y = _run(case)
+    ref = _oracle(case)
+    for a, b in ((0, 32), (32, 64)):
+        assert matvec.rel_to_max_error(y[:, a:b], ref[:, a:b]) < TOL
+    assert matvec.rel_to_max_error(y[:, 64:], ref[:, 64:]) < TOL
+
+
+def test_scale_byte_zero_is_negligible():
+    """Byte 0 is 2^-127: rows scaled by it are ~1e-37 or flushed to 0, never garbage."""
+    case = workloads.w4_case(N=32, K=128, M=1, seed=2)
+    St = case["St"].clone()
+    St[:16] = 0
+    case["St"] = St
+    y = _run(case)
+    assert np.all(np.abs(y[:, :16]) < 1e-30)
+    assert matvec.rel_to_max_error(y[:, 16:], _oracle(case)[:, 16:]) < TOL
+
+
+def test_scale_byte_255_is_nan():
+    case = workloads.w4_case(N=32, K=64, M=1, seed=3)
+    St = case["St"].clone()
+    St[5, 1] = 255
+    case["St"] = St
+    y = _run(case)
+    assert np.isnan(y[0, 5]) and np.isfinite(np.delete(y[0], 5)).all()
+
+
+def test_deterministic_and_no_out_of_bounds_writes():
+    case = workloads.w4_case(N=1000, K=1024, M=3, seed=21)
+    X, W, St = case["X"].to(DEV), case["W"].to(DEV), case["St"].to(DEV)
+    big = torch.full((3 * 1000 + 64,), 7.0, dtype=torch.bfloat16, device=DEV)
+    out = big[:3000].view(3, 1000)
+    ops.h4mv(X, W, St, out=out)
+    a = out.clone()
+    ops.h4mv(X, W, St, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(a, out)
+    assert torch.all(big[3000:] == 7.0)
+
+
+def test_reference_style_void_entry_point():
+    """The exact reference binding (h4mv/fp8kv_hipw4.py:21-23,81-83) drives our library."""
+    lib = ctypes.CDLL(_lib.lib_path())
+    lib.h4mv_launch.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
+    lib.h4mv_launch.restype = None
+    case = workloads.w4_case(N=512, K=1024, M=4, seed=5)
+    W, St, X = case["W"].to(DEV), case["St"].to(DEV), case["X"].to(DEV)
+    Y = torch.empty(4, 512, dtype=torch.bfloat16, device=DEV)
+    lib.h4mv_launch(W.data_ptr(), St.data_ptr(), X.data_ptr(), Y.data_ptr(), 512, 1024, 4,
+                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert matvec.rel_to_max_error(Y.float().cpu().numpy(), _oracle(case)) < TOL
+
+
+def test_rejects_bad_m():
+    case = workloads.w4_case(N=64, K=64, M=17, seed=1)
+    with pytest.raises(_lib.Fp8kvError):
+        ops.h4mv(case["X"].to(DEV), case["W"].to(DEV), case["St"].to(DEV))
+
+
+REF_LIB = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                       "oracle", "_ref", "libh4mv_ref.so")
+
+
+@pytest.mark.skipif(not os.path.exists(REF_LIB), reason="oracle/_ref not built")
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_oracle_and_kernel_against_reference_kernel(M):
+    """The reference's own h4mv.cu (built for gfx950 into oracle/_ref) pins the oracle, and ours
+    agrees with it.  The reference rounds half-up to bf16, so agreement is within tolerance."""
+    ref_lib = ctypes.CDLL(REF_LIB)
+    ref_lib.h4mv_launch.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
+    ref_lib.h4mv_launch.restype = None
+    N, K = 4096, 3584
+    case = workloads.w4_case(N=N, K=K, M=M, seed=77)
+    W, St, X = case["W"].to(DEV), case["St"].to(DEV), case["X"].to(DEV)
+    Y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    ref_lib.h4mv_launch(W.data_ptr(), St.data_ptr(), X.data_ptr(), Y.data_ptr(), N, K, M,
+                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    y_ref_kernel = Y.float().cpu().numpy()
+    oracle_y = _oracle(case)
+    assert matvec.rel_to_max_error(y_ref_kernel, oracle_y) < TOL
+    assert matvec.rel_to_max_error(_run(case), y_ref_kernel) < TOL
