@@ -78,6 +78,26 @@ __device__ __forceinline__ f32x4_t mfma16x16x32_bf16(bf16x8_t a, bf16x8_t b, f32
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// LDS pointer type for the direct global->LDS loads (global_load_lds_dword{,x4}).
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Copy 16 bytes per lane from global memory straight into LDS: lane i lands at lds_base + 16 i.
+// lds_base must be wave-uniform.  Completion is tracked by vmcnt only: the compiler does NOT
+// order later LDS reads after it, so callers wait with wait_vmcnt<> before reading.
+__device__ __forceinline__ void dma16_to_lds(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4_to_lds(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // Non-temporal 16-byte global load: weight and KV streams are read exactly once per launch.
 __device__ __forceinline__ u32x4_t load_nt_16(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));

@@ -1,0 +1,21 @@
+/* Host-only diagnostics exported by libfp8kv_amd.so for the test suite (not part of the drop-in
+ * ABI in include/fp8kv_amd.h).  They run no GPU code. */
+#ifndef FP8KV_DIAG_H
+#define FP8KV_DIAG_H
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Enumerate every global and LDS address the MXFP4 matvec's streaming kernel would touch for
+ * (N, K, M) and check it against the operand sizes and the LDS allocation.
+ * 0 = all in bounds, 1 = the shape uses the register-path kernel instead, >= 2 = violation id. */
+int fp8kv_h4mv_audit(int N, int K, int M);
+
+/* Tuning hook for sweeps: waves per launch the matvec's K split aims for and a forced LDS ring
+ * depth (0 and 0 = the built-in defaults).  Affects later launches and audits. */
+void fp8kv_h4mv_tune(int target_waves, int depth);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

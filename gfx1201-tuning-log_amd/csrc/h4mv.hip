@@ -5,8 +5,8 @@
 //
 // gfx950 design (not a translation of the wave-per-row dot2 kernel):
 //   * A workgroup owns a 16-row tile of W and runs one v_mfma_f32_16x16x32_bf16 chain per wave;
-//     the four waves split K and meet in LDS once at the end (split-K inside the workgroup, so
-//     N/16 workgroups of equal size fill the 256 CUs evenly).
+//     its WAVES waves split K and meet in LDS once at the end (split-K inside the workgroup, so
+//     N/16 workgroups of equal size spread evenly over the 256 CUs).
 //   * Lane (r, q) = (lane % 16, lane / 16) streams whole 16-byte scale groups of row r: one
 //     global_load_dwordx4 = 32 codes = exactly one e8m0 group, so each load needs one scale.
 //     The 16 bytes become four MFMA A fragments via v_cvt_scalef32_pk_bf16_fp4, which applies
@@ -14,28 +14,77 @@
 //   * K is a reduction index, so the kernel may visit it in any order as long as the A (weights)
 //     and B (activations) fragments agree: quad q of the wave handles group g = g0 + 4u + q and
 //     fragment j covers k = 32 g + 8 j + (0..7) on both sides.
-//   * X is the B operand: lane (m, q) loads X[m, 32 g + 8 j .. +8] for m < M and holds zeros for the
-//     padded columns m >= M, so one kernel serves 1 <= M <= 16.  X is small and stays in L2.
+//   * All weight loads of a chunk of U groups-per-quad are issued before any of them is consumed,
+//     and the next chunk is requested before the current one is converted (two register
+//     buffers), so each wave keeps U * 1 KB of the weight stream in flight.
+//   * X is the B operand: lane (m, q) supplies X[m, 32 g + 8 j .. +8] for m < M and zeros for the
+//     padded columns m >= M, so one kernel serves 1 <= M <= 16.  When M*K*2 bytes fit, X is copied
+//     to LDS once per workgroup (XLDS) and the fragments come from ds_read_b128; otherwise they are
+//     read from global memory, where X stays L2-resident.
 //   * Output tile: lane (m, q) register i holds row n0 + 4 q + i of column m, so each lane of the
-//     first wave writes 4 consecutive bf16 of Out[m, :].
+//     first wave writes 4 consecutive outputs of Out[m, :].
 #include "fp8kv_common.h"
 #include "fp8kv_status.h"
+#include "fp8kv_diag.h"
+#include <algorithm>
 
 namespace fp8kv {
 
 thread_local int g_last_status = FP8KV_OK;
 
-namespace {
+namespace h4mv_detail {
 
 constexpr int kRowsPerWG = 16;
-constexpr int kWavesPerWG = 4;
+constexpr int kXLdsMaxBytes = 64 * 1024;
 
 template <int U>
-__global__ void __launch_bounds__(256)
-h4mv_mfma_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
-                 const __bf16* __restrict__ X, __bf16* __restrict__ Out,
-                 int N, int K, int M, int groups_per_wave)
+struct Chunk {
+    u32x4_t w[U];
+    uint32_t s[U];
+};
+
+template <int U>
+__device__ __forceinline__ void load_chunk(Chunk<U>& c, const uint8_t* wrow, const uint8_t* srow,
+                                           int g0, int q, int g_end, bool row_ok)
 {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int g = g0 + 4 * u + q;
+        const bool ok = row_ok && g < g_end;
+        const u32x4_t zero = {0u, 0u, 0u, 0u};
+        c.w[u] = ok ? load_nt_16(wrow + (size_t)g * 16) : zero;
+        c.s[u] = ok ? (uint32_t)srow[g] : 127u;
+    }
+}
+
+template <int U, bool XLDS>
+__device__ __forceinline__ f32x4_t consume_chunk(const Chunk<U>& c, f32x4_t acc, const __bf16* xsrc,
+                                                 int g0, int q, int g_end, bool col_ok)
+{
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int g = g0 + 4 * u + q;
+        const bool ok = col_ok && g < g_end;
+        const float sc = e8m0_to_f32(c.s[u]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4_t zero = {0u, 0u, 0u, 0u};
+            const u32x4_t xv = ok ? load_16(xsrc + (size_t)g * 32 + 8 * j) : zero;
+            acc = mfma16x16x32_bf16(fp4x8_to_bf16x8(c.w[u][j], sc), as_bf16x8(xv), acc);
+        }
+    }
+    return acc;
+}
+
+template <int WAVES, int U, bool XLDS, typename OutT>
+__global__ void __launch_bounds__(WAVES * 64)
+h4mv_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
+            const __bf16* __restrict__ X, OutT* __restrict__ Out,
+            int N, int K, int M, int groups_per_wave)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ f32x4_t red[WAVES > 1 ? WAVES - 1 : 1][64];
+
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int r = lane & 15;        // weight row within the tile / activation column m
@@ -51,78 +100,564 @@ h4mv_mfma_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
 
     const uint8_t* wrow = W + (size_t)(row_ok ? row : 0) * (size_t)(K >> 1);
     const uint8_t* srow = St + (size_t)(row_ok ? row : 0) * (size_t)G;
-    const __bf16* xrow = X + (size_t)(col_ok ? r : 0) * (size_t)K;
 
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    // Weight stream first: the first chunk is in flight while X is staged.
+    Chunk<U> ca, cb;
+    load_chunk<U>(ca, wrow, srow, g_begin, q, g_end, row_ok);
 
-    for (int g0 = g_begin; g0 < g_end; g0 += 4 * U) {
-        u32x4_t wv[U];
-        uint32_t sb[U];
-        u32x4_t xv[U][4];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int g = g0 + 4 * u + q;
-            const bool g_ok = g < g_end;
-            const u32x4_t zero = {0u, 0u, 0u, 0u};
-            wv[u] = (g_ok && row_ok) ? load_nt_16(wrow + (size_t)g * 16) : zero;
-            sb[u] = (g_ok && row_ok) ? (uint32_t)srow[g] : 127u;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                xv[u][j] = (g_ok && col_ok) ? load_16(xrow + (size_t)g * 32 + 8 * j) : zero;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const float sc = e8m0_to_f32(sb[u]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const bf16x8_t a = fp4x8_to_bf16x8(wv[u][j], sc);
-                acc = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), acc);
-            }
-        }
+    const __bf16* xsrc;
+    if constexpr (XLDS) {
+        __bf16* xl = reinterpret_cast<__bf16*>(smem);
+        const int n16 = (M * K) >> 3;                   // 16-byte pieces of X
+        for (int i = threadIdx.x; i < n16; i += WAVES * 64)
+            *reinterpret_cast<u32x4_t*>(xl + 8 * i) = load_16(X + 8 * i);
+        __syncthreads();
+        xsrc = xl + (size_t)(col_ok ? r : 0) * (size_t)K;
+    } else {
+        xsrc = X + (size_t)(col_ok ? r : 0) * (size_t)K;
     }
 
-    __shared__ f32x4_t red[kWavesPerWG - 1][64];
-    if (wave > 0) red[wave - 1][lane] = acc;
-    __syncthreads();
-    if (wave != 0) return;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    int g0 = g_begin;
+    while (g0 < g_end) {
+        const int g1 = g0 + 4 * U;
+        if (g1 < g_end) load_chunk<U>(cb, wrow, srow, g1, q, g_end, row_ok);
+        acc = consume_chunk<U, XLDS>(ca, acc, xsrc, g0, q, g_end, col_ok);
+        if (g1 >= g_end) break;
+        const int g2 = g1 + 4 * U;
+        if (g2 < g_end) load_chunk<U>(ca, wrow, srow, g2, q, g_end, row_ok);
+        acc = consume_chunk<U, XLDS>(cb, acc, xsrc, g1, q, g_end, col_ok);
+        g0 = g2;
+    }
+
+    if constexpr (WAVES > 1) {
+        if (wave > 0) red[wave - 1][lane] = acc;
+        __syncthreads();
+        if (wave != 0) return;
 #pragma unroll
-    for (int w = 0; w < kWavesPerWG - 1; ++w) acc += red[w][lane];
+        for (int w = 0; w < WAVES - 1; ++w) acc += red[w][lane];
+    }
 
     const int m = r;
     if (m >= M) return;
     const int n = n0 + 4 * q;
-    __bf16* orow = Out + (size_t)m * (size_t)N;
-    if (n + 3 < N && ((N & 3) == 0) && aligned(Out, 8)) {
-        u32x2_t v = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
-        *reinterpret_cast<u32x2_t*>(orow + n) = v;
+    OutT* orow = Out + (size_t)m * (size_t)N;
+    const bool vec = n + 3 < N && ((N & 3) == 0) && aligned(Out, 4 * sizeof(OutT));
+    if constexpr (sizeof(OutT) == 2) {
+        if (vec) {
+            u32x2_t v = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+            *reinterpret_cast<u32x2_t*>(orow + n) = v;
+            return;
+        }
     } else {
+        if (vec) {
+            *reinterpret_cast<f32x4_t*>(orow + n) = acc;
+            return;
+        }
+    }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (n + i < N) orow[n + i] = (__bf16)acc[i];
+    for (int i = 0; i < 4; ++i)
+        if (n + i < N) orow[n + i] = (OutT)acc[i];
+}
+
+// ---------------------------------------------------------------------------------------------
+// Streaming kernel for K % 512 == 0 (every shape of the target model).
+//
+// The MFMA A layout pins lane (r, q) to weight row r, so direct per-lane loads would make adjacent
+// lanes read rows K/2 bytes apart (measured: 4.9 TB/s read-only ceiling for that pattern, versus
+// 6.1 TB/s for coalesced reads).  Instead each wave copies its share of the 16-row tile into LDS
+// with coalesced global_load_lds_dwordx4 and reads MFMA fragments back with ds_read_b128.
+//   * step = 16 scale groups (256 B) of each of the 16 rows = 4 KB of codes;
+//   * a workgroup owns one tile and has NW waves; wave w owns the contiguous steps
+//     [w * per, w * per + per) and streams their codes through a DEPTH-slot LDS ring: a slot is
+//     refilled as soon as its fragments are in registers, before they are converted and multiplied;
+//   * the wave's scale bytes (16 rows x per x 16 B) are copied once at the start, row by row, so
+//     consecutive lanes read consecutive bytes (per-step 16-byte scale pieces from 16 rows cost a
+//     measured 1 us per launch at cfg1);
+//   * activations: copied once per wave for all its steps when they fit (XSTAGE), else each slot
+//     carries MMAX KB of activation rows next to its codes;
+//   * the waves of the workgroup meet once in LDS to add their partial tiles;
+//   * LDS code layout: row r at 256 r, 16-byte piece p at slot p ^ (r & 7), so the 16 lanes that
+//     read one piece index of 16 rows hit distinct bank groups;
+//   * copies complete out of the compiler's sight, so every wait is an explicit s_waitcnt vmcnt
+//     with the exact number of copy instructions still allowed in flight;
+//   * columns m >= M of the B operand only feed output columns that are never stored, so lanes
+//     r >= M neither read activations nor zero their registers.
+// ---------------------------------------------------------------------------------------------
+constexpr int kStepGroups = 16;
+constexpr int kStepCodeBytes = 16 * 256;
+constexpr int kXStageMaxBytes = 0;           // activation bytes per wave staged once (XSTAGE);
+                                             // measured: per-step copies from L2 cost less than
+                                             // the LDS (and so the waves per CU) staging takes
+constexpr int kDmaAux = 2;                    // streaming cache policy for the code copies
+
+// LDS layout of one wave (bytes), shared by kernel, planner and audit.
+struct WaveLds {
+    int slot;        // bytes per ring slot
+    int ring;        // DEPTH * slot
+    int scales;      // 16 rows * per * 16
+    int xs;          // staged activations (XSTAGE) or 0
+    int total;
+};
+
+__host__ __device__ inline WaveLds wave_lds(int mmax, bool xstage, int depth, int per)
+{
+    WaveLds w;
+    w.slot = kStepCodeBytes + (xstage ? 0 : mmax * 1024);
+    w.ring = depth * w.slot;
+    w.scales = 16 * per * 16;
+    w.xs = xstage ? mmax * per * 1024 : 0;
+    w.total = w.ring + w.scales + w.xs;
+    return w;
+}
+
+// ---- index math shared by the kernel and the host-side address audit --------------------------
+// Code copy instruction i (0..3) of a step: lane -> row 4 i + lane / 16 of the tile (clamped to
+// N - 1) and the 16-byte piece (lane % 16) ^ (row & 7); byte offset from the tile's first code byte.
+__host__ __device__ inline uint32_t stream_w_lane_off(int n0, int N, int K, int lane, int i)
+{
+    const int rr = 4 * i + (lane >> 4);
+    const int rowc = (n0 + rr < N ? n0 + rr : N - 1) - n0;
+    return (uint32_t)rowc * (uint32_t)(K >> 1) + 16u * (uint32_t)((lane & 15) ^ (rr & 7));
+}
+// Scale copy: segment t (0 .. 16 per - 1) = row t / per, step t % per of the wave's slice; byte
+// offset from St.  Segment t lands at 16 t in the wave's scale area.
+__host__ __device__ inline size_t stream_s_seg_off(int n0, int N, int K, int per, int step0, int t)
+{
+    const int row = t / per, st = t % per;
+    const int rowc = n0 + row < N ? n0 + row : N - 1;
+    return (size_t)rowc * (size_t)(K >> 5) + (size_t)(step0 + st) * kStepGroups;
+}
+// Activation copy of row m (clamped to M - 1) for step gs (first group) and lane: offset from X.
+__host__ __device__ inline size_t stream_x_off(int K, int M, int m, int gs, int lane)
+{
+    const int mm = m < M ? m : M - 1;
+    return (size_t)mm * (size_t)K * 2 + (size_t)gs * 64 + 16u * (uint32_t)lane;
+}
+// LDS read offsets: codes of group q + 4u of row r within a slot; activation fragment (u, j) of
+// row r within one 1 KB step block.
+__host__ __device__ inline int stream_w_read_off(int r, int q, int u) { return 256 * r + 16 * ((q + 4 * u) ^ (r & 7)); }
+__host__ __device__ inline int stream_x_frag_off(int q, int u, int j) { return q * 64 + u * 256 + j * 16; }
+
+template <int MMAX, bool XSTAGE>
+constexpr int copies_per_step() { return 4 + (XSTAGE ? 0 : MMAX); }
+
+// Wait until the oldest outstanding step has landed, leaving `ahead` younger steps in flight.
+template <int MMAX, bool XSTAGE, int A>
+__device__ __forceinline__ void wait_ahead_ct(int ahead)
+{
+    if constexpr (A == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (ahead >= A) wait_vmcnt<A * copies_per_step<MMAX, XSTAGE>()>();
+        else wait_ahead_ct<MMAX, XSTAGE, A - 1>(ahead);
     }
 }
 
-}  // namespace
+template <int MMAX, bool XSTAGE>
+__device__ __forceinline__ void issue_step(unsigned char* slot, const uint8_t* wtile,
+                                           const unsigned char* xbytes, const uint32_t (&woff)[4],
+                                           int gs, int K, int M, int lane)
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_global_load_lds((const void*)(wtile + (size_t)gs * 16 + woff[i]),
+                                         (lds_void_t*)(slot + i * 1024), 16, 0, kDmaAux);
+    if constexpr (!XSTAGE) {
+#pragma unroll
+        for (int m = 0; m < MMAX; ++m)
+            dma16_to_lds(xbytes + stream_x_off(K, M, m, gs, lane), slot + kStepCodeBytes + m * 1024);
+    }
+}
+
+template <int MMAX, bool XSTAGE, int DEPTH, typename OutT>
+__global__ void __launch_bounds__(1024)
+h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
+                   const __bf16* __restrict__ X, OutT* __restrict__ Out,
+                   int N, int K, int M, int per)
+{
+    static_assert((DEPTH - 1) * copies_per_step<MMAX, XSTAGE>() < 64, "vmcnt holds at most 63");
+    extern __shared__ __align__(16) unsigned char smem[];
+    const WaveLds L = wave_lds(MMAX, XSTAGE, DEPTH, per);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    const int steps_total = K >> 9;
+    const int n0 = blockIdx.x * kRowsPerWG;
+    const bool col_ok = r < M;
+
+    unsigned char* base = smem + wave * L.total;
+    unsigned char* ring = base;
+    unsigned char* sarea = base + L.ring;
+    unsigned char* xarea = sarea + L.scales;
+    const int step0 = wave * per;
+    const int nsteps = max(0, min(per, steps_total - step0));
+
+    const uint8_t* wtile = W + (size_t)n0 * (size_t)(K >> 1);
+    const unsigned char* xbytes = reinterpret_cast<const unsigned char*>(X);
+    uint32_t woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) woff[i] = stream_w_lane_off(n0, N, K, lane, i);
+
+    // ---- one-time copies: the wave's scale slice (and activation slice) ------------------------
+    if (nsteps > 0) {
+        for (int t0 = 0; t0 < 16 * per; t0 += 64) {
+            const int t = t0 + lane;
+            if (t < 16 * per && (t % per) < nsteps)
+                dma16_to_lds(St + stream_s_seg_off(n0, N, K, per, step0, t), sarea + t0 * 16);
+        }
+        if constexpr (XSTAGE) {
+            for (int s = 0; s < nsteps; ++s)
+                for (int m = 0; m < M; ++m)
+                    dma16_to_lds(xbytes + stream_x_off(K, M, m, (step0 + s) * kStepGroups, lane),
+                                 xarea + (m * per + s) * 1024);
+        }
+    }
+    // ---- fill the ring ------------------------------------------------------------------------
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s)
+        if (s < nsteps)
+            issue_step<MMAX, XSTAGE>(ring + s * L.slot, wtile, xbytes, woff, (step0 + s) * kStepGroups,
+                                     K, M, lane);
+
+    int rdoff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rdoff[u] = stream_w_read_off(r, q, u);
+
+    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc1 = {0.f, 0.f, 0.f, 0.f};
+    u32x4_t xv[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "=v"(xv[u][j]));   // columns m >= M: any value
+
+    for (int s = 0; s < nsteps; ++s) {
+        const int slot = s % DEPTH;
+        unsigned char* sl = ring + slot * L.slot;
+        wait_ahead_ct<MMAX, XSTAGE, DEPTH - 1>(min(nsteps - 1 - s, DEPTH - 1));
+        const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(sarea + (r * per + s) * 16);
+        u32x4_t wv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wv[u] = *reinterpret_cast<const u32x4_t*>(sl + rdoff[u]);
+        if (col_ok) {
+            const unsigned char* xrow = XSTAGE ? xarea + (r * per + s) * 1024
+                                               : sl + kStepCodeBytes + r * 1024;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    xv[u][j] = *reinterpret_cast<const u32x4_t*>(xrow + stream_x_frag_off(q, u, j));
+        }
+        // All fragments of this slot are in registers: refill it before the math.
+        __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0)
+        if (s + DEPTH < nsteps)
+            issue_step<MMAX, XSTAGE>(sl, wtile, xbytes, woff, (step0 + s + DEPTH) * kStepGroups,
+                                     K, M, lane);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float sc = e8m0_to_f32((sv[u] >> (8 * q)) & 0xFFu);   // group q + 4u of row r
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bf16x8_t a = fp4x8_to_bf16x8(wv[u][j], sc);
+                if (u & 1) acc1 = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), acc1);
+                else       acc0 = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), acc0);
+            }
+        }
+    }
+    f32x4_t acc = acc0 + acc1;
+
+    // ---- reduce over the waves of the workgroup ------------------------------------------------
+    if (nwaves > 1) {
+        __syncthreads();                                   // every wave is done with its LDS
+        if (wave > 0) reinterpret_cast<f32x4_t*>(base)[lane] = acc;
+        __syncthreads();
+        if (wave != 0) return;
+        for (int w = 1; w < nwaves; ++w)
+            acc += reinterpret_cast<const f32x4_t*>(smem + w * L.total)[lane];
+    }
+
+    const int m = r;
+    if (m >= M) return;
+    const int n = n0 + 4 * q;
+    OutT* orow = Out + (size_t)m * (size_t)N;
+    const bool vec = n + 3 < N && ((N & 3) == 0) && aligned(Out, 4 * sizeof(OutT));
+    if constexpr (sizeof(OutT) == 2) {
+        if (vec) {
+            u32x2_t v = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+            *reinterpret_cast<u32x2_t*>(orow + n) = v;
+            return;
+        }
+    } else {
+        if (vec) {
+            *reinterpret_cast<f32x4_t*>(orow + n) = acc;
+            return;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (n + i < N) orow[n + i] = (OutT)acc[i];
+}
+
+// Waves per tile: enough tiles x waves to cover the GPU, at most 16 per workgroup and at most one
+// per step.
+inline int stream_waves(int N, int K, int target_waves)
+{
+    const int tiles = (N + kRowsPerWG - 1) / kRowsPerWG;
+    const int steps = (K >> 5) / kStepGroups;
+    int nw = (target_waves + tiles - 1) / tiles;
+    nw = max(1, min(nw, min(16, steps)));
+    return nw;
+}
+
+// Launch geometry shared by the production entry points and the tuning harness.
+struct Plan {
+    int waves;
+    int groups_per_wave;
+    bool xlds;
+    size_t lds_bytes;
+};
+
+inline Plan make_plan(int K, int M, int waves)
+{
+    const int G = K >> 5;
+    Plan p;
+    p.waves = waves;
+    int per = (G + waves - 1) / waves;
+    p.groups_per_wave = (per + 3) & ~3;
+    p.xlds = (size_t)M * (size_t)K * 2 <= (size_t)kXLdsMaxBytes;
+    p.lds_bytes = p.xlds ? (size_t)M * (size_t)K * 2 : 0;
+    return p;
+}
+
+template <int WAVES, int U, typename OutT>
+void launch_with(const Plan& p, const void* W, const void* St, const void* Xb, void* Out,
+                 int N, int K, int M, hipStream_t s)
+{
+    const dim3 grid((unsigned)((N + kRowsPerWG - 1) / kRowsPerWG));
+    const dim3 block(64 * WAVES);
+    if (p.xlds)
+        hipLaunchKernelGGL((h4mv_kernel<WAVES, U, true, OutT>), grid, block, p.lds_bytes, s,
+                           static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St),
+                           static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M,
+                           p.groups_per_wave);
+    else
+        hipLaunchKernelGGL((h4mv_kernel<WAVES, U, false, OutT>), grid, block, 0, s,
+                           static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St),
+                           static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M,
+                           p.groups_per_wave);
+}
+
+constexpr size_t kLdsPerCU = 160 * 1024;
+
+// Tunables (host state; fp8kv_h4mv_tune changes them for sweeps).  0 = the measured defaults:
+// one wave per tile when there are >= 1024 tiles, otherwise a K split aiming at 4096 waves, and
+// a two-slot ring (deeper rings measured slower at every cfg1/cfg4 shape).
+int g_target_waves = 0;
+int g_depth_override = 0;
+
+inline int stream_mmax(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+
+struct StreamPlan {
+    int mmax, depth, nw, per;
+    bool xstage;
+    size_t lds;
+};
+
+// Plan for the streaming kernel, or false when (K, M) needs the register-path kernel.
+inline bool stream_plan(int N, int K, int M, StreamPlan& p)
+{
+    if ((K & 511) != 0 || M > 8) return false;
+    p.mmax = stream_mmax(M);
+    const int steps_total = K >> 9;
+    const int tiles = (N + kRowsPerWG - 1) / kRowsPerWG;
+    const int target = g_target_waves > 0 ? g_target_waves : (tiles >= 1024 ? tiles : 4096);
+    int nreq = stream_waves(N, K, target);
+    for (;;) {
+        p.per = (steps_total + nreq - 1) / nreq;
+        p.nw = (steps_total + p.per - 1) / p.per;
+        p.xstage = p.mmax * p.per * 1024 <= kXStageMaxBytes;
+        const WaveLds w2 = wave_lds(p.mmax, p.xstage, 2, p.per);
+        if ((size_t)p.nw * w2.total <= kLdsPerCU || nreq == 1) break;
+        nreq = std::max(1, nreq - 1);
+    }
+    const int copies = 4 + (p.xstage ? 0 : p.mmax);
+    int depth = 2;
+    if (g_depth_override) depth = std::max(2, std::min(4, g_depth_override));
+    while (depth > 2 && ((depth - 1) * copies >= 64 ||
+                         (size_t)p.nw * wave_lds(p.mmax, p.xstage, depth, p.per).total > kLdsPerCU))
+        --depth;
+    const WaveLds w = wave_lds(p.mmax, p.xstage, depth, p.per);
+    p.depth = depth;
+    p.lds = (size_t)p.nw * w.total;
+    return p.lds <= kLdsPerCU;
+}
+
+template <int MMAX, bool XSTAGE, typename OutT>
+void launch_stream_x(const StreamPlan& p, const void* W, const void* St, const void* Xb, void* Out,
+                     int N, int K, int M, hipStream_t s)
+{
+    const dim3 grid((unsigned)((N + kRowsPerWG - 1) / kRowsPerWG));
+    const dim3 block(64 * p.nw);
+#define FP8KV_D(D) \
+    case D: hipLaunchKernelGGL((h4mv_stream_kernel<MMAX, XSTAGE, D, OutT>), grid, block, p.lds, s, \
+                               static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
+                               static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M, p.per); \
+            break;
+    switch (p.depth) {
+        FP8KV_D(2) FP8KV_D(3) FP8KV_D(4)
+        default: break;
+    }
+#undef FP8KV_D
+}
+
+template <typename OutT>
+void launch_stream_m(const StreamPlan& p, const void* W, const void* St, const void* Xb, void* Out,
+                     int N, int K, int M, hipStream_t s)
+{
+    if (p.xstage) {
+        switch (p.mmax) {
+            case 1: launch_stream_x<1, true, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+            case 2: launch_stream_x<2, true, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+            case 4: launch_stream_x<4, true, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+            default: launch_stream_x<8, true, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+        }
+    } else {
+        switch (p.mmax) {
+            case 1: launch_stream_x<1, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+            case 2: launch_stream_x<2, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+            case 4: launch_stream_x<4, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+            default: launch_stream_x<8, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+        }
+    }
+}
+
+template <typename OutT>
+int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N, int K, int M,
+                void* stream)
+{
+    if (!W || !St || !Xb || !Out) return FP8KV_ERR_ARG;
+    if (N < 1 || K < 32 || M < 1) return FP8KV_ERR_ARG;
+    if (M > 16 || (K & 31) != 0) return FP8KV_ERR_SHAPE;
+    if (!aligned(W, 16) || !aligned(Xb, 16) || !aligned(Out, sizeof(OutT))) return FP8KV_ERR_ALIGN;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    StreamPlan p;
+    if (aligned(St, 4) && stream_plan(N, K, M, p)) {
+        launch_stream_m<OutT>(p, W, St, Xb, Out, N, K, M, s);
+    } else {
+        const Plan rp = make_plan(K, M, 4);
+        launch_with<4, 8, OutT>(rp, W, St, Xb, Out, N, K, M, s);
+    }
+    return finish_launch();
+}
+
+}  // namespace h4mv_detail
 }  // namespace fp8kv
+
+// ---------------------------------------------------------------------------------------------
+// Host-side address audit of the streaming kernel: enumerates, for the launch the entry points
+// would make for (N, K, M), every global byte each copy instruction reads and every LDS byte each
+// copy writes or each fragment read touches, and checks them against the operand sizes and the
+// dynamic LDS allocation.  Returns 0 when every access is in bounds, 1 when the shape does not
+// use the streaming kernel, and 2 + the index of the first violated check otherwise.
+// ---------------------------------------------------------------------------------------------
+namespace fp8kv { namespace h4mv_detail {
+
+int audit_stream(int N, int K, int M, const StreamPlan& p)
+{
+    const int steps_total = K >> 9;
+    const int per = p.per, nw = p.nw, depth = p.depth, MMAX = p.mmax;
+    if (nw > 16 || nw * per < steps_total || (nw - 1) * per >= steps_total) return 2;
+    if (p.lds > kLdsPerCU || depth < 2 || depth > 4) return 3;
+    if ((depth - 1) * (4 + (p.xstage ? 0 : MMAX)) >= 64) return 3;
+    const WaveLds L = wave_lds(MMAX, p.xstage, depth, per);
+    if ((size_t)nw * L.total != p.lds) return 3;
+    const size_t wbytes = (size_t)N * (size_t)(K >> 1), sbytes = (size_t)N * (size_t)(K >> 5);
+    const size_t xbytes = (size_t)M * (size_t)K * 2;
+    for (int tile = 0; tile * kRowsPerWG < N; ++tile) {
+        const int n0 = tile * kRowsPerWG;
+        for (int w = 0; w < nw; ++w) {
+            const size_t wb = (size_t)w * L.total;
+            const int step0 = w * per;
+            const int nsteps = std::max(0, std::min(per, steps_total - step0));
+            if (nsteps > 0) {
+                for (int t = 0; t < 16 * per; ++t) {          // one-time scale copies
+                    if ((t % per) >= nsteps) continue;
+                    if (stream_s_seg_off(n0, N, K, per, step0, t) + 16 > sbytes) return 6;
+                    if (wb + L.ring + 16 * (size_t)t + 16 > wb + L.ring + L.scales) return 7;
+                }
+                if (p.xstage)
+                    for (int s = 0; s < nsteps; ++s)
+                        for (int m = 0; m < M; ++m)
+                            for (int lane = 0; lane < 64; ++lane) {
+                                if (stream_x_off(K, M, m, (step0 + s) * kStepGroups, lane) + 16 > xbytes) return 8;
+                                if (L.ring + L.scales + (size_t)(m * per + s) * 1024 + 16 * lane + 16 > (size_t)L.total) return 9;
+                            }
+            }
+            for (int s = 0; s < nsteps; ++s) {
+                const int gs = (step0 + s) * kStepGroups;
+                const size_t slot = wb + (size_t)(s % depth) * L.slot;
+                for (int lane = 0; lane < 64; ++lane) {
+                    for (int i = 0; i < 4; ++i) {
+                        const size_t g = (size_t)n0 * (K >> 1) + (size_t)gs * 16 + stream_w_lane_off(n0, N, K, lane, i);
+                        if (g + 16 > wbytes) return 4;
+                        if (slot + i * 1024 + 16 * lane + 16 > slot + kStepCodeBytes) return 5;
+                    }
+                    if (!p.xstage)
+                        for (int m = 0; m < MMAX; ++m) {
+                            if (stream_x_off(K, M, m, gs, lane) + 16 > xbytes) return 8;
+                            if (kStepCodeBytes + m * 1024 + 16 * lane + 16 > L.slot) return 9;
+                        }
+                    const int r = lane & 15, q = lane >> 4;
+                    if (L.ring + (size_t)(r * per + s) * 16 + 16 > (size_t)(L.ring + L.scales)) return 10;
+                    for (int u = 0; u < 4; ++u) {
+                        if (stream_w_read_off(r, q, u) + 16 > kStepCodeBytes) return 11;
+                        for (int j = 0; j < 4; ++j) {
+                            if (r >= M) continue;
+                            const size_t xo = p.xstage ? L.ring + L.scales + (size_t)(r * per + s) * 1024
+                                                       : (size_t)(s % depth) * L.slot + kStepCodeBytes + r * 1024;
+                            const size_t end = p.xstage ? (size_t)L.total : (size_t)(s % depth) * L.slot + L.slot;
+                            if (xo + stream_x_frag_off(q, u, j) + 16 > end) return 12;
+                        }
+                    }
+                }
+            }
+            if (wb + 64 * 16 > p.lds) return 13;                // partial-tile exchange
+        }
+    }
+    return 0;
+}
+
+}}  // namespace fp8kv::h4mv_detail
+
+extern "C" int fp8kv_h4mv_audit(int N, int K, int M)
+{
+    using namespace fp8kv::h4mv_detail;
+    if (N < 1 || K < 32 || M < 1 || M > 16 || (K & 31)) return 2;
+    StreamPlan p;
+    if (!stream_plan(N, K, M, p)) return 1;
+    return audit_stream(N, K, M, p);
+}
+
+extern "C" void fp8kv_h4mv_tune(int target_waves, int depth)
+{
+    fp8kv::h4mv_detail::g_target_waves = target_waves > 0 ? target_waves : 0;
+    fp8kv::h4mv_detail::g_depth_override = depth;
+}
 
 extern "C" int h4mv_launch_status(const void* W, const void* St, const void* Xb, void* Out,
                                   int N, int K, int M, void* stream)
 {
-    using namespace fp8kv;
-    if (!W || !St || !Xb || !Out) return FP8KV_ERR_ARG;
-    if (N < 1 || K < 32 || M < 1) return FP8KV_ERR_ARG;
-    if (M > 16 || (K & 31) != 0) return FP8KV_ERR_SHAPE;
-    if (!aligned(W, 16) || !aligned(Xb, 16) || !aligned(Out, 2)) return FP8KV_ERR_ALIGN;
-    const int G = K >> 5;
-    int per_wave = (G + kWavesPerWG - 1) / kWavesPerWG;
-    per_wave = (per_wave + 3) & ~3;
-    const dim3 grid((unsigned)((N + kRowsPerWG - 1) / kRowsPerWG));
-    const dim3 block(64 * kWavesPerWG);
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(h4mv_mfma_kernel<4>, grid, block, 0, s,
-                       static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St),
-                       static_cast<const __bf16*>(Xb), static_cast<__bf16*>(Out), N, K, M, per_wave);
-    return finish_launch();
+    return fp8kv::h4mv_detail::launch_h4mv<__bf16>(W, St, Xb, Out, N, K, M, stream);
+}
+
+extern "C" int h4mv_f32_launch_status(const void* W, const void* St, const void* Xb, void* Out,
+                                      int N, int K, int M, void* stream)
+{
+    return fp8kv::h4mv_detail::launch_h4mv<float>(W, St, Xb, Out, N, K, M, stream);
 }
 
 extern "C" void h4mv_launch(const void* W, const void* St, const void* Xb, void* Out,

@@ -24,6 +24,10 @@ SIGNATURES: dict[str, tuple] = {
     # reference ABI, h4mv/h4mv.cu:106-107 / h4mv/fp8kv_hipw4.py:21-23
     "h4mv_launch": (None, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
     "h4mv_launch_status": (_c_i, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
+    "h4mv_f32_launch_status": (_c_i, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
+    # host-only diagnostics (csrc/fp8kv_diag.h)
+    "fp8kv_h4mv_audit": (_c_i, [_c_i] * 3),
+    "fp8kv_h4mv_tune": (None, [_c_i] * 2),
 }
 
 _lock = threading.Lock()

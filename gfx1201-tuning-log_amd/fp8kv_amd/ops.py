@@ -25,10 +25,11 @@ def repack_scales(weight_scale: torch.Tensor) -> torch.Tensor:
 
 
 def h4mv(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor,
-         out: torch.Tensor | None = None) -> torch.Tensor:
-    """bf16 [M, N] = x [M, K] . dequant(weight [N, K/2], scales_nk [N, K/32])^T.
+         out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """[M, N] = x [M, K] . dequant(weight [N, K/2], scales_nk [N, K/32])^T in bf16 (or fp32).
 
-    Same contract as the reference's ``lib.h4mv_launch`` call in h4mv/fp8kv_hipw4.py:78-83.
+    Same contract as the reference's ``lib.h4mv_launch`` call in h4mv/fp8kv_hipw4.py:78-83;
+    ``out_dtype=torch.float32`` selects the unrounded fp32-output entry point.
     """
     _require(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(),
              "x must be a contiguous 2-D bf16 device tensor")
@@ -40,13 +41,15 @@ def h4mv(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor,
     _require(scales_nk.dtype == torch.uint8 and tuple(scales_nk.shape) == (N, K // 32)
              and scales_nk.is_contiguous(), f"scales must be contiguous uint8 [{N}, {K // 32}]")
     _require(weight.device == x.device == scales_nk.device, "tensors on different devices")
+    _require(out_dtype in (torch.bfloat16, torch.float32), "out_dtype must be bf16 or fp32")
     if out is None:
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+        out = torch.empty((M, N), dtype=out_dtype, device=x.device)
     else:
-        _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (M, N) and out.is_contiguous(),
-                 "out must be contiguous bf16 [M, N]")
+        _require(out.dtype == out_dtype and tuple(out.shape) == (M, N) and out.is_contiguous(),
+                 f"out must be contiguous {out_dtype} [M, N]")
     lib = _lib.load()
-    st = lib.h4mv_launch_status(weight.data_ptr(), scales_nk.data_ptr(), x.data_ptr(),
-                                out.data_ptr(), N, K, M, _stream_ptr(x))
+    fn = lib.h4mv_launch_status if out_dtype == torch.bfloat16 else lib.h4mv_f32_launch_status
+    st = fn(weight.data_ptr(), scales_nk.data_ptr(), x.data_ptr(), out.data_ptr(), N, K, M,
+            _stream_ptr(x))
     _lib.check("h4mv_launch_status", st)
     return out

@@ -54,6 +54,13 @@ void h4mv_launch(const void* W, const void* St, const void* Xb, void* Out,
 int h4mv_launch_status(const void* W, const void* St, const void* Xb, void* Out,
                        int N, int K, int M, void* stream);
 
+/* Same operation with an fp32 output Out[M, N] (no output rounding).
+ * Replaces the fp32-output matvec ABI of the reference's HIP demo,
+ * w4-hip-demo/w4_hip_demo.cu:157-171 (w4matvec_v{1,2}_launch(W, St, X, Y, N, K, stream), Y fp32),
+ * generalised to 1 <= M <= 16 rows of bf16 X. */
+int h4mv_f32_launch_status(const void* W, const void* St, const void* Xb, void* Out,
+                           int N, int K, int M, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,28 @@ def w4mv(W: np.ndarray, St: np.ndarray, X: np.ndarray, chunk: int = 2048) -> np.
     return out
 
 
+def bf16_ulp(v: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 values (8 significant bits) in the binade of each |v|; 0 maps to 2^-133."""
+    v = np.abs(np.asarray(v, dtype=np.float64))
+    _, e = np.frexp(v)                                  # v = f * 2^e, f in [0.5, 1)
+    ulp = np.ldexp(1.0, e - 8)
+    return np.where(v == 0, 2.0 ** -133, ulp)
+
+
+def bf16_excess_error(y: np.ndarray, ref: np.ndarray) -> float:
+    """max over elements of (|y - ref| - ulp_bf16(ref)/2) / max|ref|, floored at 0.
+
+    A bf16 output can be no closer to the exact result than half a bf16 ulp, so this is the
+    error a bf16-output kernel adds on top of the unavoidable output rounding (0 for a
+    correctly rounded result, ~1e-6 for fp32 accumulation).
+    """
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.max(np.abs(ref))
+    ex = np.max(np.abs(y - ref) - 0.5 * bf16_ulp(ref))
+    return max(0.0, float(ex / den)) if den > 0 else float(max(0.0, ex))
+
+
 def rel_to_max_error(y: np.ndarray, ref: np.ndarray) -> float:
     """max |y - ref| / max |ref|: the matvec error measure of h4mv/h4mv_test.py:74."""
     y = np.asarray(y, dtype=np.float64)

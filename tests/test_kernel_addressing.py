@@ -1,0 +1,31 @@
+"""Host-side address audits of the hand-written kernels (CPU only, no GPU code runs).
+
+Each audit enumerates every global and LDS byte the kernel's launch would touch for a shape and
+checks it against the operand sizes and the LDS allocation, using the same index functions the
+kernel is compiled from."""
+import itertools
+import random
+
+import pytest
+
+CFG4_SHAPES = [(4096, 3584), (3584, 3072), (37888, 3584), (3584, 18944), (28672, 4096)]
+
+
+@pytest.mark.parametrize("N,K", CFG4_SHAPES)
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+def test_h4mv_stream_in_bounds_model_shapes(lib, N, K, M):
+    assert lib.fp8kv_h4mv_audit(N, K, M) == 0
+
+
+def test_h4mv_stream_in_bounds_random_shapes(lib):
+    rng = random.Random(0)
+    for _ in range(300):
+        N = rng.choice([1, 2, 15, 16, 17, 31, 33, 100, 1000, 4097]) + rng.randrange(0, 3)
+        K = 512 * rng.randrange(1, 41)
+        M = rng.randrange(1, 9)
+        assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
+
+
+def test_h4mv_register_path_shapes_are_reported(lib):
+    for N, K, M in itertools.product([1, 64], [32, 96, 4128], [1, 9, 16]):
+        assert lib.fp8kv_h4mv_audit(N, K, M) == 1

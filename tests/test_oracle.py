@@ -156,6 +156,19 @@ def test_matvec_repack_is_transpose():
     assert St.shape == (4, 3) and St.flags["C_CONTIGUOUS"] and St[2, 1] == S[1, 2]
 
 
+def test_bf16_ulp_matches_torch_rounding():
+    rng = np.random.default_rng(7)
+    v = rng.standard_normal(5000) * np.exp2(rng.integers(-30, 30, 5000))
+    u = matvec.bf16_ulp(v)
+    b = torch.tensor(v).to(torch.bfloat16).to(torch.float64).numpy()
+    assert np.all(np.abs(b - v) <= u / 2)                       # RNE lands within half an ulp
+    up = np.abs(b) + matvec.bf16_ulp(b)                         # next value up from b
+    same_binade = np.frexp(up)[1] == np.frexp(np.abs(b))[1]
+    rt = torch.tensor(up[same_binade]).to(torch.bfloat16).to(torch.float64).numpy()
+    assert np.array_equal(rt, up[same_binade])                  # ... and is representable
+    assert matvec.bf16_excess_error(b, v) == 0.0
+
+
 def test_planted_nibble_swap_fails_probe(monkeypatch):
     def swapped(p):
         p = np.asarray(p, dtype=np.uint8)
