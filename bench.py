@@ -1,19 +1,24 @@
 """Benchmark of the hot path on one MI355X: prints ONE JSON line (rank 0).
 
 Metric: "µs/layer + achieved HBM GB/s (%roofline): decode attn b8@4k, W4 GEMV M=1".
-``value`` is the W4 GEMV at M=1 on configs[1] (K=4096, N=28672) in GB/s of algorithmic bytes;
-the decode-attention b8@4k leg, the other M values and prefill are reported beside it.
+``value`` is the W4 GEMV at M=1 on configs[1] (K=4096, N=28672) in GB/s of algorithmic bytes over
+the timed region; the decode-attention b8@4k leg, M=4/8 and the other legs are reported beside it.
 
 A "step" is one launch of the kernel over one batch of synthetic input.  Inputs are resident in
 HBM before the timed region and rotate over enough copies (> 2x the 256 MB Infinity Cache) that
-every step reads its bytes from HBM.  Timing: HIP events recorded on the stream the kernels run
-on (torch's current stream), ``--warmup`` untimed steps, then exactly ``--steps`` timed steps.
+every step reads its bytes from HBM.  Timing: HIP events on the stream the kernels run on
+(torch's current stream): ``--warmup`` untimed steps, then exactly ``--steps`` timed steps, each
+bracketed by its own start/end event pair, the whole region by a synchronize on both sides; a
+GPU-side spin queued ahead of the timed region keeps the host's launch overhead out of the events.
+  * ``ms_per_step`` / ``value``: timed-region wall time / steps (includes launch gaps);
+  * ``roofline.achieved``: algorithmic bytes / mean(end_i - start_i), the kernel's own duration.
 The CPU baseline is the oracle's torch-CPU fp32 dequant path on a bounded sample (rank 0, N=1).
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import statistics
@@ -26,6 +31,7 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 ROTATE_BYTES = 1 << 30         # >= 4x the 256 MB MALL
+METRIC = "µs/layer + achieved HBM GB/s (%roofline): decode attn b8@4k, W4 GEMV M=1"
 
 
 def w4_bytes(N: int, K: int, M: int) -> int:
@@ -33,21 +39,45 @@ def w4_bytes(N: int, K: int, M: int) -> int:
     return N * K // 2 + N * K // 32 + 2 * M * K + 2 * M * N
 
 
+def decode_bytes(ctx, HQ: int, HKV: int, D: int, PBLK: int) -> int:
+    """Algorithmic bytes of one decode call: K + V of every context token, q, out, block ids."""
+    return (sum(ctx) * HKV * D * 2 + 2 * len(ctx) * HQ * D * 2
+            + sum(math.ceil(c / PBLK) for c in ctx) * 4)
+
+
 def time_launches(launch, n_sets: int, steps: int, warmup: int):
-    """Run ``launch(i % n_sets)`` warmup + steps times; return (avg ms per step, per-step ms list)."""
+    """Run ``launch(i % n_sets)`` warmup + steps times.
+
+    Returns (wall ms per step over the timed region, list of per-launch kernel ms)."""
     import torch
     for i in range(warmup):
         launch(i % n_sets)
     torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    ev[0].record()
+    # A GPU-side spin queued first lets the host enqueue every timed launch before the GPU reaches
+    # them, so the events measure GPU time and not the host's per-call launch overhead.
+    torch.cuda._sleep(int(2e6) + steps * 60000)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0.record()
     for i in range(steps):
+        st[i].record()
         launch(i % n_sets)
-        ev[i + 1].record()
+        en[i].record()
+    t1.record()
     torch.cuda.synchronize()
-    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    total = ev[0].elapsed_time(ev[steps])
-    return total / steps, per
+    per = [st[i].elapsed_time(en[i]) for i in range(steps)]
+    return t0.elapsed_time(t1) / steps, per
+
+
+def _summary(wall_ms, per, nbytes):
+    k_us = statistics.mean(per) * 1e3
+    return {"us_step": round(wall_ms * 1e3, 3), "us_kernel": round(k_us, 3),
+            "us_kernel_median": round(statistics.median(per) * 1e3, 3),
+            "bytes": nbytes, "GBps_step": round(nbytes / (wall_ms * 1e-3) / 1e9, 1),
+            "GBps_kernel": round(nbytes / (k_us * 1e-6) / 1e9, 1),
+            "frac_kernel": round(nbytes / (k_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def bench_w4(N: int, K: int, M: int, steps: int, warmup: int):
@@ -67,12 +97,58 @@ def bench_w4(N: int, K: int, M: int, steps: int, warmup: int):
     def launch(i):
         ops.h4mv(X, Ws[i], Ss[i], out=Y)
 
-    ms, per = time_launches(launch, n_sets, steps, warmup)
-    b = w4_bytes(N, K, M)
+    wall, per = time_launches(launch, n_sets, steps, warmup)
     del Ws, Ss
     torch.cuda.empty_cache()
-    return {"us": ms * 1e3, "us_median_event": statistics.median(per) * 1e3,
-            "bytes": b, "gbs": b / (ms * 1e-3) / 1e9, "rotation_sets": n_sets}
+    r = _summary(wall, per, w4_bytes(N, K, M))
+    r["rotation_sets"] = n_sets
+    return r
+
+
+def bench_decode(ctx, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK=16, pool_blocks=5060,
+                 seed=0):
+    """Decode attention over rotated engine-layout layer pools [NB, HKV, PBLK, 2D] (K | V)."""
+    import torch
+    from fp8kv_amd import ops, workloads
+    dev = torch.device("cuda")
+    NS = len(ctx)
+    pool_bytes = pool_blocks * HKV * PBLK * 2 * D
+    n_sets = max(8, -(-2 * (256 << 20) // pool_bytes) + 1)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    pools = []
+    for _ in range(n_sets):
+        kv = torch.randint(0, 256, (pool_blocks, HKV, PBLK, 2 * D), dtype=torch.uint8, device=dev,
+                           generator=g)
+        kv[(kv & 0x7F) == 0x7F] = 0x3C                   # no NaN codes in the synthetic cache
+        pools.append(workloads.engine_views(kv, D) + (kv,))
+    gc = torch.Generator().manual_seed(seed)
+    need = [math.ceil(c / PBLK) for c in ctx]
+    perm = torch.randperm(pool_blocks, generator=gc)
+    bt = torch.zeros(NS, max(need), dtype=torch.int32)
+    o = 0
+    for s, n in enumerate(need):
+        bt[s, :n] = perm[o:o + n].to(torch.int32)
+        o += n
+    bt = bt.to(dev)
+    q = torch.randn(NS, HQ, D, generator=gc).to(torch.bfloat16).to(dev)
+    out = torch.empty_like(q)
+    qsl = torch.arange(NS + 1, dtype=torch.int32, device=dev)
+    sl = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    ks = torch.tensor([0.01], device=dev)
+    vs = torch.tensor([0.01], device=dev)
+    nsplit = ops.decode_num_splits(NS, HKV, max(ctx))
+
+    def launch(i):
+        kc, vc, _ = pools[i]
+        ops.decode_attention(q, kc, vc, out, qsl, sl, bt, ks, vs, 1 / math.sqrt(D),
+                             num_splits=nsplit)
+
+    wall, per = time_launches(launch, n_sets, steps, warmup)
+    del pools
+    torch.cuda.empty_cache()
+    r = _summary(wall, per, decode_bytes(ctx, HQ, HKV, D, PBLK))
+    r.update({"rotation_sets": n_sets, "num_splits": nsplit})
+    return r
 
 
 def cpu_baseline_w4(N: int, K: int, budget_s: float = 15.0):
@@ -105,11 +181,23 @@ def cpu_baseline_w4(N: int, K: int, budget_s: float = 15.0):
         if time.perf_counter() - t_start > budget_s and len(times) >= 3:
             break
     med = statistics.median(times)
-    return {"value": w4_bytes(N, K, 1) / med / 1e9, "unit": "GB/s", "cores": threads,
+    return {"value": round(w4_bytes(N, K, 1) / med / 1e9, 4), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"full cfg1 (N={N}, K={K}, M=1) torch-CPU fp32 dequant+GEMV, median of "
                       f"{len(times)} after 3 warm-ups ({med * 1e3:.1f} ms/call)",
-            "cpu_model": platform.processor() or platform.machine()}
+            "torch_threads": torch.get_num_threads(),
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def main():
@@ -118,6 +206,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--legs", default="w4,decode",
+                    help="comma list of legs to run (w4, decode)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one GPU; "
@@ -127,39 +217,51 @@ def main():
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    legs_wanted = set(args.legs.split(","))
     N, K = 28672, 4096
-    m1 = bench_w4(N, K, 1, args.steps, args.warmup)
-    m4 = bench_w4(N, K, 4, args.steps, args.warmup)
-    m8 = bench_w4(N, K, 8, args.steps, args.warmup)
-    cpu = None if args.no_cpu_baseline else cpu_baseline_w4(N, K)
+    legs = {}
+    m1 = None
+    if "w4" in legs_wanted:
+        m1 = bench_w4(N, K, 1, args.steps, args.warmup)
+        legs["w4_gemv_M1"] = m1
+        legs["w4_gemv_M4"] = bench_w4(N, K, 4, args.steps, args.warmup)
+        legs["w4_gemv_M8"] = bench_w4(N, K, 8, args.steps, args.warmup)
+    dec = None
+    if "decode" in legs_wanted:
+        dec = bench_decode([4096] * 8, args.steps, args.warmup)
+        legs["decode_b8_4k"] = dec
+        g = torch.Generator().manual_seed(2)
+        ctx2 = torch.randint(1024, 4097, (8,), generator=g).tolist()
+        legs["decode_cfg2"] = bench_decode(ctx2, args.steps, args.warmup, seed=2)
+        legs["decode_cfg2"]["ctx"] = ctx2
+    cpu = None if (args.no_cpu_baseline or m1 is None) else cpu_baseline_w4(N, K)
+    head = m1 if m1 is not None else dec
     line = {
-        "metric": "µs/layer + achieved HBM GB/s (%roofline): decode attn b8@4k, W4 GEMV M=1",
-        "value": round(m1["gbs"], 1),
+        "metric": METRIC,
+        "value": head["GBps_step"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(m1["us"] / 1e3, 5),
+        "ms_per_step": round(head["us_step"] / 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "e2m1xbf16->f32",
-        "data": "synthetic (seeded random codes/scales/activations, rotated over >1 GB)",
-        "config": {"workload": "configs[1] MXFP4 W4A16 matvec K=4096 N=28672 M=1",
-                   "rotation_sets": m1["rotation_sets"]},
-        "roofline": {"bound": "hbm", "achieved": round(m1["gbs"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(m1["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+        "dtype": "e2m1xbf16->f32" if m1 is not None else "e4m3xbf16->f32",
+        "data": "synthetic (seeded random codes/scales/activations and fp8 KV pools, rotated over >1 GB)",
+        "config": {"workload": ("configs[1] MXFP4 W4A16 matvec K=4096 N=28672 M=1" if m1 is not None
+                                else "decode attention b8@4k, 24/4 heads, D=128, block 16"),
+                   "rotation_sets": head["rotation_sets"]},
+        "roofline": {"bound": "hbm", "achieved": head["GBps_kernel"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": head["frac_kernel"], "traffic": None},
         "cpu_baseline": cpu,
-        "legs": {
-            "w4_gemv_M1": {"us": round(m1["us"], 2), "us_median": round(m1["us_median_event"], 2),
-                           "GBps": round(m1["gbs"], 1), "frac": round(m1["gbs"] / HBM_PEAK_GBS, 4)},
-            "w4_gemv_M4": {"us": round(m4["us"], 2), "GBps": round(m4["gbs"], 1),
-                           "frac": round(m4["gbs"] / HBM_PEAK_GBS, 4)},
-            "w4_gemv_M8": {"us": round(m8["us"], 2), "GBps": round(m8["gbs"], 1),
-                           "frac": round(m8["gbs"] / HBM_PEAK_GBS, 4)},
-        },
+        "legs": legs,
     }
+    if dec is not None:
+        line["roofline_decode_b8_4k"] = {"bound": "hbm", "achieved": dec["GBps_kernel"],
+                                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                         "frac": dec["frac_kernel"], "us_per_layer": dec["us_kernel"],
+                                         "traffic": None}
     print(json.dumps(line))
 
 

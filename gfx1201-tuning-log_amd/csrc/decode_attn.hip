@@ -1,0 +1,640 @@
+// Paged fp8-e4m3 KV decode attention for gfx950 (split-context flash decoding, one launch).
+//
+// Reference semantics: vllm-fp8kv/fp8kv_v3.py:3-113 (split kernel + merge kernel) and its launch
+// wrapper fp8kv_v3.py:116-139:
+//   * one query token per sequence, at row query_start_loc[s]; it attends to tokens [0, seq_len);
+//   * token t lives in block block_table[s, t / block_size], slot t % block_size; K and V are read
+//     through independent (block, slot, head) strides, so both the standalone [NB, PBLK, HKV, D]
+//     cache and the engine's K|V-interleaved view work;
+//   * fp8 -> bf16 is exact; S = (q . k) * sm_scale * k_scale (k_scale read on the device);
+//     the probabilities are rounded to bf16 before P.V, the row sums use the fp32 values
+//     (fp8kv_v3.py:67-74); the output is (sum_t p_t v_t) * v_scale / l in bf16 (fp8kv_v3.py:110-113).
+//   * a sequence with no context writes zeros (the reference kernel writes NaN there).
+//
+// gfx950 design:
+//   * grid (num_splits, HKV, NS); a workgroup of W waves owns a 16-aligned token span of its
+//     (sequence, kv head); wave w takes chunks w, w + W, ... of the span, a chunk being NG
+//     16-token groups.  Q, the scales and the wave's block ids are requested first, then every K
+//     and V byte of the wave's first chunk (and, with DEPTH 2, of the next one while the current
+//     one is computed).
+//   * S^T = K . Q^T on v_mfma_f32_16x16x32_bf16: A = 16 tokens x 32 d of K, B = Q^T with the GQA
+//     query heads of the kv head in columns 0..GQA-1 (zero beyond).  Lane (r, p) = (lane % 16,
+//     lane / 16) loads 16 bytes of token r at d = 16 p and at d = 64 + 16 p; the d order is
+//     arbitrary for a reduction as long as the Q fragments use the same one.
+//   * O^T = V^T . P^T on the same MFMA: A = V^T (16 d x 32 tokens), B = P^T (32 tokens x heads),
+//     so S and O both keep the head in lane % 16 and the softmax rescale is lane-local.  The A
+//     operand needs 8 tokens of one d per lane while V is d-contiguous, so lane (c, p) loads
+//     8 bytes (d = 8c .. 8c+7) of each of its 8 tokens - four full 128-byte rows per load
+//     instruction - and transposes the 8 x 8 byte block in its own registers (v_perm_b32) while
+//     converting (v_cvt_scalef32_pk_bf16_fp8 turns byte pairs into bf16 pairs).
+//   * online softmax in the exp2 domain; the W waves merge in LDS, the splits merge through a
+//     per-(sequence, kv head) ticket: the workgroup that finishes last merges every split's
+//     partial record and resets the ticket to zero, so no memset is needed between calls.
+//     Records are written and read with device-coherent (agent-scope) accesses, which need no
+//     cache-wide write-back or invalidate.
+#include "fp8kv_common.h"
+#include "fp8kv_status.h"
+#include "fp8kv_diag.h"
+
+namespace fp8kv {
+namespace decode_detail {
+
+constexpr int kD = 128;
+constexpr int kMaxGqa = 16;
+constexpr int kMergeBatch = 8;           // split records requested at once by the final merge
+constexpr float kLog2e = 1.4426950408889634f;
+// Ticket counters occupy a fixed region at the start of the scratch buffer, independent of the
+// launch geometry, so a buffer shared by calls of different shapes never has one call's partial
+// records where another call expects zeroed counters.
+constexpr int kMaxPairs = 65536;
+constexpr int kMaxSplits = 256;
+
+struct Params {
+    const __bf16* q;
+    const uint8_t* k;
+    const uint8_t* v;
+    __bf16* out;
+    const int32_t* qsl;
+    const int32_t* seq_lens;
+    const int32_t* bt;
+    const float* k_scale;
+    const float* v_scale;
+    float* part;            // [records][gqa * (D + 2)]: o (gqa x D), m (gqa), l (gqa)
+    uint32_t* counters;     // [NS * HKV]
+    int64_t q_stride, o_stride, bt_stride;
+    int64_t sk0, sk1, sk2, sv0, sv1, sv2;
+    float sm_scale;
+    int hkv, gqa, pblk, nsplit;
+};
+
+__host__ __device__ inline int record_floats(int gqa) { return gqa * (kD + 2); }
+
+// Token span [lo, hi) of split `sp`: cdiv(seq_len, nsplit) rounded up to 16 tokens, so every
+// 16-token group of a span lies in one cache block when block_size % 16 == 0.
+__host__ __device__ inline void split_span(int seqlen, int nsplit, int sp, int& lo, int& hi)
+{
+    int span = (seqlen + nsplit - 1) / nsplit;
+    span = (span + 15) & ~15;
+    lo = sp * span;
+    hi = seqlen < lo + span ? seqlen : lo + span;
+}
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+
+__device__ __forceinline__ uint32_t bf16x2_bits(bf16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Device-coherent (agent-scope) accesses for the cross-workgroup partial records: they bypass the
+// per-XCD L2 state that ordinary accesses may hit, so no cache-wide write-back or invalidate is
+// needed to hand records from one workgroup to another.
+__device__ __forceinline__ void store_coherent(float* p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A fragments of O^T = V^T . P^T for one 32-token group: vr[j] = bytes d = 8c .. 8c+7 of the
+// group's k-slot j token.  Fragment n (d row 8c + n) dword k = bf16 pair (k-slot 2k, 2k+1).
+__device__ __forceinline__ void v_fragments(const u32x2_t (&vr)[8], u32x4_t (&bf)[8])
+{
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t a = vr[2 * k][w], b = vr[2 * k + 1][w];
+            const uint32_t x = __builtin_amdgcn_perm(b, a, 0x05010400u);   // a0 b0 a1 b1
+            const uint32_t y = __builtin_amdgcn_perm(b, a, 0x07030602u);   // a2 b2 a3 b3
+            bf[4 * w + 0][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, false));
+            bf[4 * w + 1][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, true));
+            bf[4 * w + 2][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(y, 1.0f, false));
+            bf[4 * w + 3][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(y, 1.0f, true));
+        }
+    }
+}
+
+// K and V registers of one chunk of NG 16-token groups (lane (r, p) = (lane % 16, lane / 16)):
+//   kr[g][j]: 16 bytes of token c0 + 16 g + r at d = 64 j + 16 p;
+//   vr[G][j]: 8 bytes (d = 8 r .. 8 r + 7) of token c0 + 32 G + 4 p + j (j < 4) or
+//             c0 + 32 G + 16 + 4 p + (j - 4) (j >= 4): the k-slot order of the P^T fragments.
+template <int NG>
+struct ChunkRegs {
+    u32x4_t kr[NG][2];
+    u32x2_t vr[NG / 2][8];
+};
+
+// Per-lane softmax state of one wave: running max and this lane's share of the running sum of
+// head lr (log2 domain), and o[n][i] = head lr at d = 32 lp + 8 i + n.
+struct WaveState {
+    float m_run;
+    float l_run;
+    f32x4_t o[8];
+};
+
+// Block ids of a wave's chunks, prefetched with one vector load per 64 / NG chunks: lane
+// NG k + g of batch b holds the block of group g of the wave's chunk (64 / NG) b + k (0 past the
+// context).
+template <int NG>
+__device__ __forceinline__ int load_block_ids(const Params& P, const int32_t* btrow, int first,
+                                              int stride, int hi, int batch, int lane)
+{
+    constexpr int CPB = 64 / NG;
+    const int t0 = first + stride * (CPB * batch + lane / NG) + 16 * (lane % NG);
+    return t0 < hi ? btrow[t0 / P.pblk] : 0;
+}
+
+// Per-lane byte offsets of the chunk loads within one 16-token group (32-bit: the host rejects
+// slot strides that could overflow them).
+struct LaneOffsets {
+    uint32_t k;          // token lr, d = 16 lp
+    uint32_t v[4];       // token 4 lp + i, d = 8 lr
+};
+
+__device__ __forceinline__ LaneOffsets lane_offsets(const Params& P, int lr, int lp)
+{
+    LaneOffsets o;
+    o.k = (uint32_t)lr * (uint32_t)P.sk1 + 16u * (uint32_t)lp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o.v[i] = (uint32_t)(4 * lp + i) * (uint32_t)P.sv1 + 8u * (uint32_t)lr;
+    return o;
+}
+
+// Request every K and V byte of the chunk starting at token c0 (tokens >= hi are zero-filled and
+// never read).  Wave-uniform branches per 16-token group: full groups load unconditionally, the
+// group holding hi masks per lane.  Group g's block id is lane NG kb_idx + g of `bids`; the
+// group's base address is scalar, the per-lane part a 32-bit offset.
+template <int NG>
+__device__ __forceinline__ void issue_chunk(ChunkRegs<NG>& c, const Params& P, const LaneOffsets& lo_,
+                                            int bids, int kb_idx, int kh, int c0, int hi, int lr, int lp)
+{
+    const u32x4_t z4 = {0u, 0u, 0u, 0u};
+    const u32x2_t z2 = {0u, 0u};
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int t0 = c0 + 16 * g;
+        if (t0 < hi) {
+            const int64_t blk = __builtin_amdgcn_readlane(bids, NG * kb_idx + g);
+            const int slot0 = t0 % P.pblk;
+            const uint8_t* kb = P.k + blk * P.sk0 + (int64_t)slot0 * P.sk1 + (int64_t)kh * P.sk2;
+            const uint8_t* vb = P.v + blk * P.sv0 + (int64_t)slot0 * P.sv1 + (int64_t)kh * P.sv2;
+            if (t0 + 16 <= hi) {
+                c.kr[g][0] = load_nt_16(kb + lo_.k);
+                c.kr[g][1] = load_nt_16(kb + lo_.k + 64);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    c.vr[g >> 1][4 * (g & 1) + i] =
+                        __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(vb + lo_.v[i]));
+            } else {
+                const bool kok = t0 + lr < hi;
+                c.kr[g][0] = kok ? load_nt_16(kb + lo_.k) : z4;
+                c.kr[g][1] = kok ? load_nt_16(kb + lo_.k + 64) : z4;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool vok = t0 + 4 * lp + i < hi;
+                    c.vr[g >> 1][4 * (g & 1) + i] =
+                        vok ? __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(vb + lo_.v[i])) : z2;
+                }
+            }
+        } else {
+            c.kr[g][0] = z4;
+            c.kr[g][1] = z4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c.vr[g >> 1][4 * (g & 1) + i] = z2;
+        }
+    }
+}
+
+// S^T = K . Q^T, online softmax update, O^T += V^T . P^T for one chunk.
+template <int NG>
+__device__ __forceinline__ void consume_chunk(const ChunkRegs<NG>& c, WaveState& st, const u32x4_t (&qf)[4],
+                                              float qk_scale, int c0, int hi, int lp)
+{
+    // lane (h, p) gets S[token c0 + 16 g + 4 p + i][head h]
+    f32x4_t s[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        acc = mfma16x16x32_bf16(fp8x8_to_bf16x8(c.kr[g][0][0], c.kr[g][0][1]), as_bf16x8(qf[0]), acc);
+        acc = mfma16x16x32_bf16(fp8x8_to_bf16x8(c.kr[g][0][2], c.kr[g][0][3]), as_bf16x8(qf[1]), acc);
+        acc = mfma16x16x32_bf16(fp8x8_to_bf16x8(c.kr[g][1][0], c.kr[g][1][1]), as_bf16x8(qf[2]), acc);
+        acc = mfma16x16x32_bf16(fp8x8_to_bf16x8(c.kr[g][1][2], c.kr[g][1][3]), as_bf16x8(qf[3]), acc);
+        s[g] = acc;
+    }
+    float mc = neg_inf();
+    if (c0 + 16 * NG <= hi) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s[g][i] *= qk_scale;
+                mc = fmaxf(mc, s[g][i]);
+            }
+    } else {
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tok = c0 + 16 * g + 4 * lp + i;
+                const float x = tok < hi ? s[g][i] * qk_scale : neg_inf();
+                s[g][i] = x;
+                mc = fmaxf(mc, x);
+            }
+    }
+    mc = fmaxf(mc, __shfl_xor(mc, 16));
+    mc = fmaxf(mc, __shfl_xor(mc, 32));
+    const float m_new = fmaxf(st.m_run, mc);
+    const float m_use = m_new == neg_inf() ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(st.m_run - m_use);
+    float psum = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float pv = __builtin_amdgcn_exp2f(s[g][i] - m_use);
+            s[g][i] = pv;
+            psum += pv;
+        }
+    st.l_run = st.l_run * alpha + psum;
+    st.m_run = m_new;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) st.o[n] *= alpha;
+#pragma unroll
+    for (int G = 0; G < NG / 2; ++G) {
+        u32x4_t pb;
+        pb[0] = pack_bf16x2(s[2 * G][0], s[2 * G][1]);
+        pb[1] = pack_bf16x2(s[2 * G][2], s[2 * G][3]);
+        pb[2] = pack_bf16x2(s[2 * G + 1][0], s[2 * G + 1][1]);
+        pb[3] = pack_bf16x2(s[2 * G + 1][2], s[2 * G + 1][3]);
+        u32x4_t va[8];
+        v_fragments(c.vr[G], va);
+#pragma unroll
+        for (int n = 0; n < 8; ++n) st.o[n] = mfma16x16x32_bf16(as_bf16x8(va[n]), as_bf16x8(pb), st.o[n]);
+    }
+}
+
+template <int W, int NG, int DEPTH>
+__global__ void __launch_bounds__(W * 64)
+decode_kernel(Params P)
+{
+    constexpr int CH = 16 * NG;                 // tokens per chunk
+    constexpr int CPB = 64 / NG;                // chunks per block-id batch
+    constexpr int T = W * 64;
+    constexpr int EPT = (kMaxGqa * kD + T - 1) / T;   // merge elements per thread (upper bound)
+    __shared__ float lds_ml[W][kMaxGqa][2];
+    __shared__ __align__(16) float lds_o[W][kMaxGqa][kD];
+    __shared__ int lds_last;
+    static_assert(W * kMaxGqa * kD >= 2 * kMaxSplits * kMaxGqa, "merge statistics must fit in lds_o");
+
+    const int sp = blockIdx.x, kh = blockIdx.y, seq = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 15;
+    const int lp = lane >> 4;
+    const int gqa = P.gqa;
+
+    const int seqlen = P.seq_lens[seq];
+    const int qtok = P.qsl[seq];
+    int lo, hi;
+    split_span(seqlen, P.nsplit, sp, lo, hi);
+    const int32_t* btrow = P.bt + (int64_t)seq * P.bt_stride;
+
+    // Q^T fragments and the scales first (they do not depend on the block table): lane (h, p)
+    // holds head h at d = 16p + (0..15) and 64 + 16p + (0..15).
+    u32x4_t qf[4];
+    {
+        const u32x4_t zero = {0u, 0u, 0u, 0u};
+        const bool ok = lr < gqa;
+        const __bf16* qrow = P.q + (int64_t)qtok * P.q_stride + (int64_t)(kh * gqa + (ok ? lr : 0)) * kD;
+        qf[0] = ok ? load_16(qrow + 16 * lp) : zero;
+        qf[1] = ok ? load_16(qrow + 16 * lp + 8) : zero;
+        qf[2] = ok ? load_16(qrow + 64 + 16 * lp) : zero;
+        qf[3] = ok ? load_16(qrow + 64 + 16 * lp + 8) : zero;
+    }
+    const float qk_scale = P.sm_scale * P.k_scale[0] * kLog2e;
+    const float vs = P.v_scale[0];
+
+    // Block ids of the wave's first two batches of chunks, then the first chunk's loads.
+    const int stride = CH * W;
+    const int c_first = lo + CH * wave;
+    int c0 = c_first;
+    int bid_cur = load_block_ids<NG>(P, btrow, c_first, stride, hi, 0, lane);
+    int bid_next = load_block_ids<NG>(P, btrow, c_first, stride, hi, 1, lane);
+    const LaneOffsets lofs = lane_offsets(P, lr, lp);
+    ChunkRegs<NG> ca;
+    [[maybe_unused]] ChunkRegs<NG> cb;
+    issue_chunk<NG>(ca, P, lofs, bid_cur, 0, kh, c0, hi, lr, lp);
+    int k_issue = 1;                       // index (within the wave) of the next chunk to request
+
+    WaveState st;
+    st.m_run = neg_inf();
+    st.l_run = 0.f;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) st.o[n] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+
+    // Block-id batches rotate every CPB chunks, one batch ahead of the loads that need them.
+    auto next_ids = [&]() {
+        if (k_issue % CPB == 0) {
+            bid_cur = bid_next;
+            bid_next = load_block_ids<NG>(P, btrow, c_first, stride, hi, k_issue / CPB + 1, lane);
+        }
+    };
+    if constexpr (DEPTH == 1) {
+        while (c0 < hi) {
+            consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
+            c0 += stride;
+            if (c0 >= hi) break;
+            next_ids();
+            issue_chunk<NG>(ca, P, lofs, bid_cur, k_issue % CPB, kh, c0, hi, lr, lp);
+            ++k_issue;
+        }
+    } else {
+        // two-deep software pipeline: the next chunk is requested before the current one is used
+        while (c0 < hi) {
+            const int c1 = c0 + stride;
+            next_ids();
+            issue_chunk<NG>(cb, P, lofs, bid_cur, k_issue % CPB, kh, c1, hi, lr, lp);
+            ++k_issue;
+            consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
+            if (c1 >= hi) break;
+            const int c2 = c1 + stride;
+            next_ids();
+            issue_chunk<NG>(ca, P, lofs, bid_cur, k_issue % CPB, kh, c2, hi, lr, lp);
+            ++k_issue;
+            consume_chunk<NG>(cb, st, qf, qk_scale, c1, hi, lp);
+            c0 = c2;
+        }
+    }
+
+    // ---- merge the W waves in LDS ---------------------------------------------------------------
+    float l_run = st.l_run;
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    if (lp == 0 && lr < gqa) {
+        lds_ml[wave][lr][0] = st.m_run;
+        lds_ml[wave][lr][1] = l_run;
+    }
+    if (lr < gqa) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f32x4_t a = {st.o[0][i], st.o[1][i], st.o[2][i], st.o[3][i]};
+            f32x4_t b = {st.o[4][i], st.o[5][i], st.o[6][i], st.o[7][i]};
+            *reinterpret_cast<f32x4_t*>(&lds_o[wave][lr][32 * lp + 8 * i]) = a;
+            *reinterpret_cast<f32x4_t*>(&lds_o[wave][lr][32 * lp + 8 * i + 4]) = b;
+        }
+    }
+    __syncthreads();
+
+    const int E = gqa * kD;
+    const int64_t pair = (int64_t)seq * P.hkv + kh;
+    if (P.nsplit == 1) {
+        for (int e = tid; e < E; e += T) {
+            const int h = e / kD, d = e % kD;
+            float m = neg_inf();
+#pragma unroll
+            for (int w = 0; w < W; ++w) m = fmaxf(m, lds_ml[w][h][0]);
+            const float mu = m == neg_inf() ? 0.f : m;
+            float acc = 0.f, l = 0.f;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float f = __builtin_amdgcn_exp2f(lds_ml[w][h][0] - mu);
+                acc += f * lds_o[w][h][d];
+                l += f * lds_ml[w][h][1];
+            }
+            const float r = l > 0.f ? acc * vs / l : 0.f;
+            P.out[(int64_t)qtok * P.o_stride + (int64_t)(kh * gqa + h) * kD + d] = (__bf16)r;
+        }
+        return;
+    }
+
+    // ---- this split's partial record -------------------------------------------------------------
+    const int rf = record_floats(gqa);
+    float* rec = P.part + (pair * P.nsplit + sp) * rf;
+    for (int e = tid; e < E; e += T) {
+        const int h = e / kD, d = e % kD;
+        float m = neg_inf();
+#pragma unroll
+        for (int w = 0; w < W; ++w) m = fmaxf(m, lds_ml[w][h][0]);
+        const float mu = m == neg_inf() ? 0.f : m;
+        float acc = 0.f, l = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float f = __builtin_amdgcn_exp2f(lds_ml[w][h][0] - mu);
+            acc += f * lds_o[w][h][d];
+            l += f * lds_ml[w][h][1];
+        }
+        store_coherent(rec + e, acc);
+        if (d == 0) {
+            store_coherent(rec + E + h, m);
+            store_coherent(rec + E + gqa + h, l);
+        }
+    }
+
+    // ---- ticket: the last split of this (sequence, kv head) merges --------------------------------
+    // The records were written with device-coherent stores; once they have completed
+    // (vmcnt(0)) the ticket increment may be observed.  The merging workgroup reads them with
+    // device-coherent loads issued after it has seen the final ticket value.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t t = __hip_atomic_fetch_add(P.counters + pair, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        lds_last = (t == (uint32_t)(P.nsplit - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!lds_last) return;
+
+    // Final merge, one round trip per kMergeBatch splits: m and l of every split go to LDS once
+    // (one load per split and head), each thread loads the o values of its own elements
+    // tid + T j, and both are in flight together before the barrier.
+    const float* recs = P.part + pair * P.nsplit * rf;
+    const int NSG = P.nsplit * gqa;
+    float* wm = &lds_o[0][0][0];            // [nsplit][gqa] m, then [nsplit][gqa] l
+    float m[EPT], acc[EPT], l[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) { m[j] = neg_inf(); acc[j] = 0.f; l[j] = 0.f; }
+    for (int s0 = 0; s0 < P.nsplit; s0 += kMergeBatch) {
+        float ov[EPT][kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const int e = tid + T * j;
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b) {
+                const int s2 = s0 + b < P.nsplit ? s0 + b : P.nsplit - 1;
+                ov[j][b] = e < E ? load_coherent(recs + (int64_t)s2 * rf + e) : 0.f;
+            }
+        }
+        if (s0 == 0) {
+            for (int i = tid; i < NSG; i += T) {
+                const int s2 = i / gqa, h = i % gqa;
+                wm[i] = load_coherent(recs + (int64_t)s2 * rf + E + h);
+                wm[NSG + i] = load_coherent(recs + (int64_t)s2 * rf + E + gqa + h);
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const int h = (tid + T * j) / kD;
+            if (h >= gqa) continue;
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b) {
+                if (s0 + b >= P.nsplit) break;
+                const float ms = wm[(s0 + b) * gqa + h];
+                const float mn = fmaxf(m[j], ms);
+                const float mu = mn == neg_inf() ? 0.f : mn;
+                const float a = __builtin_amdgcn_exp2f(m[j] - mu);
+                const float f = __builtin_amdgcn_exp2f(ms - mu);
+                acc[j] = acc[j] * a + f * ov[j][b];
+                l[j] = l[j] * a + f * wm[NSG + (s0 + b) * gqa + h];
+                m[j] = mn;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = tid + T * j;
+        if (e < E) {
+            const float r = l[j] > 0.f ? acc[j] * vs / l[j] : 0.f;
+            P.out[(int64_t)qtok * P.o_stride + (int64_t)(kh * gqa) * kD + e] = (__bf16)r;
+        }
+    }
+    if (tid == 0)
+        __hip_atomic_store(P.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+inline size_t counters_bytes() { return (size_t)kMaxPairs * sizeof(uint32_t); }
+
+inline size_t scratch_bytes(int ns, int hq, int hkv, int nsplit)
+{
+    if (nsplit <= 1) return 0;
+    const int gqa = hq / hkv;
+    return counters_bytes() +
+           (size_t)ns * (size_t)hkv * (size_t)nsplit * (size_t)record_floats(gqa) * sizeof(float);
+}
+
+// Launch variants (waves per workgroup, 16-token groups per chunk, chunks in flight per wave).
+struct Variant {
+    int waves, ng, depth;
+};
+constexpr Variant kVariants[] = {{8, 4, 1}, {8, 2, 1}, {4, 4, 1}, {4, 4, 2}};
+constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
+
+// Launch tunables (host state; fp8kv_decode_tune changes them for sweeps).
+int g_variant = 0;
+int g_target_wgs = 256;
+
+// Splits per (sequence, kv head): enough workgroups to reach g_target_wgs, but never fewer
+// than one chunk per workgroup and never more than needed to give every wave one chunk... unless
+// that leaves the grid short of the target.
+inline int plan_splits(int ns, int hkv, int max_seq_len)
+{
+    if (max_seq_len <= 0) return 1;
+    const Variant v = kVariants[g_variant];
+    const int chunk = 16 * v.ng;
+    const int pairs = ns * hkv;
+    const int by_fill = (g_target_wgs + pairs - 1) / pairs;                  // fill the GPU
+    const int by_chunks = (max_seq_len + chunk - 1) / chunk;                 // >= 1 chunk per WG
+    const int by_waves = (max_seq_len + v.waves * chunk - 1) / (v.waves * chunk);  // <= 1 chunk per wave
+    int n = by_fill < by_chunks ? by_fill : by_chunks;
+    if (n < by_waves) n = by_waves;
+    if (n < 1) n = 1;
+    if (n > kMaxSplits) n = kMaxSplits;
+    return n;
+}
+
+}  // namespace decode_detail
+}  // namespace fp8kv
+
+using namespace fp8kv;
+using namespace fp8kv::decode_detail;
+
+extern "C" int fp8kv_decode_num_splits(int num_seqs, int num_kv_heads, int max_seq_len)
+{
+    if (num_seqs < 1 || num_kv_heads < 1) return 1;
+    return plan_splits(num_seqs, num_kv_heads, max_seq_len);
+}
+
+extern "C" size_t fp8kv_decode_scratch_bytes(int num_seqs, int num_q_heads, int num_kv_heads,
+                                             int head_size, int num_splits)
+{
+    if (num_seqs < 1 || num_kv_heads < 1 || num_q_heads < num_kv_heads || head_size != kD)
+        return 0;
+    return scratch_bytes(num_seqs, num_q_heads, num_kv_heads, num_splits);
+}
+
+extern "C" int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
+                                 const void* k_cache, const void* v_cache,
+                                 int64_t sk0, int64_t sk1, int64_t sk2,
+                                 int64_t sv0, int64_t sv1, int64_t sv2,
+                                 void* out, int64_t out_row_stride,
+                                 const int32_t* query_start_loc, const int32_t* seq_lens,
+                                 const int32_t* block_table, int64_t bt_stride,
+                                 const float* k_scale, const float* v_scale, float sm_scale,
+                                 int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
+                                 int block_size, int num_splits, void* scratch,
+                                 size_t scratch_bytes_given, void* stream)
+{
+    if (!q || !k_cache || !v_cache || !out || !query_start_loc || !seq_lens || !block_table ||
+        !k_scale || !v_scale)
+        return FP8KV_ERR_ARG;
+    if (num_seqs < 1 || num_kv_heads < 1 || num_q_heads < 1 || block_size < 1 || num_splits < 1 ||
+        num_splits > kMaxSplits || bt_stride < 0)
+        return FP8KV_ERR_ARG;
+    if (num_seqs > 65535 || num_kv_heads > 65535 || (int64_t)num_seqs * num_kv_heads > kMaxPairs)
+        return FP8KV_ERR_SHAPE;
+    if (head_size != kD || num_q_heads % num_kv_heads != 0) return FP8KV_ERR_SHAPE;
+    const int gqa = num_q_heads / num_kv_heads;
+    if (gqa > kMaxGqa || (block_size % 16) != 0) return FP8KV_ERR_SHAPE;
+    // K rows are read with 16-byte loads and V rows with 8-byte loads; q with 16-byte loads.
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 8) || !aligned(q, 16) || !aligned(out, 2))
+        return FP8KV_ERR_ALIGN;
+    if ((sk0 | sk1 | sk2) & 15) return FP8KV_ERR_ALIGN;
+    if ((sv0 | sv1 | sv2) & 7) return FP8KV_ERR_ALIGN;
+    if (q_row_stride & 7) return FP8KV_ERR_ALIGN;
+    // Per-lane offsets within a 16-token group are 32-bit.
+    if (sk1 < 0 || sv1 < 0 || sk1 > ((int64_t)1 << 26) || sv1 > ((int64_t)1 << 26)) return FP8KV_ERR_SHAPE;
+    const size_t need = scratch_bytes(num_seqs, num_q_heads, num_kv_heads, num_splits);
+    if (need > 0 && (!scratch || scratch_bytes_given < need || !aligned(scratch, 256)))
+        return FP8KV_ERR_SCRATCH;
+
+    Params P;
+    P.q = static_cast<const __bf16*>(q);
+    P.k = static_cast<const uint8_t*>(k_cache);
+    P.v = static_cast<const uint8_t*>(v_cache);
+    P.out = static_cast<__bf16*>(out);
+    P.qsl = query_start_loc;
+    P.seq_lens = seq_lens;
+    P.bt = block_table;
+    P.k_scale = k_scale;
+    P.v_scale = v_scale;
+    P.counters = static_cast<uint32_t*>(scratch);
+    P.part = need > 0 ? reinterpret_cast<float*>(static_cast<unsigned char*>(scratch) + counters_bytes())
+                      : nullptr;
+    P.q_stride = q_row_stride;
+    P.o_stride = out_row_stride;
+    P.bt_stride = bt_stride;
+    P.sk0 = sk0; P.sk1 = sk1; P.sk2 = sk2;
+    P.sv0 = sv0; P.sv1 = sv1; P.sv2 = sv2;
+    P.sm_scale = sm_scale;
+    P.hkv = num_kv_heads;
+    P.gqa = gqa;
+    P.pblk = block_size;
+    P.nsplit = num_splits;
+
+    const dim3 grid((unsigned)num_splits, (unsigned)num_kv_heads, (unsigned)num_seqs);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    switch (g_variant) {
+        case 1: hipLaunchKernelGGL((decode_kernel<8, 2, 1>), grid, dim3(8 * 64), 0, st, P); break;
+        case 2: hipLaunchKernelGGL((decode_kernel<4, 4, 1>), grid, dim3(4 * 64), 0, st, P); break;
+        case 3: hipLaunchKernelGGL((decode_kernel<4, 4, 2>), grid, dim3(4 * 64), 0, st, P); break;
+        default: hipLaunchKernelGGL((decode_kernel<8, 4, 1>), grid, dim3(8 * 64), 0, st, P); break;
+    }
+    return finish_launch();
+}
+
+extern "C" void fp8kv_decode_tune(int variant, int target_wgs)
+{
+    g_variant = (variant >= 0 && variant < kNumVariants) ? variant : 0;
+    g_target_wgs = target_wgs > 0 ? target_wgs : 256;
+}

@@ -51,16 +51,15 @@ __device__ __forceinline__ bf16x2_t fp8x2_to_bf16x2(uint32_t w) {
     return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
 }
 
-// Eight e4m3fn bytes (two dwords, byte order = element order) -> bf16x8.
+// Eight e4m3fn bytes (two dwords, byte order = element order) -> bf16x8, assembled from whole
+// dwords (element-wise 16-bit inserts would cost a register move per element).
 __device__ __forceinline__ bf16x8_t fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
-    bf16x2_t a = fp8x2_to_bf16x2<false>(lo);
-    bf16x2_t b = fp8x2_to_bf16x2<true>(lo);
-    bf16x2_t c = fp8x2_to_bf16x2<false>(hi);
-    bf16x2_t d = fp8x2_to_bf16x2<true>(hi);
-    bf16x8_t r;
-    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
-    r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
-    return r;
+    u32x4_t r;
+    r[0] = __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<false>(lo));
+    r[1] = __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<true>(lo));
+    r[2] = __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<false>(hi));
+    r[3] = __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<true>(hi));
+    return __builtin_bit_cast(bf16x8_t, r);
 }
 
 // f32 -> bf16 bits, round to nearest even (NaN stays NaN): v_cvt_pk_bf16_f32.

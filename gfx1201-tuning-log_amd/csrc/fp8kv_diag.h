@@ -15,6 +15,10 @@ int fp8kv_h4mv_audit(int N, int K, int M);
  * depth (0 and 0 = the built-in defaults).  Affects later launches and audits. */
 void fp8kv_h4mv_tune(int target_waves, int depth);
 
+/* Tuning hook for sweeps of the decode attention launch: waves per workgroup (4 or 8) and the
+ * workgroup count its split planner aims for (0 = default 512).  Affects later launches. */
+void fp8kv_decode_tune(int waves, int target_wgs);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,9 +25,16 @@ SIGNATURES: dict[str, tuple] = {
     "h4mv_launch": (None, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
     "h4mv_launch_status": (_c_i, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
     "h4mv_f32_launch_status": (_c_i, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
+    # paged fp8 decode attention (csrc/decode_attn.hip)
+    "fp8kv_decode_num_splits": (_c_i, [_c_i] * 3),
+    "fp8kv_decode_scratch_bytes": (_c_sz, [_c_i] * 5),
+    "fp8kv_decode_attn": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_i64] * 6 + [_c_vp, _c_i64]
+                          + [_c_vp] * 3 + [_c_i64] + [_c_vp] * 2 + [_c_f] + [_c_i] * 6
+                          + [_c_vp, _c_sz, _c_vp]),
     # host-only diagnostics (csrc/fp8kv_diag.h)
     "fp8kv_h4mv_audit": (_c_i, [_c_i] * 3),
     "fp8kv_h4mv_tune": (None, [_c_i] * 2),
+    "fp8kv_decode_tune": (None, [_c_i] * 2),
 }
 
 _lock = threading.Lock()

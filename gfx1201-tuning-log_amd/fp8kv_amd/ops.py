@@ -53,3 +53,106 @@ def h4mv(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor,
             _stream_ptr(x))
     _lib.check("h4mv_launch_status", st)
     return out
+
+
+# ------------------------------------------------------------------------------ decode attention
+
+_scratch_cache: dict = {}
+
+
+def decode_num_splits(num_seqs: int, num_kv_heads: int, max_seq_len: int) -> int:
+    return int(_lib.load().fp8kv_decode_num_splits(num_seqs, num_kv_heads, max_seq_len))
+
+
+def decode_scratch_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, num_splits: int,
+                         head_size: int = 128) -> int:
+    return int(_lib.load().fp8kv_decode_scratch_bytes(num_seqs, num_q_heads, num_kv_heads,
+                                                     head_size, num_splits))
+
+
+def decode_scratch(nbytes: int, device, allow_alloc: bool = True) -> torch.Tensor | None:
+    """Zero-filled scratch of at least ``nbytes`` for ``device``, reused across calls.
+
+    The kernel leaves the buffer ready for the next call, so it is zeroed only when allocated.
+    With ``allow_alloc=False`` (e.g. during graph capture) a too-small cache returns None.
+    """
+    if nbytes <= 0:
+        return None
+    dev = torch.device(device)
+    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+    buf = _scratch_cache.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if not allow_alloc:
+            return None
+        size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
+        buf = torch.zeros(size, dtype=torch.uint8, device=dev)
+        _scratch_cache[key] = buf
+    return buf
+
+
+def _scale_tensor(x, device) -> torch.Tensor:
+    if torch.is_tensor(x):
+        _require(x.dtype == torch.float32 and x.numel() >= 1 and x.device == device,
+                 "k/v scales must be fp32 device tensors")
+        return x
+    return torch.tensor([float(x)], dtype=torch.float32, device=device)
+
+
+def _fp8_cache_check(c: torch.Tensor, name: str) -> None:
+    _require(c.is_cuda and c.dim() == 4, f"{name} must be a 4-D device tensor [NB, PBLK, HKV, D]")
+    _require(c.dtype in (torch.float8_e4m3fn, torch.uint8), f"{name} must be float8_e4m3fn (or raw uint8)")
+    _require(c.stride(3) == 1, f"{name} must be contiguous along head_size")
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     out: torch.Tensor, query_start_loc: torch.Tensor, seq_lens: torch.Tensor,
+                     block_table: torch.Tensor, k_scale, v_scale, sm_scale: float,
+                     num_splits: int | None = None, max_seq_len: int | None = None,
+                     scratch: torch.Tensor | None = None) -> torch.Tensor:
+    """Paged fp8 decode attention; writes ``out[query_start_loc[s]]`` for every sequence s.
+
+    Contract of vllm-fp8kv/fp8kv_v3.py:116-139 (q [T, HQ, D] bf16, caches [NB, PBLK, HKV, D] fp8
+    views with arbitrary block/slot/head strides, int32 metadata, device fp32 scales).
+    ``num_splits`` defaults to the library's plan for ``max_seq_len`` (read from ``seq_lens`` when
+    not given, which synchronises).  ``scratch`` defaults to a per-device cached buffer.
+    """
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1
+             and q.stride(1) == q.shape[2], "q must be bf16 [T, HQ, D] with contiguous heads")
+    _require(out.dtype == torch.bfloat16 and out.dim() == 3 and out.stride(2) == 1
+             and out.stride(1) == out.shape[2] and out.shape[1:] == q.shape[1:],
+             "out must be bf16 [T, HQ, D] with contiguous heads")
+    _fp8_cache_check(k_cache, "k_cache")
+    _fp8_cache_check(v_cache, "v_cache")
+    for t, n in ((query_start_loc, "query_start_loc"), (seq_lens, "seq_lens"),
+                 (block_table, "block_table")):
+        _require(t.dtype == torch.int32 and t.is_cuda, f"{n} must be an int32 device tensor")
+    _require(block_table.dim() == 2 and block_table.stride(1) == 1, "block_table must be [NS, max_blocks]")
+    NS = block_table.shape[0]
+    HQ, D = q.shape[1], q.shape[2]
+    HKV = k_cache.shape[2]
+    PBLK = k_cache.shape[1]
+    dev = q.device
+    ks = _scale_tensor(k_scale, dev)
+    vs = _scale_tensor(v_scale, dev)
+    if num_splits is None:
+        if max_seq_len is None:
+            max_seq_len = int(seq_lens.max().item()) if NS > 0 else 0
+        num_splits = decode_num_splits(NS, HKV, int(max_seq_len))
+    need = decode_scratch_bytes(NS, HQ, HKV, num_splits, D)
+    if scratch is None:
+        scratch = decode_scratch(need, dev)
+    elif need > 0:
+        _require(scratch.is_cuda and scratch.numel() * scratch.element_size() >= need,
+                 f"scratch needs {need} bytes")
+    sbytes = 0 if scratch is None else scratch.numel() * scratch.element_size()
+    lib = _lib.load()
+    st = lib.fp8kv_decode_attn(
+        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
+        out.data_ptr(), out.stride(0), query_start_loc.data_ptr(), seq_lens.data_ptr(),
+        block_table.data_ptr(), block_table.stride(0), ks.data_ptr(), vs.data_ptr(),
+        float(sm_scale), NS, HQ, HKV, D, PBLK, int(num_splits),
+        None if scratch is None else scratch.data_ptr(), sbytes, _stream_ptr(q))
+    _lib.check("fp8kv_decode_attn", st)
+    return out

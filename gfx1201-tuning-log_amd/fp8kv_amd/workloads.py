@@ -5,7 +5,9 @@ machine; the bench's cache-defeating rotation copies are generated on the device
 
   * ``w4_case``      MXFP4 matvec: codes uniform over all 16 values (uniform bytes), e8m0 scale
                      bytes uniform in [119, 123] (2^-8 .. 2^-4), x ~ N(0,1) bf16.
-  * ``decode_case``  paged fp8 decode: K, V ~ N(0,1) quantised per tensor with scale amax/448,
+  * ``decode_case``  paged fp8 decode: K, V ~ N(0,1) quantised per tensor with scale amax/448
+                     (``kv_gen="ref"``: N(0,1) * 2 cast straight to e4m3 with scale 1, the
+                     reference's self-test data),
                      a pool of blocks handed out by a seeded permutation, one query per sequence.
   * ``prefill_case`` paged fp8 prefill, single sequence or varlen (cu_seqlens).
 Layouts: ``"standalone"`` caches are [NB, PBLK, HKV, D]; ``"engine"`` caches are views of one
@@ -37,11 +39,19 @@ def quantize_per_tensor(x: torch.Tensor):
     return q, scale
 
 
-def _make_cache(nb: int, pblk: int, hkv: int, d: int, g: torch.Generator, layout: str):
+def _make_cache(nb: int, pblk: int, hkv: int, d: int, g: torch.Generator, layout: str,
+                kv_gen: str = "amax"):
     k = torch.randn(nb, pblk, hkv, d, generator=g)
     v = torch.randn(nb, pblk, hkv, d, generator=g)
-    kq, ks = quantize_per_tensor(k)
-    vq, vs = quantize_per_tensor(v)
+    if kv_gen == "amax":
+        kq, ks = quantize_per_tensor(k)
+        vq, vs = quantize_per_tensor(v)
+    elif kv_gen == "ref":
+        # the reference's self-test data: N(0,1) * 2 cast straight to e4m3 (vllm-fp8kv/fp8kv_v3.py:150-151)
+        kq, ks = (k * 2).to(torch.float8_e4m3fn), 1.0
+        vq, vs = (v * 2).to(torch.float8_e4m3fn), 1.0
+    else:
+        raise ValueError(kv_gen)
     if layout == "standalone":
         return kq, vq, None, ks, vs
     if layout == "engine":
@@ -62,7 +72,7 @@ def engine_views(kv_cache: torch.Tensor, head_size: int):
 
 def decode_case(ctx_lens, HQ: int = 24, HKV: int = 4, D: int = 128, PBLK: int = 16,
                 pool_blocks: int | None = None, seed: int = 0, layout: str = "standalone",
-                contiguous_bt: bool = False):
+                contiguous_bt: bool = False, kv_gen: str = "amax"):
     ctx_lens = [int(c) for c in ctx_lens]
     NS = len(ctx_lens)
     need = [math.ceil(c / PBLK) for c in ctx_lens]
@@ -70,7 +80,7 @@ def decode_case(ctx_lens, HQ: int = 24, HKV: int = 4, D: int = 128, PBLK: int = 
         pool_blocks = max(1, sum(need))
     assert sum(need) <= pool_blocks, "pool too small"
     g = torch.Generator().manual_seed(seed)
-    kc, vc, kv, ks, vs = _make_cache(pool_blocks, PBLK, HKV, D, g, layout)
+    kc, vc, kv, ks, vs = _make_cache(pool_blocks, PBLK, HKV, D, g, layout, kv_gen)
     max_blocks = max(1, max(need))
     bt = torch.zeros(NS, max_blocks, dtype=torch.int32)
     ids = torch.arange(pool_blocks) if contiguous_bt else torch.randperm(pool_blocks, generator=g)
@@ -89,12 +99,12 @@ def decode_case(ctx_lens, HQ: int = 24, HKV: int = 4, D: int = 128, PBLK: int = 
 
 def prefill_case(qlens, q0s, HQ: int = 24, HKV: int = 4, D: int = 128, PBLK: int = 16,
                  pool_blocks: int | None = None, seed: int = 0, layout: str = "standalone",
-                 contiguous_bt: bool = False):
+                 contiguous_bt: bool = False, kv_gen: str = "amax"):
     """Packed varlen prefill: sequence s has qlens[s] new tokens after q0s[s] cached ones."""
     qlens = [int(x) for x in qlens]
     q0s = [int(x) for x in q0s]
     ctx = [a + b for a, b in zip(qlens, q0s)]
-    case = decode_case(ctx, HQ, HKV, D, PBLK, pool_blocks, seed, layout, contiguous_bt)
+    case = decode_case(ctx, HQ, HKV, D, PBLK, pool_blocks, seed, layout, contiguous_bt, kv_gen)
     g = torch.Generator().manual_seed(seed + 7919)
     T = sum(qlens)
     case["q"] = torch.randn(T, HQ, D, generator=g).to(torch.bfloat16)

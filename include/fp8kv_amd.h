@@ -61,6 +61,55 @@ int h4mv_launch_status(const void* W, const void* St, const void* Xb, void* Out,
 int h4mv_f32_launch_status(const void* W, const void* St, const void* Xb, void* Out,
                            int N, int K, int M, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Paged fp8-e4m3 KV decode attention (one query token per sequence, split-context, one launch).
+ *
+ *   out[qsl[s], h, :] = bf16( v_scale * softmax_t( q[qsl[s], h, :] . K_t * sm_scale * k_scale ) . V_t )
+ *   for t in [0, seq_lens[s]), h in [0, num_q_heads); query head h reads kv head h / (HQ / HKV).
+ *
+ *   q            bf16 [tokens, HQ, 128], row stride q_row_stride elements, heads contiguous (16 B aligned)
+ *   k_cache      fp8 e4m3fn bytes; element (block, slot, kv_head, d) at
+ *                k_cache + block*sk0 + slot*sk1 + kv_head*sk2 + d   (strides in bytes, multiples of 16)
+ *   v_cache      same with sv0..sv2 (multiples of 8).  Both the standalone [NB, PBLK, HKV, D] cache and the
+ *                engine's interleaved [NB, HKV, PBLK, 2D] tensor viewed as K | V halves are accepted.
+ *   out          bf16 [tokens, HQ, 128], row stride out_row_stride; only rows qsl[s] are written
+ *   query_start_loc int32 [NS + 1] (row of sequence s = query_start_loc[s]); seq_lens int32 [NS];
+ *   block_table  int32 [NS, bt_stride]; k_scale, v_scale fp32 device scalars (read on the device)
+ *   head_size == 128, HQ % HKV == 0, HQ / HKV <= 16, block_size % 16 == 0, 1 <= num_splits <= 256.
+ *   A sequence with seq_len 0 gets zeros.
+ *
+ * Scratch: fp8kv_decode_scratch_bytes() bytes (0 when num_splits == 1), 256-byte aligned.  It must be
+ * zero-filled once after allocation; every call leaves it ready for the next one (its per-sequence
+ * tickets return to zero).  Calls sharing one scratch buffer must not overlap in time.
+ *
+ * Replaces: vllm-fp8kv/fp8kv_v3.py:116-139, run(q, k_cache, v_cache, out, qsl, slens, bt, kscale,
+ * vscale, sm_scale, TILE, warps, stages, nsplit, scratch), which launches the Triton kernels
+ * _decode_attn_split (fp8kv_v3.py:3-80) and _decode_attn_reduce (fp8kv_v3.py:83-113) with the cache
+ * strides k_cache.stride(0..2) / v_cache.stride(0..2) and block-table stride bt.stride(0).
+ */
+int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
+                      const void* k_cache, const void* v_cache,
+                      int64_t sk0, int64_t sk1, int64_t sk2,
+                      int64_t sv0, int64_t sv1, int64_t sv2,
+                      void* out, int64_t out_row_stride,
+                      const int32_t* query_start_loc, const int32_t* seq_lens,
+                      const int32_t* block_table, int64_t bt_stride,
+                      const float* k_scale, const float* v_scale, float sm_scale,
+                      int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
+                      int block_size, int num_splits, void* scratch, size_t scratch_bytes,
+                      void* stream);
+
+/* Split count the library would choose for a batch whose longest context is max_seq_len
+ * (replaces the fixed NSPLIT = 8 of vllm-fp8kv/fp8kv_override.py:43).  Any value in [1, 256]
+ * gives the same result up to rounding; this one fills the GPU. */
+int fp8kv_decode_num_splits(int num_seqs, int num_kv_heads, int max_seq_len);
+
+/* Scratch bytes fp8kv_decode_attn needs for this geometry and split count (0 = none; 0 is also
+ * returned for a geometry the kernel rejects).  Replaces the scratch sizing of
+ * vllm-fp8kv/fp8kv_v3.py:121-124 and vllm-fp8kv/fp8kv_override.py:87-96. */
+size_t fp8kv_decode_scratch_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
+                                  int num_splits);
+
 #ifdef __cplusplus
 }
 #endif

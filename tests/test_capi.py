@@ -69,3 +69,36 @@ def test_loader_fails_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(FileNotFoundError):
         _lib.load()
+
+
+def _decode_args(**kw):
+    a = dict(q=A, qs=24 * 128, k=A, v=A, sk0=16 * 4 * 128, sk1=4 * 128, sk2=128, sv0=16 * 4 * 128,
+             sv1=4 * 128, sv2=128, out=A, os=24 * 128, qsl=A, sl=A, bt=A, bts=64, ks=A, vs=A,
+             sm=0.088, ns=8, hq=24, hkv=4, hd=128, pblk=16, nsplit=1, scr=None, scrb=0, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(q=0), 1), (dict(ns=0), 1), (dict(nsplit=0), 1), (dict(nsplit=257), 1),
+    (dict(hd=64), 2), (dict(hq=25), 2), (dict(hq=68, hkv=4), 2), (dict(pblk=8), 2),
+    (dict(k=A + 8), 3), (dict(sk1=4 * 128 + 8), 3), (dict(sv2=4), 3), (dict(qs=24 * 128 + 4), 3),
+    (dict(nsplit=8), 5), (dict(nsplit=8, scr=A, scrb=100), 5),
+])
+def test_decode_rejects_before_launch(lib, kw, code):
+    assert lib.fp8kv_decode_attn(*_decode_args(**kw)) == code
+
+
+def test_decode_scratch_sizing(lib):
+    assert lib.fp8kv_decode_scratch_bytes(8, 24, 4, 128, 1) == 0
+    b = lib.fp8kv_decode_scratch_bytes(8, 24, 4, 128, 8)
+    assert b == 65536 * 4 + 8 * 4 * 8 * 6 * 130 * 4
+    assert lib.fp8kv_decode_scratch_bytes(8, 24, 4, 64, 8) == 0
+
+
+def test_decode_split_planner(lib):
+    assert lib.fp8kv_decode_num_splits(8, 4, 4096) == 8       # b8@4k: one workgroup per CU
+    assert lib.fp8kv_decode_num_splits(8, 4, 0) == 1
+    for ns, hkv, ctx in [(1, 1, 100000), (64, 8, 8192), (1, 4, 17), (300, 8, 4096)]:
+        n = lib.fp8kv_decode_num_splits(ns, hkv, ctx)
+        assert 1 <= n <= 256
