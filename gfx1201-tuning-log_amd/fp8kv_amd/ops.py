@@ -156,3 +156,73 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
         None if scratch is None else scratch.data_ptr(), sbytes, _stream_ptr(q))
     _lib.check("fp8kv_decode_attn", st)
     return out
+
+
+# ------------------------------------------------------------------------------ prefill attention
+
+def _prefill_common(q, k_cache, v_cache, out, block_table):
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1
+             and q.stride(1) == q.shape[2], "q must be bf16 [T, HQ, D] with contiguous heads")
+    _require(out.dtype == torch.bfloat16 and out.dim() == 3 and out.stride(2) == 1
+             and out.stride(1) == out.shape[2] and out.shape[1:] == q.shape[1:],
+             "out must be bf16 [T, HQ, D] with contiguous heads")
+    _fp8_cache_check(k_cache, "k_cache")
+    _fp8_cache_check(v_cache, "v_cache")
+    _require(block_table.dtype == torch.int32 and block_table.is_cuda and block_table.dim() == 2
+             and block_table.stride(1) == 1, "block_table must be int32 [NS, max_blocks] on the device")
+
+
+def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      out: torch.Tensor, block_table: torch.Tensor, k_scale, v_scale,
+                      sm_scale: float, q0: int, qlen: int) -> torch.Tensor:
+    """Single-sequence causal prefill: query i of q[:qlen] is token q0 + i (sees keys <= q0 + i).
+
+    Contract of vllm-fp8kv/fp8kv_prefill.py:124-144 run(q, k_cache, v_cache, out, bt, kscale,
+    vscale, sm_scale, q0, qlen): block-table row 0 holds the sequence, scales are device fp32.
+    """
+    _prefill_common(q, k_cache, v_cache, out, block_table)
+    _require(0 <= qlen <= q.shape[0] and qlen <= out.shape[0] and q0 >= 0, "bad q0 / qlen")
+    dev = q.device
+    ks = _scale_tensor(k_scale, dev)
+    vs = _scale_tensor(v_scale, dev)
+    st = _lib.load().fp8kv_prefill_attn(
+        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
+        out.data_ptr(), out.stride(0), block_table.data_ptr(), block_table.stride(0),
+        ks.data_ptr(), vs.data_ptr(), float(sm_scale), q.shape[1], k_cache.shape[2], q.shape[2],
+        k_cache.shape[1], int(q0), int(qlen), _stream_ptr(q))
+    _lib.check("fp8kv_prefill_attn", st)
+    return out
+
+
+def prefill_attention_varlen(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                             out: torch.Tensor, cu_seqlens_q: torch.Tensor, seq_lens: torch.Tensor,
+                             block_table: torch.Tensor, k_scale, v_scale, sm_scale: float,
+                             max_query_len: int | None = None) -> torch.Tensor:
+    """Causal prefill of sequences packed along the token axis (vLLM varlen metadata).
+
+    Sequence s owns q rows cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1; its context has seq_lens[s]
+    tokens (new ones included), so its q0 is seq_lens[s] - qlen_s; block_table row s maps it.
+    ``max_query_len`` sizes the grid (read from ``cu_seqlens_q`` when not given, which syncs).
+    """
+    _prefill_common(q, k_cache, v_cache, out, block_table)
+    for t, n in ((cu_seqlens_q, "cu_seqlens_q"), (seq_lens, "seq_lens")):
+        _require(t.dtype == torch.int32 and t.is_cuda, f"{n} must be an int32 device tensor")
+    NS = block_table.shape[0]
+    _require(cu_seqlens_q.numel() == NS + 1 and seq_lens.numel() == NS, "metadata sizes differ")
+    if max_query_len is None:
+        max_query_len = int((cu_seqlens_q[1:] - cu_seqlens_q[:-1]).max().item()) if NS else 0
+    dev = q.device
+    ks = _scale_tensor(k_scale, dev)
+    vs = _scale_tensor(v_scale, dev)
+    st = _lib.load().fp8kv_prefill_attn_varlen(
+        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
+        out.data_ptr(), out.stride(0), cu_seqlens_q.data_ptr(), seq_lens.data_ptr(),
+        block_table.data_ptr(), block_table.stride(0), ks.data_ptr(), vs.data_ptr(),
+        float(sm_scale), NS, q.shape[1], k_cache.shape[2], q.shape[2], k_cache.shape[1],
+        int(max_query_len), _stream_ptr(q))
+    _lib.check("fp8kv_prefill_attn_varlen", st)
+    return out

@@ -110,6 +110,49 @@ int fp8kv_decode_num_splits(int num_seqs, int num_kv_heads, int max_seq_len);
 size_t fp8kv_decode_scratch_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
                                   int num_splits);
 
+/* ---------------------------------------------------------------------------------------------
+ * Paged fp8-e4m3 KV causal prefill attention, one sequence.
+ *
+ *   out[i, h, :] = bf16( v_scale * softmax_{t <= q0 + i}( q[i, h, :] . K_t * sm_scale * k_scale ) . V_t )
+ *   for i in [0, qlen): query i is token q0 + i of a sequence whose context (q0 + qlen tokens,
+ *   the new ones included) is mapped by block_table row 0.  Layouts, strides, scales and geometry
+ *   limits as for fp8kv_decode_attn (out additionally 16-byte aligned with row stride % 8 == 0).
+ *
+ * Replaces: vllm-fp8kv/fp8kv_prefill.py:124-144, run(q, k_cache, v_cache, out, bt, kscale, vscale,
+ * sm_scale, q0, qlen, BM, BN, warps, stages), the launch of the Triton kernel _prefill_attn
+ * (fp8kv_prefill.py:31-121).  Any GQA <= 16 is exact (the reference's row packing is not when GQA
+ * does not divide its BM).
+ */
+int fp8kv_prefill_attn(const void* q, int64_t q_row_stride,
+                       const void* k_cache, const void* v_cache,
+                       int64_t sk0, int64_t sk1, int64_t sk2,
+                       int64_t sv0, int64_t sv1, int64_t sv2,
+                       void* out, int64_t out_row_stride,
+                       const int32_t* block_table, int64_t bt_stride,
+                       const float* k_scale, const float* v_scale, float sm_scale,
+                       int num_q_heads, int num_kv_heads, int head_size, int block_size,
+                       int q0, int qlen, void* stream);
+
+/* Causal prefill of several sequences packed along the token axis (vLLM varlen metadata):
+ * sequence s owns q / out rows cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1 (device int32 [NS + 1]),
+ * its context is seq_lens[s] tokens (device int32 [NS], new tokens included), so its first query
+ * is token seq_lens[s] - qlen_s, and block_table row s maps it.  max_query_len (host) bounds the
+ * grid; sequences with no new tokens are skipped.
+ *
+ * Replaces: the multi-sequence prefill the reference leaves to vLLM's stock path (its hook gates on
+ * exactly one sequence, vllm-fp8kv/fp8kv_prefill.py:163, and falls through to
+ * TritonAttentionImpl.forward otherwise, :195-196). */
+int fp8kv_prefill_attn_varlen(const void* q, int64_t q_row_stride,
+                              const void* k_cache, const void* v_cache,
+                              int64_t sk0, int64_t sk1, int64_t sk2,
+                              int64_t sv0, int64_t sv1, int64_t sv2,
+                              void* out, int64_t out_row_stride,
+                              const int32_t* cu_seqlens_q, const int32_t* seq_lens,
+                              const int32_t* block_table, int64_t bt_stride,
+                              const float* k_scale, const float* v_scale, float sm_scale,
+                              int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
+                              int block_size, int max_query_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

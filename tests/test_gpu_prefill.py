@@ -1,0 +1,177 @@
+"""GPU parity of the paged fp8 causal prefill attention against the CPU oracle.
+
+Bar (BASELINE): bf16 output vs the oracle within rtol = atol = 1e-2 elementwise; the reference's
+own bar (max-abs < 0.05, vllm-fp8kv/prefill_test.py:49) is also checked on its data regime.
+Cases follow vllm-fp8kv/prefill_test.py:95-98 (first chunk, continuation, small tail, scales
+0.5 / 2.0) at the BASELINE head geometry (24/4) and at the reference's own (32/8), plus configs[3]
+(2048 new tokens over 2048 cached), varlen batches and every GQA the kernel plans for.
+"""
+import pytest
+import torch
+
+from fp8kv_amd import _lib, ops, workloads
+from oracle import attention
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+RTOL = ATOL = 1e-2
+
+
+def _run_single(c, q0, qlen, ks=None, vs=None, out=None):
+    d = workloads.to_device(c, DEV)
+    ks = c["k_scale"] if ks is None else ks
+    vs = c["v_scale"] if vs is None else vs
+    if out is None:
+        out = torch.zeros_like(d["q"])
+    ops.prefill_attention(d["q"], d["k_cache"], d["v_cache"], out, d["block_table"],
+                          torch.tensor([ks], device=DEV), torch.tensor([vs], device=DEV),
+                          c["sm_scale"], q0, qlen)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _oracle_single(c, q0, qlen, ks=None, vs=None, dtype=torch.float64):
+    ks = c["k_scale"] if ks is None else ks
+    vs = c["v_scale"] if vs is None else vs
+    return attention.prefill_attention(c["q"], c["k_cache"], c["v_cache"], c["block_table"][0],
+                                       ks, vs, c["sm_scale"], q0, qlen, dtype=dtype)
+
+
+def _check_single(qlen, q0, HQ=24, HKV=4, seed=0, ks=None, vs=None, layout="standalone",
+                  kv_gen="amax", PBLK=16, dtype=torch.float64):
+    c = workloads.prefill_case([qlen], [q0], HQ=HQ, HKV=HKV, PBLK=PBLK, seed=seed, layout=layout,
+                               kv_gen=kv_gen)
+    got = _run_single(c, q0, qlen, ks, vs)[:qlen].to(torch.float64)
+    ref = _oracle_single(c, q0, qlen, ks, vs, dtype).to(torch.float64)
+    torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
+    return (got - ref).abs().max().item(), c
+
+
+# --- vllm-fp8kv/prefill_test.py:95-98, on the reference's data regime (N(0,1)*2 cast to e4m3) ------
+
+@pytest.mark.parametrize("hq,hkv", [(24, 4), (32, 8)])
+@pytest.mark.parametrize("qlen,q0,ks,vs", [
+    (2048, 0, 1.0, 1.0),        # first chunk
+    (850, 2048, 1.0, 1.0),      # continuation, ctx 2898
+    (256, 3840, 1.0, 1.0),      # small tail
+    (512, 0, 0.5, 2.0),         # scales
+])
+def test_reference_cases(hq, hkv, qlen, q0, ks, vs):
+    err, _ = _check_single(qlen, q0, HQ=hq, HKV=hkv, seed=qlen + q0, ks=ks, vs=vs, kv_gen="ref",
+                           dtype=torch.float32 if qlen * (qlen + q0) > 3_000_000 else torch.float64)
+    assert err < 0.05
+
+
+def test_config3_2048_over_2048_cached():
+    """2048 query tokens after 2048 cached ones, 24/4 heads, engine cache layout."""
+    err, _ = _check_single(2048, 2048, seed=3, layout="engine", dtype=torch.float32)
+    print(f"cfg3 max-abs {err:.2e}")
+
+
+def test_first_row_is_v0():
+    """q0 = 0: query 0 sees key 0 only, so its output is v_scale * V_0 (rounded to bf16)."""
+    c = workloads.prefill_case([40], [0], seed=4)
+    got = _run_single(c, 0, 40, 1.0, 1.5)
+    blk = int(c["block_table"][0, 0])
+    for h in range(24):
+        v0 = (c["v_cache"][blk, 0, h // 6].to(torch.float64) * 1.5).to(torch.bfloat16)
+        assert torch.equal(got[0, h], v0)
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (16, 4), (20, 4), (32, 4), (64, 4), (28, 4)])
+def test_gqa_plans(hq, hkv):
+    """GQA 1, 2, 4, 5, 8, 16, 7: every (token blocks, row-sets per wave) plan of the kernel."""
+    _check_single(197, 61, HQ=hq, HKV=hkv, seed=hq)
+
+
+@pytest.mark.parametrize("qlen,q0", [(1, 0), (1, 5000), (15, 0), (16, 16), (17, 3), (31, 1),
+                                     (33, 32), (64, 0), (100, 31), (129, 4095)])
+def test_edge_lengths(qlen, q0):
+    _check_single(qlen, q0, seed=qlen * 7 + q0)
+
+
+def test_block_size_32_engine_layout():
+    _check_single(300, 77, PBLK=32, layout="engine", seed=8)
+
+
+def test_rows_beyond_qlen_untouched_and_deterministic():
+    c = workloads.prefill_case([120], [33], seed=9)
+    d = workloads.to_device(c, DEV)
+    T = d["q"].shape[0]
+    big = torch.full((T + 8, 24, 128), 5.0, dtype=torch.bfloat16, device=DEV)
+    out = big[:T]
+    ks = torch.tensor([c["k_scale"]], device=DEV)
+    vs = torch.tensor([c["v_scale"]], device=DEV)
+    ops.prefill_attention(d["q"], d["k_cache"], d["v_cache"], out, d["block_table"], ks, vs,
+                          c["sm_scale"], 33, 100)                  # only the first 100 rows
+    a = big.clone()
+    ops.prefill_attention(d["q"], d["k_cache"], d["v_cache"], out, d["block_table"], ks, vs,
+                          c["sm_scale"], 33, 100)
+    torch.cuda.synchronize()
+    assert torch.equal(a, big)
+    assert torch.all(big[100:] == 5.0)
+    ref = _oracle_single(c, 33, 100)
+    torch.testing.assert_close(big[:100].cpu().to(torch.float64), ref, rtol=RTOL, atol=ATOL)
+
+
+# --- varlen -------------------------------------------------------------------------------------
+
+def _check_varlen(qlens, q0s, seed, HQ=24, HKV=4, layout="standalone", dtype=torch.float64):
+    c = workloads.prefill_case(qlens, q0s, HQ=HQ, HKV=HKV, seed=seed, layout=layout)
+    d = workloads.to_device(c, DEV)
+    out = torch.full_like(d["q"], 7.0)
+    ops.prefill_attention_varlen(d["q"], d["k_cache"], d["v_cache"], out, d["cu_seqlens_q"],
+                                 d["seq_lens"], d["block_table"],
+                                 torch.tensor([c["k_scale"]], device=DEV),
+                                 torch.tensor([c["v_scale"]], device=DEV), c["sm_scale"])
+    torch.cuda.synchronize()
+    ref = attention.varlen_prefill_attention(c["q"], c["k_cache"], c["v_cache"], c["cu_seqlens_q"],
+                                             c["seq_lens"], c["block_table"], c["k_scale"],
+                                             c["v_scale"], c["sm_scale"], dtype=dtype)
+    torch.testing.assert_close(out.cpu().to(torch.float64), ref.to(torch.float64), rtol=RTOL, atol=ATOL)
+
+
+def test_config3_varlen_4x512():
+    """configs[3] varlen variant: 4 sequences of 512 new tokens (q0 = 0 each)."""
+    _check_varlen([512] * 4, [0] * 4, seed=10, layout="engine")
+
+
+def test_varlen_mixed_offsets():
+    _check_varlen([5, 100, 33, 512, 1], [0, 7, 1000, 3, 250], seed=11)
+
+
+def test_varlen_equals_single_runs():
+    qlens, q0s = [70, 130, 16], [10, 0, 300]
+    c = workloads.prefill_case(qlens, q0s, seed=12)
+    d = workloads.to_device(c, DEV)
+    ks = torch.tensor([c["k_scale"]], device=DEV)
+    vs = torch.tensor([c["v_scale"]], device=DEV)
+    out = torch.zeros_like(d["q"])
+    ops.prefill_attention_varlen(d["q"], d["k_cache"], d["v_cache"], out, d["cu_seqlens_q"],
+                                 d["seq_lens"], d["block_table"], ks, vs, c["sm_scale"])
+    cu = c["cu_seqlens_q"].tolist()
+    for s in range(3):
+        single = torch.zeros_like(d["q"][cu[s]:cu[s + 1]])
+        ops.prefill_attention(d["q"][cu[s]:cu[s + 1]], d["k_cache"], d["v_cache"], single,
+                              d["block_table"][s:s + 1], ks, vs, c["sm_scale"], q0s[s], qlens[s])
+        torch.cuda.synchronize()
+        assert torch.equal(single, out[cu[s]:cu[s + 1]])
+
+
+def test_rejects_bad_arguments():
+    c = workloads.prefill_case([16], [0], seed=13)
+    d = workloads.to_device(c, DEV)
+    out = torch.zeros_like(d["q"])
+    lib = _lib.load()
+    st = lib.fp8kv_prefill_attn(d["q"].data_ptr(), d["q"].stride(0), d["k_cache"].data_ptr(),
+                                d["v_cache"].data_ptr(), *d["k_cache"].stride()[:3],
+                                *d["v_cache"].stride()[:3], out.data_ptr(), out.stride(0),
+                                d["block_table"].data_ptr(), d["block_table"].stride(0), None, None,
+                                0.1, 24, 4, 128, 16, 0, 16, None)
+    assert st == 1                                     # null scales
+    st = lib.fp8kv_prefill_attn(d["q"].data_ptr(), d["q"].stride(0), d["k_cache"].data_ptr(),
+                                d["v_cache"].data_ptr(), *d["k_cache"].stride()[:3],
+                                *d["v_cache"].stride()[:3], out.data_ptr(), out.stride(0),
+                                d["block_table"].data_ptr(), d["block_table"].stride(0),
+                                d["q"].data_ptr(), d["q"].data_ptr(), 0.1, 24, 5, 128, 16, 0, 16, None)
+    assert st == 2                                     # HQ % HKV != 0
