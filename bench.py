@@ -30,6 +30,7 @@ sys.path.insert(0, os.path.join(REPO, "gfx1201-tuning-log_amd"))
 sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0 # MI355X dense bf16 MFMA
 ROTATE_BYTES = 1 << 30         # >= 4x the 256 MB MALL
 METRIC = "µs/layer + achieved HBM GB/s (%roofline): decode attn b8@4k, W4 GEMV M=1"
 
@@ -151,6 +152,57 @@ def bench_decode(ctx, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK=16, poo
     return r
 
 
+def prefill_flops(qlens, q0s, HQ: int, D: int) -> int:
+    """Algorithmic FLOPs of causal prefill: 4 D HQ per visible (query, key) pair."""
+    pairs = sum(sum(q0 + i + 1 for i in range(n)) for n, q0 in zip(qlens, q0s))
+    return 4 * D * HQ * pairs
+
+
+def bench_prefill(qlens, q0s, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK=16, seed=0):
+    """Causal prefill (single sequence or varlen) on an engine-layout cache."""
+    import torch
+    from fp8kv_amd import ops, workloads
+    dev = torch.device("cuda")
+    NS = len(qlens)
+    ctx = [a + b for a, b in zip(qlens, q0s)]
+    need = [math.ceil(c / PBLK) for c in ctx]
+    nb = sum(need)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    kv = torch.randint(0, 256, (nb, HKV, PBLK, 2 * D), dtype=torch.uint8, device=dev, generator=g)
+    kv[(kv & 0x7F) == 0x7F] = 0x3C
+    kc, vc = workloads.engine_views(kv, D)
+    gc = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(nb, generator=gc)
+    bt = torch.zeros(NS, max(need), dtype=torch.int32)
+    o = 0
+    for s, n in enumerate(need):
+        bt[s, :n] = perm[o:o + n].to(torch.int32)
+        o += n
+    bt = bt.to(dev)
+    T = sum(qlens)
+    q = torch.randn(T, HQ, D, generator=gc).to(torch.bfloat16).to(dev)
+    out = torch.empty_like(q)
+    ks = torch.tensor([0.02], device=dev)
+    vs = torch.tensor([0.02], device=dev)
+    cu = torch.tensor([0] + list(torch.tensor(qlens).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+    sl = torch.tensor(ctx, dtype=torch.int32, device=dev)
+
+    if NS == 1:
+        def launch(i):
+            ops.prefill_attention(q, kc, vc, out, bt, ks, vs, 1 / math.sqrt(D), q0s[0], qlens[0])
+    else:
+        def launch(i):
+            ops.prefill_attention_varlen(q, kc, vc, out, cu, sl, bt, ks, vs, 1 / math.sqrt(D),
+                                         max_query_len=max(qlens))
+
+    wall, per = time_launches(launch, 1, steps, warmup)
+    fl = prefill_flops(qlens, q0s, HQ, D)
+    k_us = statistics.mean(per) * 1e3
+    return {"us_step": round(wall * 1e3, 3), "us_kernel": round(k_us, 3),
+            "flops": fl, "TFLOPs_kernel": round(fl / (k_us * 1e-6) / 1e12, 2),
+            "frac_kernel": round(fl / (k_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
 def cpu_baseline_w4(N: int, K: int, budget_s: float = 15.0):
     """Oracle-style torch CPU fp32 dequant + GEMV at M=1 on the full cfg1 shape."""
     import torch
@@ -206,8 +258,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--legs", default="w4,decode",
-                    help="comma list of legs to run (w4, decode)")
+    ap.add_argument("--legs", default="w4,decode,prefill",
+                    help="comma list of legs to run (w4, decode, prefill)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one GPU; "
@@ -234,6 +286,11 @@ def main():
         ctx2 = torch.randint(1024, 4097, (8,), generator=g).tolist()
         legs["decode_cfg2"] = bench_decode(ctx2, args.steps, args.warmup, seed=2)
         legs["decode_cfg2"]["ctx"] = ctx2
+    if "prefill" in legs_wanted:
+        pf_steps = max(5, args.steps // 4)
+        legs["prefill_cfg3"] = bench_prefill([2048], [2048], pf_steps, max(2, args.warmup // 4))
+        legs["prefill_cfg3_varlen_4x512"] = bench_prefill([512] * 4, [0] * 4, pf_steps,
+                                                          max(2, args.warmup // 4), seed=1)
     cpu = None if (args.no_cpu_baseline or m1 is None) else cpu_baseline_w4(N, K)
     head = m1 if m1 is not None else dec
     line = {
@@ -257,6 +314,11 @@ def main():
         "cpu_baseline": cpu,
         "legs": legs,
     }
+    if "prefill_cfg3" in legs:
+        pf = legs["prefill_cfg3"]
+        line["roofline_prefill_cfg3"] = {"bound": "mfma", "achieved": pf["TFLOPs_kernel"],
+                                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                         "frac": pf["frac_kernel"], "traffic": None}
     if dec is not None:
         line["roofline_decode_b8_4k"] = {"bound": "hbm", "achieved": dec["GBps_kernel"],
                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",

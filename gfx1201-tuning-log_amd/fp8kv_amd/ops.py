@@ -79,7 +79,10 @@ def decode_scratch(nbytes: int, device, allow_alloc: bool = True) -> torch.Tenso
     if nbytes <= 0:
         return None
     dev = torch.device(device)
-    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+    idx = dev.index
+    if idx is None:
+        idx = torch.cuda.current_device() if dev.type == "cuda" else 0
+    key = (dev.type, idx)
     buf = _scratch_cache.get(key)
     if buf is None or buf.numel() < nbytes:
         if not allow_alloc:

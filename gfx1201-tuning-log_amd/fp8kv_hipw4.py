@@ -1,0 +1,164 @@
+"""Route small-M MXFP4 linear layers through the gfx950 matvec (vLLM op-level hook).
+
+Drop-in for h4mv/fp8kv_hipw4.py.  With FP8KV_HIPW4=1, importing this module starts a poller
+thread (fp8kv_hipw4.py:45-58, 98) that waits for the engine's ``radiance_mxfp4`` module, stands
+down when ``radiance_mxfp4.WPERM`` is set (:50-52), steals the current CUDA body of
+``radiance::mxfp4_linear`` - ``_backend_fns["cuda"]`` or ``_init_fn`` (:54); calling the module
+attribute instead would recurse - and re-registers the op's CUDA implementation (:62).  The new
+implementation takes the fast path when the reference's gate holds (:70-76): x is a contiguous
+2-D bf16 tensor with 1 <= M <= FP8KV_HIPW4_MAX_M (default 4; the kernel accepts up to 16),
+K % 32 == 0, N >= 8, weight_scale has K / 32 rows and the weight pointer is 16-byte aligned.  It
+then repacks weight_scale [K/32, N] -> [N, K/32] once per tensor (cached by data pointer and
+shape, cache cleared above 512 entries, never during graph capture: :32-43) and calls
+``h4mv_launch`` of libfp8kv_amd.so through ctypes with the reference's exact binding (:21-23,
+81-83), returning a fresh bf16 [M, N] tensor (bias is applied outside, :9-10).  Anything else,
+or any exception, runs the stolen body (:91-94).
+
+The library path is FP8KV_AMD_LIB if set, else the in-tree build (the reference hard-codes
+/opt/fp8kv/libh4mv.so).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+import threading
+import time
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+if _PKG not in sys.path:
+    sys.path.insert(0, _PKG)
+
+TAG = "[hipw4]"
+STATS = {"fast": 0, "slow": 0, "logged": False, "calls": 0}
+_STATE = {"installed": False, "body": None, "patched": None}
+
+
+def _log(msg: str) -> None:
+    sys.stderr.write(f"{TAG} {msg}\n")
+
+
+def load_launcher(path: str | None = None):
+    """ctypes handle of ``h4mv_launch`` bound exactly as the reference binds it."""
+    if path is None:
+        from fp8kv_amd import _lib
+        path = _lib.lib_path()
+    lib = ctypes.CDLL(path)
+    lib.h4mv_launch.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
+    lib.h4mv_launch.restype = None
+    return lib.h4mv_launch
+
+
+class ScaleRepack:
+    """weight_scale [K/32, N] -> contiguous [N, K/32], cached by (data_ptr, shape)."""
+
+    def __init__(self, is_capturing, limit: int = 512):
+        self.cache: dict = {}
+        self.is_capturing = is_capturing
+        self.limit = limit
+
+    def __call__(self, s):
+        key = (s.data_ptr(), tuple(s.shape))
+        ent = self.cache.get(key)
+        if ent is not None:
+            return ent
+        if self.is_capturing():
+            return None                      # never allocate or launch helper work during capture
+        st = s.t().contiguous()
+        if len(self.cache) > self.limit:
+            self.cache.clear()
+        self.cache[key] = st
+        return st
+
+
+def fast_path_ok(x, weight, weight_scale, maxm: int, torch) -> bool:
+    """The reference's gate (h4mv/fp8kv_hipw4.py:70-76)."""
+    if not (torch.is_tensor(x) and x.dim() == 2 and x.is_contiguous()
+            and 1 <= x.shape[0] <= maxm and x.dtype == torch.bfloat16):
+        return False
+    N = weight.shape[0]
+    K = weight.shape[1] * 2
+    return (K % 32 == 0 and N >= 8 and weight_scale.shape[0] == K // 32
+            and weight.data_ptr() % 16 == 0)
+
+
+def make_patched(body, launch, repack, maxm: int, torch, stream_ptr):
+    """The replacement op body: fast path through ``launch`` (h4mv_launch), else ``body``."""
+
+    def _patched(x, weight, weight_scale, wref):
+        try:
+            if STATS["calls"] < 3:
+                STATS["calls"] += 1
+                _log(f"call#{STATS['calls']} x={tuple(x.shape)}/{x.dtype}/c={x.is_contiguous()} "
+                     f"w={tuple(weight.shape)}/{weight.dtype} s={tuple(weight_scale.shape)}")
+            if fast_path_ok(x, weight, weight_scale, maxm, torch):
+                st = repack(weight_scale)
+                if st is not None:
+                    M, N, K = x.shape[0], weight.shape[0], weight.shape[1] * 2
+                    out = torch.empty((M, N), device=x.device, dtype=torch.bfloat16)
+                    launch(weight.data_ptr(), st.data_ptr(), x.data_ptr(), out.data_ptr(), N, K, M,
+                           ctypes.c_void_p(stream_ptr()))
+                    STATS["fast"] += 1
+                    if not STATS["logged"]:
+                        STATS["logged"] = True
+                        _log(f"ENGAGED N={N} K={K} M={M} (x={tuple(x.shape)} w={tuple(weight.shape)} "
+                             f"s={tuple(weight_scale.shape)})")
+                    return out
+        except Exception as e:
+            _log(f"fast path failed ({e!r}), falling back")
+        STATS["slow"] += 1
+        return body(x, weight, weight_scale, wref)
+
+    return _patched
+
+
+def steal_body(rm):
+    """The op's current CUDA body, taken before re-registering (h4mv/fp8kv_hipw4.py:53-54)."""
+    f = rm.mxfp4_linear
+    return f._backend_fns.get("cuda") or f._init_fn
+
+
+def register(patched, torch):
+    torch.library.impl("radiance::mxfp4_linear", "CUDA")(patched)
+
+
+def _poll(launch, maxm, tries: int = 1500, delay: float = 0.2):
+    import torch
+    body = None
+    for _ in range(tries):
+        try:
+            import radiance_mxfp4 as rm
+            if getattr(rm, "WPERM", False):
+                _log("WPERM=1, standing down")
+                return
+            body = steal_body(rm)
+            break
+        except Exception:
+            time.sleep(delay)
+    if body is None:
+        _log("radiance module never appeared")
+        return
+    repack = ScaleRepack(torch.cuda.is_current_stream_capturing)
+    patched = make_patched(body, launch, repack, maxm, torch,
+                           lambda: torch.cuda.current_stream().cuda_stream)
+    register(patched, torch)
+    _STATE.update(body=body, patched=patched)
+    _log("op impl overridden")
+
+
+def _install() -> bool:
+    if os.environ.get("FP8KV_HIPW4", "0") != "1":
+        return False
+    try:
+        launch = load_launcher()
+    except Exception as e:
+        _log(f"lib load fail: {e}")
+        return False
+    maxm = int(os.environ.get("FP8KV_HIPW4_MAX_M", "4"))
+    threading.Thread(target=_poll, args=(launch, maxm), daemon=True).start()
+    _STATE["installed"] = True
+    _log("installed")
+    return True
+
+
+_install()

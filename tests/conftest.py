@@ -3,6 +3,9 @@ import sys
 
 import pytest
 
+# the decode hook's 15-second counter thread stays quiet under test
+os.environ.setdefault("FP8KV_OVERRIDE_COUNTERS", "0")
+
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG_DIR = os.path.join(REPO, "gfx1201-tuning-log_amd")
 for p in (REPO, PKG_DIR):
