@@ -6,6 +6,29 @@ namespace fp8kv {
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
+// Reductions over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the k-parts of one MFMA column) with
+// the gfx950 lane swaps: v_permlane16_swap_b32 on (x, x) hands every lane the values of lanes
+// l & ~16 and l | 16, v_permlane32_swap_b32 those of lanes l & ~32 and l | 32.  Pure VALU, no LDS
+// round trip; every lane gets the bitwise-identical result.
+__device__ __forceinline__ float max_xor16_32(float v)
+{
+    const uint32_t b = __float_as_uint(v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    const float m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const uint32_t c = __float_as_uint(m);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+__device__ __forceinline__ float sum_xor16_32(float v)
+{
+    const uint32_t b = __float_as_uint(v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    const float m = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const uint32_t c = __float_as_uint(m);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
 __device__ __forceinline__ uint32_t bf16x2_bits(bf16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
 // Device-coherent (agent-scope) accesses for the cross-workgroup partial records: they bypass the

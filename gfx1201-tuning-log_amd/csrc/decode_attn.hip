@@ -65,7 +65,7 @@ struct Params {
     int64_t q_stride, o_stride, bt_stride;
     int64_t sk0, sk1, sk2, sv0, sv1, sv2;
     float sm_scale;
-    int hkv, gqa, pblk, nsplit;
+    int hkv, gqa, pblk, pshift, nsplit;
 };
 
 __host__ __device__ inline int record_floats(int gqa) { return gqa * (kD + 2); }
@@ -107,7 +107,7 @@ __device__ __forceinline__ int load_block_ids(const Params& P, const int32_t* bt
 {
     constexpr int CPB = 64 / NG;
     const int t0 = first + stride * (CPB * batch + lane / NG) + 16 * (lane % NG);
-    return t0 < hi ? btrow[t0 / P.pblk] : 0;
+    return t0 < hi ? btrow[t0 >> P.pshift] : 0;
 }
 
 // Per-lane byte offsets of the chunk loads within one 16-token group (32-bit: the host rejects
@@ -141,7 +141,7 @@ __device__ __forceinline__ void issue_chunk(ChunkRegs<NG>& c, const Params& P, c
         const int t0 = c0 + 16 * g;
         if (t0 < hi) {
             const int64_t blk = __builtin_amdgcn_readlane(bids, NG * kb_idx + g);
-            const int slot0 = t0 % P.pblk;
+            const int slot0 = t0 & (P.pblk - 1);
             const uint8_t* kb = P.k + blk * P.sk0 + (int64_t)slot0 * P.sk1 + (int64_t)kh * P.sk2;
             const uint8_t* vb = P.v + blk * P.sv0 + (int64_t)slot0 * P.sv1 + (int64_t)kh * P.sv2;
             if (t0 + 16 <= hi) {
@@ -207,8 +207,7 @@ __device__ __forceinline__ void consume_chunk(const ChunkRegs<NG>& c, WaveState&
                 mc = fmaxf(mc, x);
             }
     }
-    mc = fmaxf(mc, __shfl_xor(mc, 16));
-    mc = fmaxf(mc, __shfl_xor(mc, 32));
+    mc = max_xor16_32(mc);
     const float m_new = fmaxf(st.m_run, mc);
     const float m_use = m_new == neg_inf() ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(st.m_run - m_use);
@@ -335,8 +334,7 @@ decode_kernel(Params P)
 
     // ---- merge the W waves in LDS ---------------------------------------------------------------
     float l_run = st.l_run;
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = sum_xor16_32(l_run);
     if (lp == 0 && lr < gqa) {
         lds_ml[wave][lr][0] = st.m_run;
         lds_ml[wave][lr][1] = l_run;
@@ -551,7 +549,8 @@ extern "C" int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
         return FP8KV_ERR_SHAPE;
     if (head_size != kD || num_q_heads % num_kv_heads != 0) return FP8KV_ERR_SHAPE;
     const int gqa = num_q_heads / num_kv_heads;
-    if (gqa > kMaxGqa || (block_size % 16) != 0) return FP8KV_ERR_SHAPE;
+    if (gqa > kMaxGqa) return FP8KV_ERR_SHAPE;
+    if (block_size < 16 || (block_size & (block_size - 1)) != 0) return FP8KV_ERR_SHAPE;
     // K rows are read with 16-byte loads and V rows with 8-byte loads; q with 16-byte loads.
     if (!aligned(k_cache, 16) || !aligned(v_cache, 8) || !aligned(q, 16) || !aligned(out, 2))
         return FP8KV_ERR_ALIGN;
@@ -586,10 +585,12 @@ extern "C" int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
     P.hkv = num_kv_heads;
     P.gqa = gqa;
     P.pblk = block_size;
+    P.pshift = __builtin_ctz((unsigned)block_size);
     P.nsplit = num_splits;
 
     const dim3 grid((unsigned)num_splits, (unsigned)num_kv_heads, (unsigned)num_seqs);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    begin_launch();
     switch (g_variant) {
         case 1: hipLaunchKernelGGL((decode_kernel<8, 2, 1>), grid, dim3(8 * 64), 0, st, P); break;
         case 2: hipLaunchKernelGGL((decode_kernel<4, 4, 1>), grid, dim3(4 * 64), 0, st, P); break;

@@ -19,6 +19,10 @@ void fp8kv_h4mv_tune(int target_waves, int depth);
  * workgroup count its split planner aims for (0 = default 512).  Affects later launches. */
 void fp8kv_decode_tune(int waves, int target_wgs);
 
+/* Tuning hook for sweeps of the prefill attention launch: index of the (waves, row-sets per wave,
+ * LDS ring depth) shape to use for every GQA, or -1 for the per-GQA default. */
+void fp8kv_prefill_tune(int shape);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,9 +10,18 @@ namespace fp8kv {
 // reference's void signature, so callers that want the error ask for it afterwards).
 extern thread_local int g_last_status;
 
+// HIP error code behind the last FP8KV_ERR_LAUNCH on this host thread.
+extern thread_local int g_last_hip_error;
+
+// Clear an error left by earlier, unrelated HIP calls so that finish_launch() reports only the
+// launch that follows.
+inline void begin_launch() { (void)hipGetLastError(); }
+
 inline int finish_launch() {
     hipError_t e = hipGetLastError();
-    return e == hipSuccess ? FP8KV_OK : FP8KV_ERR_LAUNCH;
+    if (e == hipSuccess) return FP8KV_OK;
+    g_last_hip_error = (int)e;
+    return FP8KV_ERR_LAUNCH;
 }
 
 __host__ __device__ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }

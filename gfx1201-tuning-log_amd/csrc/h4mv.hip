@@ -31,6 +31,7 @@
 namespace fp8kv {
 
 thread_local int g_last_status = FP8KV_OK;
+thread_local int g_last_hip_error = 0;
 
 namespace h4mv_detail {
 
@@ -544,6 +545,7 @@ int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N,
     if (M > 16 || (K & 31) != 0) return FP8KV_ERR_SHAPE;
     if (!aligned(W, 16) || !aligned(Xb, 16) || !aligned(Out, sizeof(OutT))) return FP8KV_ERR_ALIGN;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    begin_launch();
     StreamPlan p;
     if (aligned(St, 4) && stream_plan(N, K, M, p)) {
         launch_stream_m<OutT>(p, W, St, Xb, Out, N, K, M, s);
@@ -667,6 +669,13 @@ extern "C" void h4mv_launch(const void* W, const void* St, const void* Xb, void*
 }
 
 extern "C" int fp8kv_last_status(void) { return fp8kv::g_last_status; }
+
+extern "C" int fp8kv_last_hip_error(void) { return fp8kv::g_last_hip_error; }
+
+extern "C" const char* fp8kv_last_hip_error_string(void)
+{
+    return hipGetErrorString(static_cast<hipError_t>(fp8kv::g_last_hip_error));
+}
 
 extern "C" const char* fp8kv_status_string(int status)
 {

@@ -13,41 +13,39 @@
 //     gives every 16-row MFMA set a single head and 16 consecutive tokens instead.
 //
 // gfx950 design:
-//   * grid (token blocks, HKV, sequences), token blocks in reverse order so the longest causal rows
-//     start first; a workgroup (4 waves) owns 16 * nb query tokens of all GQA heads of one KV
-//     head: nb * GQA row-sets of 16 rows, row-set r = (head r % GQA, token block r / GQA), wave w
-//     taking r = w, w + 4, ... (RS row-sets at most).
-//   * keys are walked in 32-key tiles; each tile is loaded once per workgroup from the paged fp8
-//     cache (global -> registers one tile ahead), converted to bf16 and written to LDS in the
-//     layouts the MFMA fragments are read in:
-//       K  [32 keys][128 d] bf16, 16-byte chunk c of key r stored at chunk c ^ (r & 15), so the 16
-//          keys of one fragment read hit distinct banks;
-//       V^T [128 d][32 keys] bf16 (rows padded to 80 bytes), keys permuted into the k-slot order of
-//          the P^T fragments, transposed in registers during the conversion.
-//     LDS is double-buffered: one barrier per tile.
+//   * 1-D grid over (token-block rank, kv head) per sequence.  A workgroup of W waves owns nb
+//     16-token blocks of all GQA heads of one kv head: nb * GQA row-sets of 16 rows, row-set r =
+//     (head r % GQA, block r / GQA), wave w taking r = w, w + W, ... (RS at most).  With `paired`
+//     the two blocks are r and n16 - 1 - r, so every workgroup has the same causal work; otherwise
+//     ranks start from the longest causal rows.  Workgroups are spread so that each XCD's L2
+//     serves one kv head (dispatch is round-robin over the 8 XCDs).
+//   * keys are walked in 32-key tiles.  Raw fp8 K and V rows stream from the paged cache into an
+//     LDS ring R tiles deep with global_load_lds_dwordx4 (block id per copy instruction from a
+//     register via readlane), placed so that the fragment reads are bank-conflict free; each
+//     wave waits only for its own copies (explicit vmcnt) and one LDS-only barrier per tile
+//     publishes the tile.
+//   * every wave widens its fragments itself: K with v_cvt_scalef32_pk_bf16_fp8, V with the
+//     in-register 8 x 8 byte transpose shared with the decode kernel.
 //   * S^T = K . Q^T and O^T = V^T . P^T on v_mfma_f32_16x16x32_bf16 (the decode kernel's
 //     formulation): the query token stays in lane % 16 in S and O, so the online-softmax rescale is
-//     lane-local; K and V fragments are read once per tile and shared by the wave's row-sets.
+//     lane-local, and the row max reduces over the four k-parts with lane swaps.  The rescale is
+//     lazy: accumulators move to a new reference max only when it grows by more than 2^8.
 //   * the causal mask is applied only on diagonal tiles; tiles entirely above a row-set's diagonal
 //     are skipped for that row-set.
 #include "fp8kv_common.h"
 #include "fp8kv_status.h"
 #include "attn_common.h"
+#include "fp8kv_diag.h"
 
 namespace fp8kv {
 namespace prefill_detail {
 
 constexpr int kD = 128;
 constexpr int kBN = 32;                       // keys per tile
-constexpr int kWaves = 4;
-constexpr int kT = kWaves * 64;
 constexpr int kMaxGqa = 16;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kKRow = 256;                    // bytes per bf16 K row
-constexpr int kKTile = kBN * kKRow;           // 8 KB
-constexpr int kVRow = 80;                     // bytes per V^T row: 32 bf16 keys + 16 bytes of pad
-constexpr int kVTile = kD * kVRow;            // 10 KB
-constexpr int kBuf = kKTile + kVTile;
+constexpr float kRescaleSlack = 8.f;          // log2 growth of a row max tolerated before rescaling
+constexpr int kTileBytes = 8192;              // raw fp8 tile: K rows 0..31 (4 KB), then V rows (4 KB)
 
 struct Params {
     const __bf16* q;
@@ -62,88 +60,144 @@ struct Params {
     int64_t q_stride, o_stride, bt_stride;
     int64_t sk0, sk1, sk2, sv0, sv1, sv2;
     float sm_scale;
-    int hkv, gqa, pblk, nb;
+    int hkv, gqa, pblk, pshift, nb;
+    int paired;                 // 1: nb == 2 and the two 16-token blocks are r and n16 - 1 - r
+    int ntb_grid;               // token blocks per (sequence, kv head) the grid covers
+    int xcd_map;                // 1: kv head from the XCD index (8 % HKV == 0), see kernel
     int q0_host, qlen_host;
 };
 
-// Fragment chunk (16 bytes = 8 d) read by k-part p for QK step s: d = 16p + 8s (s < 2) and
-// 64 + 16p + 8(s - 2) (s >= 2), the same d order the Q^T fragments use.
-__device__ __forceinline__ int k_chunk(int s, int p) { return (s < 2 ? 0 : 8) + 2 * p + (s & 1); }
+// ---- raw fp8 tile placement in LDS ---------------------------------------------------------------
+// The tile is copied by eight 1 KB global_load_lds_dwordx4 instructions: I = 0..3 carry K rows
+// 8I .. 8I+7, I = 4..7 carry V rows 8(I-4) .. +7; lane l of an instruction lands at 16 l.  Which
+// (row, 16-byte chunk) a lane fetches is chosen so that the fragment reads below are free of bank
+// conflicts:
+//   K: row r (0..7), chunk c at slot 8 r + (c ^ (r >> 1)) - the 16 rows one fragment read touches
+//      (same chunk) fall in 16 distinct 16-byte bank groups;
+//   V: row r at slot 8 rho(r) + c with rho(r) = 2 (r & 3) + (r >> 2) - the rows 4p + j one
+//      transposing read touches (p = 0..3) alternate between the two bank halves.
+__host__ __device__ inline int k_slot(int r, int c) { return 8 * r + (c ^ (r >> 1)); }
+__host__ __device__ inline int v_slot(int r, int c) { return 8 * (2 * (r & 3) + (r >> 2)) + c; }
 
-// Staging registers of one tile: thread tid converts K bytes 16 (tid & 7) .. +15 of key tid >> 3;
-// threads of wave 0 also handle V for lane (c, p) = (lane % 16, lane / 16): 8 bytes d = 8c .. 8c+7
-// of the tile's k-slot tokens T_p[j] = 4p + j (j < 4), 16 + 4p + (j - 4) (j >= 4).
-struct Stage {
-    u32x4_t kr;
-    u32x2_t vr[8];
-};
-
-// Issue the global loads of tile k0 (keys >= k_hi zero-filled).  b0 / b1: cache blocks of the
-// tile's two 16-key groups.
-__device__ __forceinline__ void stage_load(Stage& sg, const Params& P, int kh, int k0, int k_hi,
-                                           int64_t b0, int64_t b1, int tid)
+// (row within the 8-row group, chunk) lane l of a K or V copy instruction fetches.
+__device__ __forceinline__ void dma_lane_rc(bool is_v, int lane, int& r, int& c)
 {
-    const int kr = tid >> 3, j8 = tid & 7;
-    {
-        const int tok = k0 + kr;
-        const int64_t blk = (kr >> 4) ? b1 : b0;
-        const int slot = tok % P.pblk;
-        const uint8_t* src = P.k + blk * P.sk0 + (int64_t)slot * P.sk1 + (int64_t)kh * P.sk2 + 16 * j8;
-        const u32x4_t z4 = {0u, 0u, 0u, 0u};
-        sg.kr = tok < k_hi ? load_nt_16(src) : z4;
+    if (!is_v) {
+        r = lane >> 3;
+        c = (lane & 7) ^ (r >> 1);
+    } else {
+        const int rho = lane >> 3;
+        c = lane & 7;
+        r = (rho >> 1) + 4 * (rho & 1);
     }
-    if (tid < 64) {
-        const int c = tid & 15, p = tid >> 4;
+}
+
+// global_load_lds_dwordx4 issued as inline assembly: lane i's 16 bytes land at lds_dst + 16 i.  The
+// compiler does not see this copy, so it inserts no wait for it: in particular no vmcnt(0)
+// before LDS reads it cannot prove disjoint from the copy's destination, which would drain the
+// whole prefetch ring each tile.  Completion is tracked only by the kernel's explicit
+// vmcnt waits (vmcnt counts in issue order, so the compiler's own waits for its loads stay
+// correct - at worst they wait longer).  lds_dst must be wave-uniform.
+__device__ __forceinline__ void dma16_untracked(const void* src, unsigned char* lds_dst)
+{
+    const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_void_t*)lds_dst;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :: "s"(lds_addr), "v"(src) : "memory", "m0");
+}
+
+// Block ids of 16-key groups 64 b .. 64 b + 63 (batch b), one per lane (0 past the context).
+__device__ __forceinline__ int load_group_blocks(const Params& P, const int32_t* btrow, int batch,
+                                                 int k_hi, int lane)
+{
+    const int key = 16 * (64 * batch + lane);
+    return key < k_hi ? btrow[key >> P.pshift] : 0;
+}
+
+// Issue this wave's share (instructions I = wave, wave + W, ...) of tile t's copies into `dst`.
+// One instruction covers 8 rows of one 16-key group, hence one cache block: its id comes from
+// the batch register `bids` (batch `batch`, which holds tile t) with readlane, its base address is
+// scalar and only slot and chunk vary per lane.  Keys >= k_hi fetch key k_hi - 1 (a real, finite
+// row in the same or the previous group; the causal mask removes it).
+template <int W>
+__device__ __forceinline__ void issue_tile(const Params& P, unsigned char* dst, int bids, int batch,
+                                           int kh, int t, int k_hi, int wave, int lane)
+{
+    const int g_last = (k_hi - 1) >> 4;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int kk = (j < 4 ? 0 : 16) + 4 * p + (j & 3);
-            const int tok = k0 + kk;
-            const int64_t blk = j < 4 ? b0 : b1;
-            const int slot = tok % P.pblk;
-            const uint8_t* src = P.v + blk * P.sv0 + (int64_t)slot * P.sv1 + (int64_t)kh * P.sv2 + 8 * c;
-            const u32x2_t z2 = {0u, 0u};
-            sg.vr[j] = tok < k_hi ? __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(src)) : z2;
-        }
+    for (int I = wave; I < 8; I += W) {
+        const bool is_v = I >= 4;
+        int r, c;
+        dma_lane_rc(is_v, lane, r, c);
+        const int grp = min(2 * t + ((I & 3) >> 1), g_last);
+        const int64_t blk = __builtin_amdgcn_readlane(bids, grp - 64 * batch);
+        int key = t * kBN + 8 * (I & 3) + r;
+        key = key < k_hi ? key : k_hi - 1;
+        const uint32_t slot = (uint32_t)key & (uint32_t)(P.pblk - 1);
+        const uint8_t* base = is_v ? P.v + blk * P.sv0 + (int64_t)kh * P.sv2
+                                   : P.k + blk * P.sk0 + (int64_t)kh * P.sk2;
+        const uint32_t off = slot * (uint32_t)(is_v ? P.sv1 : P.sk1) + 16u * (uint32_t)c;
+        dma16_untracked(base + off, dst + I * 1024);
     }
 }
 
-// Convert the staged tile to bf16 and write it to LDS buffer `buf` (layouts above).
-__device__ __forceinline__ void stage_store(const Stage& sg, unsigned char* buf, int tid)
+// Workgroup barrier that orders LDS only.  __syncthreads() carries a workgroup-scope release
+// fence, which on gfx950 waits for every outstanding vector-memory operation - including the
+// async tile copies still in flight for later tiles.  Here each wave has already waited for its
+// own copies of the tile it is about to read (vmcnt), so the barrier only needs this wave's LDS
+// reads of the previous tile to have completed (lgkmcnt) before the slot is overwritten; the
+// "memory" clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier()
 {
-    const int kr = tid >> 3, j8 = tid & 7;
-    const int sw = kr & 15;
-    unsigned char* krow = buf + kr * kKRow;
-    *reinterpret_cast<bf16x8_t*>(krow + 16 * ((2 * j8) ^ sw)) = fp8x8_to_bf16x8(sg.kr[0], sg.kr[1]);
-    *reinterpret_cast<bf16x8_t*>(krow + 16 * ((2 * j8 + 1) ^ sw)) = fp8x8_to_bf16x8(sg.kr[2], sg.kr[3]);
-    if (tid < 64) {
-        const int c = tid & 15, p = tid >> 4;
-        u32x4_t va[8];
-        v_fragments(sg.vr, va);
-        unsigned char* vt = buf + kKTile;
-#pragma unroll
-        for (int n = 0; n < 8; ++n)
-            *reinterpret_cast<u32x4_t*>(vt + (16 * n + c) * kVRow + 16 * p) = va[n];
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int W>
+constexpr int copies_per_wave(int wave) { return (8 - wave + W - 1) / W; }
+
+// s_waitcnt vmcnt(n) for a runtime n in 0..12.
+__device__ __forceinline__ void wait_vmcnt_rt(int n)
+{
+    switch (n) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<1>(); break;
+        case 2: wait_vmcnt<2>(); break;
+        case 3: wait_vmcnt<3>(); break;
+        case 4: wait_vmcnt<4>(); break;
+        case 5: wait_vmcnt<5>(); break;
+        case 6: wait_vmcnt<6>(); break;
+        case 7: wait_vmcnt<7>(); break;
+        case 8: wait_vmcnt<8>(); break;
+        case 9: wait_vmcnt<9>(); break;
+        case 10: wait_vmcnt<10>(); break;
+        case 11: wait_vmcnt<11>(); break;
+        default: wait_vmcnt<12>(); break;
     }
 }
 
-// Block ids of the two 16-key groups of tile k0, one vector load (lanes alternate groups); the
-// caller reads lanes 0 and 1 with readlane.
-__device__ __forceinline__ int load_tile_blocks(const Params& P, const int32_t* btrow, int k0, int k_hi, int lane)
-{
-    const int t = k0 + 16 * (lane & 1);
-    return t < k_hi ? btrow[t / P.pblk] : 0;
-}
-
-template <int RS>
-__global__ void __launch_bounds__(kT)
+template <int W, int RS, int R>
+__global__ void __launch_bounds__(W * 64)
 prefill_kernel(Params P)
 {
-    __shared__ __align__(16) unsigned char lds[2 * kBuf];
+    static_assert(R >= 2 && (R - 2) * ((8 + W - 1) / W) <= 12, "ring depth vs vmcnt range");
+    __shared__ __align__(16) unsigned char ring[R * kTileBytes];
 
-    const int kh = blockIdx.y, seq = blockIdx.z;
+    // Work item from the 1-D grid.  Workgroups are dispatched round-robin over the 8 XCDs, so with
+    // xcd_map workgroup lin (on XCD lin % 8) takes kv head (lin % 8) % HKV: every XCD's L2 then
+    // holds the K/V of one kv head instead of all of them.  Ranks count from the longest causal
+    // rows.  The mapping is a bijection whatever the dispatch order; only the L2 reuse depends on it.
+    const int lin = blockIdx.x, seq = blockIdx.z;
+    int kh, rank;
+    if (P.xcd_map) {
+        const int xcd = lin & 7, per = 8 / P.hkv;
+        kh = xcd % P.hkv;
+        rank = (lin >> 3) * per + xcd / P.hkv;
+    } else {
+        kh = lin % P.hkv;
+        rank = lin / P.hkv;
+    }
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15;
     const int lp = lane >> 4;
     const int gqa = P.gqa;
@@ -158,22 +212,46 @@ prefill_kernel(Params P)
         qlen = P.qlen_host;
         q0 = P.q0_host;
     }
-    const int BT = 16 * P.nb;
-    const int ntb = (qlen + BT - 1) / BT;
-    const int tb = (int)gridDim.x - 1 - (int)blockIdx.x;      // longest causal rows first
-    if (tb >= ntb || q0 < 0) return;                          // whole workgroup, before any barrier
-    const int t0 = tb * BT;
-    const int k_hi = q0 + min(t0 + BT, qlen);                 // keys [0, k_hi)
+    // Token blocks (of 16) of this workgroup: nb consecutive ones, or with `paired` the blocks
+    // r and n16 - 1 - r, whose causal spans add up to the same work for every workgroup.
+    // Token blocks (of 16) of this workgroup: block b is blk_a + b (nb consecutive ones), or with
+    // `paired` blk_a = r and blk_b = n16 - 1 - r, whose causal spans add up to the same work for
+    // every workgroup.
+    const int n16 = (qlen + 15) >> 4;
+    const int tb = P.ntb_grid - 1 - rank;                     // longest causal rows first
+    int blk_a, blk_b, nblocks, last16;
+    if (P.paired) {
+        if (tb < 0 || tb >= ((n16 + 1) >> 1) || q0 < 0) return;   // whole workgroup, before any barrier
+        blk_a = tb;
+        blk_b = n16 - 1 - tb;
+        nblocks = blk_b > blk_a ? 2 : 1;
+        last16 = blk_b;
+    } else {
+        if (tb < 0 || tb >= (n16 + P.nb - 1) / P.nb || q0 < 0) return;
+        blk_a = tb * P.nb;
+        blk_b = blk_a + 1;
+        nblocks = min(P.nb, n16 - blk_a);
+        last16 = blk_a + nblocks - 1;
+    }
+    const int paired = P.paired;
+    auto block_of = [&](int b) { return paired ? (b ? blk_b : blk_a) : blk_a + b; };
+    const int k_hi = q0 + min(16 * (last16 + 1), qlen);      // keys [0, k_hi)
     const int32_t* btrow = P.bt + (int64_t)seq * P.bt_stride;
-    const int nrs = P.nb * gqa;
+    const int nrs = nblocks * gqa;
+    const int ntiles = (k_hi + kBN - 1) / kBN;
+    const int my_copies = copies_per_wave<W>(wave);
 
-    // ---- Q^T fragments of the wave's row-sets ---------------------------------------------------
+    // ---- block ids, Q^T fragments, first tiles in flight ------------------------------------------
+    int bid_batch = 0;
+    int bid_cur = load_group_blocks(P, btrow, 0, k_hi, lane);
+    int bid_next = load_group_blocks(P, btrow, 1, k_hi, lane);
+
     u32x4_t qf[RS][4];
 #pragma unroll
     for (int j = 0; j < RS; ++j) {
-        const int r = wave + kWaves * j;
+        const int r = wave + W * j;
         const int g = r % gqa, b = r / gqa;
-        const int tok = t0 + 16 * b + lr;
+        const int tok = 16 * block_of(b) + lr;
         const bool ok = r < nrs && tok < qlen;
         const u32x4_t zero = {0u, 0u, 0u, 0u};
         const __bf16* qrow = P.q + (int64_t)(q_begin + (ok ? tok : 0)) * P.q_stride +
@@ -185,6 +263,10 @@ prefill_kernel(Params P)
     }
     const float qk_scale = P.sm_scale * P.k_scale[0] * kLog2e;
     const float vs = P.v_scale[0];
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int t = 0; t < R - 1; ++t)
+        if (t < ntiles) issue_tile<W>(P, ring + t * kTileBytes, bid_cur, 0, kh, t, k_hi, wave, lane);
 
     float m_run[RS], l_run[RS];
     f32x4_t o[RS][8];
@@ -196,64 +278,82 @@ prefill_kernel(Params P)
         for (int n = 0; n < 8; ++n) o[j][n] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     }
 
-    // ---- tile pipeline: block ids two tiles ahead, K/V bytes one tile ahead ---------------------
-    const int ntiles = (k_hi + kBN - 1) / kBN;
-    Stage sg;
-    {
-        const int bt0 = load_tile_blocks(P, btrow, 0, k_hi, lane);
-        stage_load(sg, P, kh, 0, k_hi, __builtin_amdgcn_readlane(bt0, 0), __builtin_amdgcn_readlane(bt0, 1), tid);
-    }
-    int bt_next = load_tile_blocks(P, btrow, kBN, k_hi, lane);
-
-    for (int it = 0; it < ntiles; ++it) {
-        const int k0 = it * kBN;
-        unsigned char* buf = lds + (it & 1) * kBuf;
-        stage_store(sg, buf, tid);
-        __syncthreads();
-        if (it + 1 < ntiles) {
-            const int64_t b0 = __builtin_amdgcn_readlane(bt_next, 0);
-            const int64_t b1 = __builtin_amdgcn_readlane(bt_next, 1);
-            bt_next = load_tile_blocks(P, btrow, k0 + 2 * kBN, k_hi, lane);
-            stage_load(sg, P, kh, k0 + kBN, k_hi, b0, b1, tid);
+    for (int t = 0; t < ntiles; ++t) {
+        const int k0 = t * kBN;
+        // Tile t's copies (this wave's) are the oldest still counted; younger: tiles t+1 ..
+        // min(t + R - 2, ntiles - 1).  The barrier then makes every wave's copies visible and
+        // guarantees that tile t - 1's slot is no longer read.
+        const int younger = min(R - 2, ntiles - 1 - t);
+        wait_vmcnt_rt(younger * my_copies);
+        lds_barrier();
+        const int tn = t + R - 1;
+        if (tn < ntiles) {
+            if ((tn >> 5) != bid_batch) {                     // 32 tiles per block-id batch
+                ++bid_batch;
+                bid_cur = bid_next;
+                bid_next = load_group_blocks(P, btrow, bid_batch + 1, k_hi, lane);
+            }
+            issue_tile<W>(P, ring + (tn % R) * kTileBytes, bid_cur, bid_batch, kh, tn, k_hi, wave, lane);
         }
+        const unsigned char* buf = ring + (t % R) * kTileBytes;
 
-        // K fragments (2 key groups x 4 d steps) and V^T fragments (8 d blocks), shared by the
-        // wave's row-sets.
+        // K fragments: lane (r, p) of key group kg = key 16 kg + r; step s covers d = 16p + 8s
+        // (s < 2) / 64 + 16p + 8(s - 2): chunk (s >> 1) * 4 + p, half s & 1.
         u32x4_t kf[2][4];
 #pragma unroll
-        for (int kg = 0; kg < 2; ++kg)
+        for (int kg = 0; kg < 2; ++kg) {
+            const int row = 16 * kg + lr;
+            const unsigned char* kb = buf + (row >> 3) * 1024;
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                kf[kg][s] = *reinterpret_cast<const u32x4_t*>(buf + (16 * kg + lr) * kKRow +
-                                                              16 * (k_chunk(s, lp) ^ lr));
-        u32x4_t vf[8];
-#pragma unroll
-        for (int n = 0; n < 8; ++n)
-            vf[n] = *reinterpret_cast<const u32x4_t*>(buf + kKTile + (16 * n + lr) * kVRow + 16 * lp);
-
+            for (int st = 0; st < 4; ++st) {
+                const u32x2_t raw = *reinterpret_cast<const u32x2_t*>(
+                    kb + 16 * k_slot(row & 7, (st >> 1) * 4 + lp) + 8 * (st & 1));
+                kf[kg][st] = __builtin_bit_cast(u32x4_t, fp8x8_to_bf16x8(raw[0], raw[1]));
+            }
+        }
+        // S^T for every row-set first (K fragments then die), softmax and P.V after.
+        f32x4_t sc[RS][2];
+        bool live[RS];
 #pragma unroll
         for (int j = 0; j < RS; ++j) {
-            const int r = wave + kWaves * j;
-            if (r >= nrs) continue;
-            const int qpos0 = q0 + t0 + 16 * (r / gqa);           // position of the row-set's first query
-            if (k0 > qpos0 + 15) continue;                         // tile above the diagonal
-            f32x4_t s[2];
+            const int r = wave + W * j;
+            const int qpos0 = q0 + 16 * block_of(r / gqa);
+            live[j] = r < nrs && k0 <= qpos0 + 15;                // else: tile above the diagonal
+            if (!live[j]) continue;
 #pragma unroll
             for (int kg = 0; kg < 2; ++kg) {
                 f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int st = 0; st < 4; ++st)
                     acc = mfma16x16x32_bf16(as_bf16x8(kf[kg][st]), as_bf16x8(qf[j][st]), acc);
-                s[kg] = acc;
+                sc[j][kg] = acc;
             }
+        }
+        // V^T fragments: lane (c, p) transposes d = 8c .. 8c+7 of its k-slot tokens.
+        u32x4_t vf[8];
+        {
+            u32x2_t vr[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const int row = (jj < 4 ? 0 : 16) + 4 * lp + (jj & 3);
+                const unsigned char* vb = buf + 4096 + (row >> 3) * 1024;
+                vr[jj] = *reinterpret_cast<const u32x2_t*>(vb + 16 * v_slot(row & 7, lr >> 1) + 8 * (lr & 1));
+            }
+            v_fragments(vr, vf);
+        }
+#pragma unroll
+        for (int j = 0; j < RS; ++j) {
+            if (!live[j]) continue;
+            const int r = wave + W * j;
+            const int qpos0 = q0 + 16 * block_of(r / gqa);
             float mc = neg_inf();
             if (k0 + kBN - 1 <= qpos0) {
 #pragma unroll
                 for (int kg = 0; kg < 2; ++kg)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        s[kg][i] *= qk_scale;
-                        mc = fmaxf(mc, s[kg][i]);
+                        sc[j][kg][i] *= qk_scale;
+                        mc = fmaxf(mc, sc[j][kg][i]);
                     }
             } else {
                 const int qpos = qpos0 + lr;
@@ -262,50 +362,53 @@ prefill_kernel(Params P)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int key = k0 + 16 * kg + 4 * lp + i;
-                        const float x = key <= qpos ? s[kg][i] * qk_scale : neg_inf();
-                        s[kg][i] = x;
+                        const float x = key <= qpos ? sc[j][kg][i] * qk_scale : neg_inf();
+                        sc[j][kg][i] = x;
                         mc = fmaxf(mc, x);
                     }
             }
-            mc = fmaxf(mc, __shfl_xor(mc, 16));
-            mc = fmaxf(mc, __shfl_xor(mc, 32));
-            const float m_new = fmaxf(m_run[j], mc);
-            const float m_use = m_new == neg_inf() ? 0.f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_use);
+            mc = max_xor16_32(mc);
+            // Lazy rescale: the accumulators move to a new reference max only when the row max
+            // grew by more than kRescaleSlack (then probabilities stay below 2^kRescaleSlack).
+            const bool need = mc > m_run[j] + kRescaleSlack;
+            if (__any(need)) {
+                const float m_new = need ? mc : m_run[j];
+                const float alpha = __builtin_amdgcn_exp2f(m_run[j] - (m_new == neg_inf() ? 0.f : m_new));
+                l_run[j] *= alpha;
+#pragma unroll
+                for (int n = 0; n < 8; ++n) o[j][n] *= alpha;
+                m_run[j] = m_new;
+            }
+            const float m_use = m_run[j] == neg_inf() ? 0.f : m_run[j];
             float psum = 0.f;
 #pragma unroll
             for (int kg = 0; kg < 2; ++kg)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float pv = __builtin_amdgcn_exp2f(s[kg][i] - m_use);
-                    s[kg][i] = pv;
+                    const float pv = __builtin_amdgcn_exp2f(sc[j][kg][i] - m_use);
+                    sc[j][kg][i] = pv;
                     psum += pv;
                 }
-            l_run[j] = l_run[j] * alpha + psum;
-            m_run[j] = m_new;
+            l_run[j] += psum;
             u32x4_t pb;
-            pb[0] = pack_bf16x2(s[0][0], s[0][1]);
-            pb[1] = pack_bf16x2(s[0][2], s[0][3]);
-            pb[2] = pack_bf16x2(s[1][0], s[1][1]);
-            pb[3] = pack_bf16x2(s[1][2], s[1][3]);
+            pb[0] = pack_bf16x2(sc[j][0][0], sc[j][0][1]);
+            pb[1] = pack_bf16x2(sc[j][0][2], sc[j][0][3]);
+            pb[2] = pack_bf16x2(sc[j][1][0], sc[j][1][1]);
+            pb[3] = pack_bf16x2(sc[j][1][2], sc[j][1][3]);
 #pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                o[j][n] *= alpha;
-                o[j][n] = mfma16x16x32_bf16(as_bf16x8(vf[n]), as_bf16x8(pb), o[j][n]);
-            }
+            for (int n = 0; n < 8; ++n) o[j][n] = mfma16x16x32_bf16(as_bf16x8(vf[n]), as_bf16x8(pb), o[j][n]);
         }
     }
 
     // ---- normalise and store: lane (q, p) holds d = 32p + 8i + n of query row q ------------------
 #pragma unroll
     for (int j = 0; j < RS; ++j) {
-        const int r = wave + kWaves * j;
+        const int r = wave + W * j;
         float l = l_run[j];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+        l = sum_xor16_32(l);
         if (r >= nrs) continue;
         const int g = r % gqa, b = r / gqa;
-        const int tok = t0 + 16 * b + lr;
+        const int tok = 16 * block_of(b) + lr;
         if (tok >= qlen) continue;
         const float f = l > 0.f ? vs / l : 0.f;
         __bf16* orow = P.out + (int64_t)(q_begin + tok) * P.o_stride + (int64_t)(kh * gqa + g) * kD + 32 * lp;
@@ -321,30 +424,64 @@ prefill_kernel(Params P)
     }
 }
 
-// Token blocks of 16 per workgroup and row-sets per wave for a GQA: nb * gqa row-sets over 4 waves.
-inline void plan(int gqa, int& nb, int& rs)
+// Launch shapes: (waves, row-sets per wave, ring depth).  nb token blocks of 16 per workgroup is
+// the largest count whose nb * GQA row-sets fit waves * RS.
+struct Shape {
+    int waves, rs, ring, paired;
+};
+constexpr Shape kShapes[] = {{4, 3, 4, 0}, {4, 3, 6, 0}, {8, 2, 4, 0}, {4, 4, 4, 0}, {4, 2, 4, 0},
+                             {4, 1, 4, 0}, {6, 2, 4, 1}, {8, 2, 4, 1}};
+constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
+int g_shape = -1;              // -1: choose by GQA
+
+// Default shape per GQA (measured at configs[3], GQA 6: 8 waves x 2 row-sets with paired token
+// blocks 184 us; 4 x 3 unpaired 251 us; 8 x 2 unpaired 190 us).
+inline int choose_shape(int gqa)
 {
-    nb = 12 / gqa;
+    if (g_shape >= 0) return g_shape;
+    if (gqa <= 1) return 5;                       // 4 waves x 1 row-set, 4 token blocks
+    if (gqa <= 2) return 4;                       // 4 waves x 2 row-sets, 4 token blocks
+    if (gqa <= 8) return 7;                       // 8 waves x 2 row-sets (paired blocks when nb = 2)
+    return 3;                                     // 4 waves x 4 row-sets
+}
+
+inline int plan_nb(int gqa, const Shape& s)
+{
+    int nb = (s.waves * s.rs) / gqa;
     if (nb < 1) nb = 1;
     if (nb > 4) nb = 4;
-    rs = (nb * gqa + kWaves - 1) / kWaves;
+    return nb;
 }
 
 int launch(const Params& P0, int num_seqs, int max_query_len, hipStream_t stream)
 {
     Params P = P0;
-    int nb, rs;
-    plan(P.gqa, nb, rs);
-    P.nb = nb;
-    const int bt = 16 * nb;
-    const unsigned gx = (unsigned)((max_query_len + bt - 1) / bt);
-    if (gx == 0) return FP8KV_OK;
-    const dim3 grid(gx, (unsigned)P.hkv, (unsigned)num_seqs);
-    switch (rs) {
-        case 1: hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kT), 0, stream, P); break;
-        case 2: hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kT), 0, stream, P); break;
-        case 3: hipLaunchKernelGGL(prefill_kernel<3>, grid, dim3(kT), 0, stream, P); break;
-        default: hipLaunchKernelGGL(prefill_kernel<4>, grid, dim3(kT), 0, stream, P); break;
+    const int si = choose_shape(P.gqa);
+    const Shape sh = kShapes[si];
+    if (sh.waves * sh.rs < P.gqa) return FP8KV_ERR_SHAPE;
+    P.nb = plan_nb(P.gqa, sh);
+    P.paired = sh.paired && P.nb == 2 ? 1 : 0;
+    const int n16 = (max_query_len + 15) / 16;
+    int ntb = P.paired ? (n16 + 1) / 2 : (n16 + P.nb - 1) / P.nb;
+    if (ntb == 0) return FP8KV_OK;
+    P.xcd_map = (P.hkv <= 8 && 8 % P.hkv == 0) ? 1 : 0;
+    if (P.xcd_map) {
+        const int per = 8 / P.hkv;                    // token-block ranks per kv head per XCD round
+        ntb = (ntb + per - 1) / per * per;
+    }
+    P.ntb_grid = ntb;
+    const dim3 grid((unsigned)(ntb * P.hkv), 1u, (unsigned)num_seqs);
+    const dim3 block(64 * sh.waves);
+    begin_launch();
+    switch (si) {
+        case 0: hipLaunchKernelGGL((prefill_kernel<4, 3, 4>), grid, block, 0, stream, P); break;
+        case 1: hipLaunchKernelGGL((prefill_kernel<4, 3, 6>), grid, block, 0, stream, P); break;
+        case 2: hipLaunchKernelGGL((prefill_kernel<8, 2, 4>), grid, block, 0, stream, P); break;
+        case 3: hipLaunchKernelGGL((prefill_kernel<4, 4, 4>), grid, block, 0, stream, P); break;
+        case 4: hipLaunchKernelGGL((prefill_kernel<4, 2, 4>), grid, block, 0, stream, P); break;
+        case 6: hipLaunchKernelGGL((prefill_kernel<6, 2, 4>), grid, block, 0, stream, P); break;
+        case 7: hipLaunchKernelGGL((prefill_kernel<8, 2, 4>), grid, block, 0, stream, P); break;
+        default: hipLaunchKernelGGL((prefill_kernel<4, 1, 4>), grid, block, 0, stream, P); break;
     }
     return finish_launch();
 }
@@ -359,7 +496,8 @@ int check_common(const void* q, const void* k_cache, const void* v_cache, void* 
     if (num_kv_heads < 1 || num_q_heads < 1 || block_size < 1 || bt_stride < 0) return FP8KV_ERR_ARG;
     if (num_kv_heads > 65535) return FP8KV_ERR_SHAPE;
     if (head_size != kD || num_q_heads % num_kv_heads != 0) return FP8KV_ERR_SHAPE;
-    if (num_q_heads / num_kv_heads > kMaxGqa || (block_size % 16) != 0) return FP8KV_ERR_SHAPE;
+    if (num_q_heads / num_kv_heads > kMaxGqa) return FP8KV_ERR_SHAPE;
+    if (block_size < 16 || (block_size & (block_size - 1)) != 0) return FP8KV_ERR_SHAPE;
     if (!aligned(k_cache, 16) || !aligned(v_cache, 8) || !aligned(q, 16) || !aligned(out, 16))
         return FP8KV_ERR_ALIGN;
     if ((sk0 | sk1 | sk2) & 15) return FP8KV_ERR_ALIGN;
@@ -393,7 +531,11 @@ Params make_params(const void* q, int64_t q_row_stride, const void* k_cache, con
     P.hkv = num_kv_heads;
     P.gqa = num_q_heads / num_kv_heads;
     P.pblk = block_size;
+    P.pshift = __builtin_ctz((unsigned)block_size);
     P.nb = 1;
+    P.paired = 0;
+    P.ntb_grid = 0;
+    P.xcd_map = 0;
     P.q0_host = 0;
     P.qlen_host = 0;
     return P;
@@ -427,6 +569,11 @@ extern "C" int fp8kv_prefill_attn(const void* q, int64_t q_row_stride,
     P.q0_host = q0;
     P.qlen_host = qlen;
     return launch(P, 1, qlen, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" void fp8kv_prefill_tune(int shape)
+{
+    g_shape = (shape >= 0 && shape < kNumShapes) ? shape : -1;
 }
 
 extern "C" int fp8kv_prefill_attn_varlen(const void* q, int64_t q_row_stride,

@@ -21,6 +21,8 @@ _c_sz = ctypes.c_size_t
 SIGNATURES: dict[str, tuple] = {
     "fp8kv_status_string": (ctypes.c_char_p, [_c_i]),
     "fp8kv_last_status": (_c_i, []),
+    "fp8kv_last_hip_error": (_c_i, []),
+    "fp8kv_last_hip_error_string": (ctypes.c_char_p, []),
     # reference ABI, h4mv/h4mv.cu:106-107 / h4mv/fp8kv_hipw4.py:21-23
     "h4mv_launch": (None, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
     "h4mv_launch_status": (_c_i, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
@@ -41,6 +43,7 @@ SIGNATURES: dict[str, tuple] = {
     "fp8kv_h4mv_audit": (_c_i, [_c_i] * 3),
     "fp8kv_h4mv_tune": (None, [_c_i] * 2),
     "fp8kv_decode_tune": (None, [_c_i] * 2),
+    "fp8kv_prefill_tune": (None, [_c_i]),
 }
 
 _lock = threading.Lock()
@@ -80,5 +83,8 @@ def load() -> ctypes.CDLL:
 
 def check(fn_name: str, status: int) -> None:
     if status != 0:
-        msg = load().fp8kv_status_string(status).decode()
+        lib = load()
+        msg = lib.fp8kv_status_string(status).decode()
+        if status == 4:
+            msg += f": HIP error {lib.fp8kv_last_hip_error()} ({lib.fp8kv_last_hip_error_string().decode()})"
         raise Fp8kvError(fn_name, status, msg)

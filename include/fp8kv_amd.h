@@ -32,6 +32,10 @@ const char* fp8kv_status_string(int status);
 /* Status of the last h4mv_launch() call on the calling host thread. */
 int fp8kv_last_status(void);
 
+/* HIP error code (and its text) behind the last FP8KV_ERR_LAUNCH returned on this host thread. */
+int fp8kv_last_hip_error(void);
+const char* fp8kv_last_hip_error_string(void);
+
 /* ---------------------------------------------------------------------------------------------
  * MXFP4 W4A16 matvec:  Out[m, n] = bf16( sum_k X[m, k] * e2m1(W[n, k]) * e8m0(St[n, k / 32]) )
  *   W   uint8 [N, K/2]  two e2m1 codes per byte, low nibble = even k     (16-byte aligned)
@@ -75,7 +79,8 @@ int h4mv_f32_launch_status(const void* W, const void* St, const void* Xb, void* 
  *   out          bf16 [tokens, HQ, 128], row stride out_row_stride; only rows qsl[s] are written
  *   query_start_loc int32 [NS + 1] (row of sequence s = query_start_loc[s]); seq_lens int32 [NS];
  *   block_table  int32 [NS, bt_stride]; k_scale, v_scale fp32 device scalars (read on the device)
- *   head_size == 128, HQ % HKV == 0, HQ / HKV <= 16, block_size % 16 == 0, 1 <= num_splits <= 256.
+ *   head_size == 128, HQ % HKV == 0, HQ / HKV <= 16, block_size a power of two >= 16 (vLLM's block
+ *   sizes), 1 <= num_splits <= 256.
  *   A sequence with seq_len 0 gets zeros.
  *
  * Scratch: fp8kv_decode_scratch_bytes() bytes (0 when num_splits == 1), 256-byte aligned.  It must be

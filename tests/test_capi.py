@@ -81,7 +81,7 @@ def _decode_args(**kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(q=0), 1), (dict(ns=0), 1), (dict(nsplit=0), 1), (dict(nsplit=257), 1),
-    (dict(hd=64), 2), (dict(hq=25), 2), (dict(hq=68, hkv=4), 2), (dict(pblk=8), 2),
+    (dict(hd=64), 2), (dict(hq=25), 2), (dict(hq=68, hkv=4), 2), (dict(pblk=8), 2), (dict(pblk=48), 2),
     (dict(k=A + 8), 3), (dict(sk1=4 * 128 + 8), 3), (dict(sv2=4), 3), (dict(qs=24 * 128 + 4), 3),
     (dict(nsplit=8), 5), (dict(nsplit=8, scr=A, scrb=100), 5),
 ])

@@ -175,3 +175,25 @@ def test_rejects_bad_arguments():
                                 d["block_table"].data_ptr(), d["block_table"].stride(0),
                                 d["q"].data_ptr(), d["q"].data_ptr(), 0.1, 24, 5, 128, 16, 0, 16, None)
     assert st == 2                                     # HQ % HKV != 0
+
+
+SHAPE_CAP = [12, 12, 16, 16, 8, 4, 12, 16]      # waves x row-sets of each launch shape
+
+
+@pytest.mark.parametrize("shape", [0, 1, 2, 3, 4, 5, 6, 7])
+def test_every_launch_shape(shape):
+    """Each (waves, row-sets, ring depth) shape the tuning hook can select meets the same bar,
+    single-sequence and varlen, wherever it can hold the GQA."""
+    lib = _lib.load()
+    try:
+        lib.fp8kv_prefill_tune(shape)
+        for hq in (4, 8, 24, 64):
+            cap = SHAPE_CAP[shape]
+            if hq // 4 > cap:
+                continue
+            _check_single(161, 45, HQ=hq, HKV=4, seed=shape * 100 + hq)
+            _check_single(200, 0, HQ=hq, HKV=4, seed=shape * 100 + hq + 1)     # odd block count
+        cap = SHAPE_CAP[shape]
+        _check_varlen([40, 97], [3, 200], seed=shape + 50, HQ=4 * min(6, cap), HKV=4)
+    finally:
+        lib.fp8kv_prefill_tune(-1)
