@@ -68,6 +68,13 @@ def load() -> ctypes.CDLL:
     with _lock:
         if _lib is not None:
             return _lib
+        # Load torch first when it is installed: its wheel bundles a HIP runtime with the same
+        # soname as /opt/rocm's, and whichever is loaded first serves the whole process.  Loading
+        # this library first would bind torch to the system runtime instead of its own.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         path = lib_path()
         if not os.path.exists(path):
             raise FileNotFoundError(

@@ -40,6 +40,7 @@ def _log(msg: str) -> None:
 
 def load_launcher(path: str | None = None):
     """ctypes handle of ``h4mv_launch`` bound exactly as the reference binds it."""
+    import torch  # noqa: F401  - bind the library to torch's HIP runtime (see fp8kv_amd._lib.load)
     if path is None:
         from fp8kv_amd import _lib
         path = _lib.lib_path()
