@@ -7,11 +7,14 @@ the timed region; the decode-attention b8@4k leg, M=4/8 and the other legs are r
 A "step" is one launch of the kernel over one batch of synthetic input.  Inputs are resident in
 HBM before the timed region and rotate over enough copies (> 2x the 256 MB Infinity Cache) that
 every step reads its bytes from HBM.  Timing: HIP events on the stream the kernels run on
-(torch's current stream): ``--warmup`` untimed steps, then exactly ``--steps`` timed steps, each
-bracketed by its own start/end event pair, the whole region by a synchronize on both sides; a
-GPU-side spin queued ahead of the timed region keeps the host's launch overhead out of the events.
+(torch's current stream): ``--warmup`` untimed steps, then exactly ``--steps`` timed steps
+launched back to back, the whole region bracketed by an event pair and by a synchronize on both
+sides; a GPU-side spin queued ahead of the timed region keeps the host's launch overhead out of
+the events.  Each timed launch also carries its own event pair, armed with
+``fp8kv_time_next_launch`` and stamped by hipExtLaunchKernel at the dispatch's start and end.
   * ``ms_per_step`` / ``value``: timed-region wall time / steps (includes launch gaps);
-  * ``roofline.achieved``: algorithmic bytes / mean(end_i - start_i), the kernel's own duration.
+  * ``roofline.achieved``: algorithmic bytes / mean(end_i - start_i), the kernel's own duration
+    (the figure a kernel trace reports for the same launches).
 The CPU baseline is the oracle's torch-CPU fp32 dequant path on a bounded sample (rank 0, N=1).
 """
 from __future__ import annotations
@@ -32,6 +35,10 @@ sys.path.insert(0, REPO)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 MFMA_BF16_PEAK_TFLOPS = 2500.0 # MI355X dense bf16 MFMA
 ROTATE_BYTES = 1 << 30         # >= 4x the 256 MB MALL
+# HBM bytes per launch of each leg's kernel, from two rocprofv3 --pmc runs of this script
+# (FETCH_SIZE, then WRITE_SIZE, scaled by what they read for a 256 MiB copy; commands and tables in
+# profiles/*.md).  They are properties of the kernels as built when profiled, not measured here.
+MEASURED_TRAFFIC = {"w4_gemv_M1": 62578323, "decode_b8_4k": 35999105, "prefill_cfg3": 33681605}
 METRIC = "µs/layer + achieved HBM GB/s (%roofline): decode attn b8@4k, W4 GEMV M=1"
 
 
@@ -46,28 +53,39 @@ def decode_bytes(ctx, HQ: int, HKV: int, D: int, PBLK: int) -> int:
             + sum(math.ceil(c / PBLK) for c in ctx) * 4)
 
 
-def time_launches(launch, n_sets: int, steps: int, warmup: int):
+def time_launches(launch, n_sets: int, steps: int, warmup: int, arm: bool = True):
     """Run ``launch(i % n_sets)`` warmup + steps times.
 
-    Returns (wall ms per step over the timed region, list of per-launch kernel ms)."""
+    Returns (wall ms per step over the timed region, list of per-launch kernel ms).  With
+    ``arm=False`` (a launch that is not this library's) each launch is bracketed by two events
+    recorded on the stream instead, which adds the marker overhead to its duration."""
     import torch
+    from fp8kv_amd import _lib
+    lib = _lib.load()
     for i in range(warmup):
         launch(i % n_sets)
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for e in st + en:              # torch creates the HIP event at its first record
+        e.record()
     torch.cuda.synchronize()
     # A GPU-side spin queued first lets the host enqueue every timed launch before the GPU reaches
     # them, so the events measure GPU time and not the host's per-call launch overhead.
     torch.cuda._sleep(int(2e6) + steps * 60000)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    st = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    en = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     t0.record()
     for i in range(steps):
-        st[i].record()
-        launch(i % n_sets)
-        en[i].record()
+        if arm:
+            lib.fp8kv_time_next_launch(st[i].cuda_event, en[i].cuda_event)
+            launch(i % n_sets)
+        else:
+            st[i].record()
+            launch(i % n_sets)
+            en[i].record()
     t1.record()
     torch.cuda.synchronize()
+    lib.fp8kv_time_next_launch(None, None)
     per = [st[i].elapsed_time(en[i]) for i in range(steps)]
     return t0.elapsed_time(t1) / steps, per
 
@@ -149,6 +167,26 @@ def bench_decode(ctx, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK=16, poo
     torch.cuda.empty_cache()
     r = _summary(wall, per, decode_bytes(ctx, HQ, HKV, D, PBLK))
     r.update({"rotation_sets": n_sets, "num_splits": nsplit})
+    return r
+
+
+def bench_copy(steps: int, warmup: int, nbytes: int = 256 << 20):
+    """A plain device-to-device copy of ``nbytes`` (torch's copy kernel): the practical HBM
+    read+write rate beside the kernels, and the calibration launch for the traffic counters."""
+    import torch
+    dev = torch.device("cuda")
+    n_sets = 4
+    src = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(i + 1) for i in range(n_sets)]
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+    def launch(i):
+        dst.copy_(src[i])
+
+    wall, per = time_launches(launch, n_sets, steps, warmup, arm=False)
+    del src, dst
+    torch.cuda.empty_cache()
+    r = _summary(wall, per, 2 * nbytes)
+    r["copy_bytes"] = nbytes
     return r
 
 
@@ -258,8 +296,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--legs", default="w4,decode,prefill",
-                    help="comma list of legs to run (w4, decode, prefill)")
+    ap.add_argument("--legs", default="w4,decode,prefill,copy",
+                    help="comma list of legs to run (w4, decode, prefill, copy)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one GPU; "
@@ -291,6 +329,8 @@ def main():
         legs["prefill_cfg3"] = bench_prefill([2048], [2048], pf_steps, max(2, args.warmup // 4))
         legs["prefill_cfg3_varlen_4x512"] = bench_prefill([512] * 4, [0] * 4, pf_steps,
                                                           max(2, args.warmup // 4), seed=1)
+    if "copy" in legs_wanted:
+        legs["copy_256MiB"] = bench_copy(max(5, args.steps // 4), max(2, args.warmup // 4))
     cpu = None if (args.no_cpu_baseline or m1 is None) else cpu_baseline_w4(N, K)
     head = m1 if m1 is not None else dec
     line = {
@@ -310,7 +350,8 @@ def main():
                                 else "decode attention b8@4k, 24/4 heads, D=128, block 16"),
                    "rotation_sets": head["rotation_sets"]},
         "roofline": {"bound": "hbm", "achieved": head["GBps_kernel"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": head["frac_kernel"], "traffic": None},
+                     "unit": "GB/s", "frac": head["frac_kernel"],
+                     "traffic": MEASURED_TRAFFIC["w4_gemv_M1" if m1 is not None else "decode_b8_4k"]},
         "cpu_baseline": cpu,
         "legs": legs,
     }
@@ -318,12 +359,13 @@ def main():
         pf = legs["prefill_cfg3"]
         line["roofline_prefill_cfg3"] = {"bound": "mfma", "achieved": pf["TFLOPs_kernel"],
                                          "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                         "frac": pf["frac_kernel"], "traffic": None}
+                                         "frac": pf["frac_kernel"],
+                                         "traffic": MEASURED_TRAFFIC["prefill_cfg3"]}
     if dec is not None:
         line["roofline_decode_b8_4k"] = {"bound": "hbm", "achieved": dec["GBps_kernel"],
                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                          "frac": dec["frac_kernel"], "us_per_layer": dec["us_kernel"],
-                                         "traffic": None}
+                                         "traffic": MEASURED_TRAFFIC["decode_b8_4k"]}
     print(json.dumps(line))
 
 

@@ -592,10 +592,10 @@ extern "C" int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
     switch (g_variant) {
-        case 1: hipLaunchKernelGGL((decode_kernel<8, 2, 1>), grid, dim3(8 * 64), 0, st, P); break;
-        case 2: hipLaunchKernelGGL((decode_kernel<4, 4, 1>), grid, dim3(4 * 64), 0, st, P); break;
-        case 3: hipLaunchKernelGGL((decode_kernel<4, 4, 2>), grid, dim3(4 * 64), 0, st, P); break;
-        default: hipLaunchKernelGGL((decode_kernel<8, 4, 1>), grid, dim3(8 * 64), 0, st, P); break;
+        case 1: launch_kernel(decode_kernel<8, 2, 1>, grid, dim3(8 * 64), 0, st, P); break;
+        case 2: launch_kernel(decode_kernel<4, 4, 1>, grid, dim3(4 * 64), 0, st, P); break;
+        case 3: launch_kernel(decode_kernel<4, 4, 2>, grid, dim3(4 * 64), 0, st, P); break;
+        default: launch_kernel(decode_kernel<8, 4, 1>, grid, dim3(8 * 64), 0, st, P); break;
     }
     return finish_launch();
 }

@@ -1,4 +1,4 @@
-/* Host-only diagnostics exported by libfp8kv_amd.so for the test suite (not part of the drop-in
+/* Host-only diagnostics exported by libfp8kv_amd.so for the tests and the benchmark (not part of the drop-in
  * ABI in include/fp8kv_amd.h).  They run no GPU code. */
 #ifndef FP8KV_DIAG_H
 #define FP8KV_DIAG_H
@@ -15,13 +15,20 @@ int fp8kv_h4mv_audit(int N, int K, int M);
  * depth (0 and 0 = the built-in defaults).  Affects later launches and audits. */
 void fp8kv_h4mv_tune(int target_waves, int depth);
 
-/* Tuning hook for sweeps of the decode attention launch: waves per workgroup (4 or 8) and the
- * workgroup count its split planner aims for (0 = default 512).  Affects later launches. */
+/* Tuning hook for sweeps of the decode attention launch: kernel variant index (0 = default: 8 waves,
+ * 4 groups of 16 keys per wave) and the workgroup count its split planner aims for (0 = default
+ * 256).  Affects later launches. */
 void fp8kv_decode_tune(int waves, int target_wgs);
 
 /* Tuning hook for sweeps of the prefill attention launch: index of the (waves, row-sets per wave,
  * LDS ring depth) shape to use for every GQA, or -1 for the per-GQA default. */
 void fp8kv_prefill_tune(int shape);
+
+/* Measurement hook: the next kernel launched by this host thread through any entry point records
+ * start_event / stop_event (hipEvent_t, either may be NULL) at its own start and end, via
+ * hipExtLaunchKernel.  hipEventElapsedTime between them is then the kernel's execution time.
+ * The events are used once; a rejected call leaves them armed for the next launch. */
+void fp8kv_time_next_launch(void* start_event, void* stop_event);
 
 #ifdef __cplusplus
 }

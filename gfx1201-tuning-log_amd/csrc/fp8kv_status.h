@@ -1,6 +1,7 @@
 // Status codes and small host helpers shared by the C-ABI entry points.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <cstdint>
 #include "fp8kv_amd.h"
 
@@ -22,6 +23,21 @@ inline int finish_launch() {
     if (e == hipSuccess) return FP8KV_OK;
     g_last_hip_error = (int)e;
     return FP8KV_ERR_LAUNCH;
+}
+
+// Events armed by fp8kv_time_next_launch() for the next kernel this host thread launches.
+extern thread_local hipEvent_t g_time_start;
+extern thread_local hipEvent_t g_time_stop;
+
+// Every kernel of the library is launched through here.  hipExtLaunchKernel stamps the armed
+// events with the dispatch's own start and end, so a timed launch reports the kernel's execution
+// time (what a kernel trace reports), not the time between two markers queued around it.
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes,
+                          hipStream_t stream, Args... args) {
+    hipEvent_t a = g_time_start, b = g_time_stop;
+    g_time_start = g_time_stop = nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, stream, a, b, 0, static_cast<KArgs>(args)...);
 }
 
 __host__ __device__ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }

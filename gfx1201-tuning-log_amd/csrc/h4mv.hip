@@ -32,6 +32,8 @@ namespace fp8kv {
 
 thread_local int g_last_status = FP8KV_OK;
 thread_local int g_last_hip_error = 0;
+thread_local hipEvent_t g_time_start = nullptr;
+thread_local hipEvent_t g_time_stop = nullptr;
 
 namespace h4mv_detail {
 
@@ -441,12 +443,12 @@ void launch_with(const Plan& p, const void* W, const void* St, const void* Xb, v
     const dim3 grid((unsigned)((N + kRowsPerWG - 1) / kRowsPerWG));
     const dim3 block(64 * WAVES);
     if (p.xlds)
-        hipLaunchKernelGGL((h4mv_kernel<WAVES, U, true, OutT>), grid, block, p.lds_bytes, s,
+        launch_kernel(h4mv_kernel<WAVES, U, true, OutT>, grid, block, p.lds_bytes, s,
                            static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St),
                            static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M,
                            p.groups_per_wave);
     else
-        hipLaunchKernelGGL((h4mv_kernel<WAVES, U, false, OutT>), grid, block, 0, s,
+        launch_kernel(h4mv_kernel<WAVES, U, false, OutT>, grid, block, 0, s,
                            static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St),
                            static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M,
                            p.groups_per_wave);
@@ -504,7 +506,7 @@ void launch_stream_x(const StreamPlan& p, const void* W, const void* St, const v
     const dim3 grid((unsigned)((N + kRowsPerWG - 1) / kRowsPerWG));
     const dim3 block(64 * p.nw);
 #define FP8KV_D(D) \
-    case D: hipLaunchKernelGGL((h4mv_stream_kernel<MMAX, XSTAGE, D, OutT>), grid, block, p.lds, s, \
+    case D: launch_kernel(h4mv_stream_kernel<MMAX, XSTAGE, D, OutT>, grid, block, p.lds, s, \
                                static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
                                static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M, p.per); \
             break;
@@ -669,6 +671,12 @@ extern "C" void h4mv_launch(const void* W, const void* St, const void* Xb, void*
 }
 
 extern "C" int fp8kv_last_status(void) { return fp8kv::g_last_status; }
+
+extern "C" void fp8kv_time_next_launch(void* start_event, void* stop_event)
+{
+    fp8kv::g_time_start = static_cast<hipEvent_t>(start_event);
+    fp8kv::g_time_stop = static_cast<hipEvent_t>(stop_event);
+}
 
 extern "C" int fp8kv_last_hip_error(void) { return fp8kv::g_last_hip_error; }
 

@@ -474,14 +474,14 @@ int launch(const Params& P0, int num_seqs, int max_query_len, hipStream_t stream
     const dim3 block(64 * sh.waves);
     begin_launch();
     switch (si) {
-        case 0: hipLaunchKernelGGL((prefill_kernel<4, 3, 4>), grid, block, 0, stream, P); break;
-        case 1: hipLaunchKernelGGL((prefill_kernel<4, 3, 6>), grid, block, 0, stream, P); break;
-        case 2: hipLaunchKernelGGL((prefill_kernel<8, 2, 4>), grid, block, 0, stream, P); break;
-        case 3: hipLaunchKernelGGL((prefill_kernel<4, 4, 4>), grid, block, 0, stream, P); break;
-        case 4: hipLaunchKernelGGL((prefill_kernel<4, 2, 4>), grid, block, 0, stream, P); break;
-        case 6: hipLaunchKernelGGL((prefill_kernel<6, 2, 4>), grid, block, 0, stream, P); break;
-        case 7: hipLaunchKernelGGL((prefill_kernel<8, 2, 4>), grid, block, 0, stream, P); break;
-        default: hipLaunchKernelGGL((prefill_kernel<4, 1, 4>), grid, block, 0, stream, P); break;
+        case 0: launch_kernel(prefill_kernel<4, 3, 4>, grid, block, 0, stream, P); break;
+        case 1: launch_kernel(prefill_kernel<4, 3, 6>, grid, block, 0, stream, P); break;
+        case 2: launch_kernel(prefill_kernel<8, 2, 4>, grid, block, 0, stream, P); break;
+        case 3: launch_kernel(prefill_kernel<4, 4, 4>, grid, block, 0, stream, P); break;
+        case 4: launch_kernel(prefill_kernel<4, 2, 4>, grid, block, 0, stream, P); break;
+        case 6: launch_kernel(prefill_kernel<6, 2, 4>, grid, block, 0, stream, P); break;
+        case 7: launch_kernel(prefill_kernel<8, 2, 4>, grid, block, 0, stream, P); break;
+        default: launch_kernel(prefill_kernel<4, 1, 4>, grid, block, 0, stream, P); break;
     }
     return finish_launch();
 }
