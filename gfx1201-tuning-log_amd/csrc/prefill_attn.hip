@@ -424,6 +424,382 @@ prefill_kernel(Params P)
     }
 }
 
+// ---- key-split kernel ---------------------------------------------------------------------------
+// For a GQA that splits into NG groups of RS heads (gqa = NG * RS, RS row-sets per wave): a
+// workgroup of 8 waves owns the pair of 16-token blocks (r, n16 - 1 - r) of one kv head and
+// processes them one after the other, the longer first.  For one block, wave w takes head group
+// w / NR and, of every window of NR x TPW key tiles (NR = 8 / NG), the TPW tiles of residue
+// w % NR: every wave converts each of its tiles once for RS row-sets, and two waves share each
+// SIMD.  The ring holds two windows; window i + 1 is copied (each wave issuing one 1 KB copy of
+// every tile) while window i is consumed, and one barrier per window publishes it.  At the end
+// of a block the NR partial (m, l, o) states of each head group merge in LDS in a fixed order:
+// the common max first, then residue 0 stores its rescaled o and l, residues 1 .. NR - 2 add
+// theirs in turn, and residue NR - 1 adds its own in registers, normalises and writes the output.
+constexpr int kSplitWaves = 8;
+
+constexpr int kStageFloats = 8 * 64 * 4 + 64;        // one row-set: o [n][lane][4], then l [lane]
+
+// Running-max floor of the key-split kernel: finite, so that no -inf ever enters the softmax
+// arithmetic (exp2(kMaxFloor - m) is 0 for any real row max m, and a row that has seen no key
+// keeps l = 0 and o = 0).
+constexpr float kMaxFloor = -1e30f;
+
+// max(a, b) without the NaN-quieting canonicalisation the compiler adds to fmaxf of values that
+// come from lane swaps (the scores are never NaN: finite fp8 and bf16 inputs).
+__device__ __forceinline__ float max_raw(float a, float b)
+{
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ float max_xor16_32_raw(float v)
+{
+    const uint32_t b = __float_as_uint(v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    const float m = max_raw(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const uint32_t c = __float_as_uint(m);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+    return max_raw(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+
+// Online softmax of the RS row-sets of one 32-key tile.  sc holds raw scores S^T (lane (q, p):
+// keys 16 kg + 4 p + e of query row q), -inf where masked; qk = |sm_scale * k_scale| * log2(e),
+// at least 1e-30 (a negative scale is folded into Q's sign), so the row max of the raw scores
+// times qk is the max of the scaled ones and each probability is exp2(fma(s, qk, -m)).  m_run
+// starts at kMaxFloor.  Returns the bf16 probabilities P^T as MFMA B fragments in pb.
+template <int RS>
+__device__ __forceinline__ void softmax_tile(const f32x4_t (&sc)[RS][2], float (&m_run)[RS],
+                                             float (&l_run)[RS], f32x4_t (&o)[RS][8], float qk,
+                                             u32x4_t (&pb)[RS])
+{
+#pragma unroll
+    for (int j = 0; j < RS; ++j) {
+        const float m4a = fmaxf(fmaxf(sc[j][0][0], sc[j][0][1]), fmaxf(sc[j][0][2], sc[j][0][3]));
+        const float m4b = fmaxf(fmaxf(sc[j][1][0], sc[j][1][1]), fmaxf(sc[j][1][2], sc[j][1][3]));
+        const float mraw = max_xor16_32_raw(fmaxf(m4a, m4b));
+        const float mc = mraw * qk;                    // -inf for a fully masked row (qk > 0)
+        // Lazy rescale: the accumulators move to a new reference max only when the row max
+        // grew by more than kRescaleSlack (then probabilities stay below 2^kRescaleSlack).
+        const bool need = mc > m_run[j] + kRescaleSlack;
+        if (__any(need)) {
+            const float m_new = need ? mc : m_run[j];
+            const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
+            l_run[j] *= alpha;
+#pragma unroll
+            for (int n = 0; n < 8; ++n) o[j][n] *= alpha;
+            m_run[j] = m_new;
+        }
+        const float nm = -m_run[j];
+        float p[2][4];
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                p[kg][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][kg][e], qk, nm));
+        l_run[j] += ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
+        pb[j][0] = pack_bf16x2(p[0][0], p[0][1]);
+        pb[j][1] = pack_bf16x2(p[0][2], p[0][3]);
+        pb[j][2] = pack_bf16x2(p[1][0], p[1][1]);
+        pb[j][3] = pack_bf16x2(p[1][2], p[1][3]);
+    }
+}
+
+template <int RS, int NG, int TPW>
+__global__ void __launch_bounds__(kSplitWaves * 64)
+prefill_split_kernel(Params P)
+{
+    constexpr int W = kSplitWaves;
+    constexpr int RW = 2;                                  // ring windows
+    constexpr int NR = W / NG;
+    constexpr int NT = NR * TPW;                           // tiles per window
+    static_assert(NG * NR == W && RS >= 1 && NT <= 64, "split shape");
+    constexpr int kWinBytes = NT * kTileBytes;
+    constexpr int kRingBytes = RW * kWinBytes;
+    constexpr int kStageBytes = NR > 1 ? NG * RS * kStageFloats * 4 : 0;
+    // The merge stage reuses the ring: it is written only after every wave has finished its
+    // last tile, and the next block's copies start only after the stage has been read.
+    __shared__ __align__(16) unsigned char ring[kRingBytes > kStageBytes ? kRingBytes : kStageBytes];
+    __shared__ float stage_m[NR > 1 ? NG * NR * RS * 16 : 4];
+    float* const stage = reinterpret_cast<float*>(ring);
+
+    const int lin = blockIdx.x, seq = blockIdx.z;
+    int kh, rank;
+    if (P.xcd_map) {
+        const int xcd = lin & 7, per = 8 / P.hkv;
+        kh = xcd % P.hkv;
+        rank = (lin >> 3) * per + xcd / P.hkv;
+    } else {
+        kh = lin % P.hkv;
+        rank = lin / P.hkv;
+    }
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave / NR;
+    const int res = wave % NR;
+    const int lr = lane & 15;
+    const int lp = lane >> 4;
+
+    int q_begin, qlen, q0;
+    if (P.cu_q) {
+        q_begin = P.cu_q[seq];
+        qlen = P.cu_q[seq + 1] - q_begin;
+        q0 = P.seq_lens[seq] - qlen;
+    } else {
+        q_begin = 0;
+        qlen = P.qlen_host;
+        q0 = P.q0_host;
+    }
+    const int n16 = (qlen + 15) >> 4;
+    const int tb = P.ntb_grid - 1 - rank;
+    if (tb < 0 || tb >= ((n16 + 1) >> 1) || q0 < 0) return;      // whole workgroup, before any barrier
+    const int blk_a = tb, blk_b = n16 - 1 - tb;
+    const int nphase = blk_b > blk_a ? 2 : 1;
+    const int32_t* btrow = P.bt + (int64_t)seq * P.bt_stride;
+    const float qk_signed = P.sm_scale * P.k_scale[0] * kLog2e;
+    const float qk = fmaxf(fabsf(qk_signed), 1e-30f);         // > 0: -inf * qk stays -inf
+    const uint32_t qflip = qk_signed < 0.f ? 0x80008000u : 0u;   // negate Q (exact in bf16)
+    const float vs = P.v_scale[0];
+
+    // This wave's copy instruction of every tile: K rows (waves 0-3) or V rows (waves 4-7)
+    // 8 (wave & 3) .. +7, lane (row, chunk) as chosen by dma_lane_rc.
+    const bool dma_v = wave >= 4;
+    int dma_r, dma_c;
+    dma_lane_rc(dma_v, lane, dma_r, dma_c);
+    const int dma_rk = 8 * (wave & 3) + dma_r;                     // key offset within a tile
+    const uint8_t* dma_base = dma_v ? P.v + (int64_t)kh * P.sv2 : P.k + (int64_t)kh * P.sk2;
+    const int64_t dma_s0 = dma_v ? P.sv0 : P.sk0;
+    const uint64_t dma_s1 = (uint64_t)(dma_v ? P.sv1 : P.sk1);
+    const uint64_t dma_chunk = 16u * (uint32_t)dma_c;
+
+    for (int ph = 0; ph < nphase; ++ph) {
+        const int blk = ph == 0 ? blk_b : blk_a;
+        const int qpos0 = q0 + 16 * blk;
+        const int k_hi = q0 + min(16 * blk + 16, qlen);           // keys [0, k_hi)
+        const int ntiles = (k_hi + kBN - 1) / kBN;
+        const int nwin = (ntiles + NT - 1) / NT;
+
+        u32x4_t qf[RS][4];
+        const int tok = 16 * blk + lr;
+        const bool tok_ok = tok < qlen;
+#pragma unroll
+        for (int j = 0; j < RS; ++j) {
+            const u32x4_t zero = {0u, 0u, 0u, 0u};
+            const __bf16* qrow = P.q + (int64_t)(q_begin + (tok_ok ? tok : 0)) * P.q_stride +
+                                 (int64_t)(kh * P.gqa + grp * RS + j) * kD;
+            qf[j][0] = tok_ok ? load_16(qrow + 16 * lp) : zero;
+            qf[j][1] = tok_ok ? load_16(qrow + 16 * lp + 8) : zero;
+            qf[j][2] = tok_ok ? load_16(qrow + 64 + 16 * lp) : zero;
+            qf[j][3] = tok_ok ? load_16(qrow + 64 + 16 * lp + 8) : zero;
+        }
+        wait_vmcnt<0>();
+#pragma unroll
+        for (int j = 0; j < RS; ++j)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) qf[j][st] ^= qflip;
+
+        // Block ids for this wave's copy instruction of each tile of window wi (its 8 rows lie
+        // in one 16-key group, hence one cache block; index clamped to the last key): lane u
+        // loads the id for tile u of the window, one window ahead of the copies.  With a ring of
+        // two windows the wait for window i's copies also covers this load (issued after them).
+        int bids = 0;
+        auto load_bids = [&](int wi) {
+            const int key0 = min((wi * NT + lane) * kBN + 8 * (wave & 3), k_hi - 1);
+            bids = lane < NT ? btrow[key0 >> P.pshift] : 0;
+        };
+        // Copies of tiles u0 .. u1 - 1 of window wi (keys >= k_hi fetch key k_hi - 1; the causal
+        // mask removes them).
+        auto issue_window = [&](int wi, int u0, int u1) {
+#pragma unroll
+            for (int u = u0; u < u1; ++u) {
+                const int t = wi * NT + u;
+                if (t < ntiles) {
+                    int key = t * kBN + dma_rk;
+                    if (t * kBN + kBN > k_hi) key = min(key, k_hi - 1);
+                    const uint64_t off = (uint64_t)(uint32_t)(key & (P.pblk - 1)) * dma_s1 + dma_chunk;
+                    const int64_t b = __builtin_amdgcn_readlane(bids, u);
+                    dma16_untracked(dma_base + b * dma_s0 + off,
+                                    ring + (wi % RW) * kWinBytes + u * kTileBytes + wave * 1024);
+                }
+            }
+        };
+#pragma unroll
+        for (int wi = 0; wi < RW - 1; ++wi)
+            if (wi < nwin) {
+                load_bids(wi);
+                issue_window(wi, 0, NT);
+            }
+        if (RW - 1 < nwin) load_bids(RW - 1);
+
+        float m_run[RS], l_run[RS];
+        f32x4_t o[RS][8];
+#pragma unroll
+        for (int j = 0; j < RS; ++j) {
+            m_run[j] = kMaxFloor;
+            l_run[j] = 0.f;
+#pragma unroll
+            for (int n = 0; n < 8; ++n) o[j][n] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        }
+
+        for (int i = 0; i < nwin; ++i) {
+            // Everything this wave has in flight: window i's copies and the block ids of window
+            // i + 1.  The barrier then publishes window i and frees window i - 1's slot.
+            wait_vmcnt<0>();
+            lds_barrier();
+            const bool more = i + RW - 1 < nwin;
+
+#pragma unroll
+            for (int v = 0; v < TPW; ++v) {
+                // The next window's copies go out in TPW parts, one before each tile, so that the
+                // copy traffic of the eight waves spreads over the window instead of queueing
+                // behind the barrier.
+                if (more) issue_window(i + RW - 1, v * NT / TPW, (v + 1) * NT / TPW);
+                const int tw = res * TPW + v;                    // tile within the window
+                const int t = i * NT + tw;
+                if (t >= ntiles) continue;
+                const int k0 = t * kBN;
+                const unsigned char* buf = ring + (i % RW) * kWinBytes + tw * kTileBytes;
+
+                u32x4_t kf[2][4];
+#pragma unroll
+                for (int kg = 0; kg < 2; ++kg) {
+                    const int row = 16 * kg + lr;
+                    const unsigned char* kb = buf + (row >> 3) * 1024;
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+                        const u32x2_t raw = *reinterpret_cast<const u32x2_t*>(
+                            kb + 16 * k_slot(row & 7, (st >> 1) * 4 + lp) + 8 * (st & 1));
+                        kf[kg][st] = __builtin_bit_cast(u32x4_t, fp8x8_to_bf16x8(raw[0], raw[1]));
+                    }
+                }
+                f32x4_t sc[RS][2];
+#pragma unroll
+                for (int j = 0; j < RS; ++j)
+#pragma unroll
+                    for (int kg = 0; kg < 2; ++kg) {
+                        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int st = 0; st < 4; ++st)
+                            acc = mfma16x16x32_bf16(as_bf16x8(kf[kg][st]), as_bf16x8(qf[j][st]), acc);
+                        sc[j][kg] = acc;
+                    }
+                if (k0 + kBN - 1 > qpos0) {                        // tile reaches past the first row
+                    const int qpos = qpos0 + lr;
+#pragma unroll
+                    for (int j = 0; j < RS; ++j)
+#pragma unroll
+                        for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (k0 + 16 * kg + 4 * lp + e > qpos) sc[j][kg][e] = neg_inf();
+                }
+                u32x4_t pb[RS];
+                softmax_tile<RS>(sc, m_run, l_run, o, qk, pb);
+
+                // V^T fragments in two halves (fragment 4w + i comes from dword w of each row)
+                // to keep the register peak low; lane (c, p) transposes d = 8c .. 8c+7.
+                u32x2_t vr[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int row = (jj < 4 ? 0 : 16) + 4 * lp + (jj & 3);
+                    const unsigned char* vb = buf + 4096 + (row >> 3) * 1024;
+                    vr[jj] = *reinterpret_cast<const u32x2_t*>(vb + 16 * v_slot(row & 7, lr >> 1) + 8 * (lr & 1));
+                }
+#pragma unroll
+                for (int w = 0; w < 2; ++w) {
+                    u32x4_t vf[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t a = vr[2 * k][w], b = vr[2 * k + 1][w];
+                        const uint32_t x = __builtin_amdgcn_perm(b, a, 0x05010400u);
+                        const uint32_t y = __builtin_amdgcn_perm(b, a, 0x07030602u);
+                        vf[0][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, false));
+                        vf[1][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, true));
+                        vf[2][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(y, 1.0f, false));
+                        vf[3][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(y, 1.0f, true));
+                    }
+#pragma unroll
+                    for (int j = 0; j < RS; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            o[j][4 * w + q] = mfma16x16x32_bf16(as_bf16x8(vf[q]), as_bf16x8(pb[j]), o[j][4 * w + q]);
+                }
+            }
+            // Block ids for the next window's copies, after this iteration's LDS reads so that
+            // no LDS wait in the tile work has to cover the scalar loads.
+            if (i + RW < nwin) load_bids(i + RW);
+        }
+
+        // ---- merge the NR partial states of each head group, then normalise and store ----------
+        if constexpr (NR > 1) {
+            // m_run is the same in the four lane groups of a query row: lanes 0..15 publish it.
+            if (lp == 0) {
+#pragma unroll
+                for (int j = 0; j < RS; ++j) stage_m[((grp * NR + res) * RS + j) * 16 + lr] = m_run[j];
+            }
+            lds_barrier();
+#pragma unroll
+            for (int j = 0; j < RS; ++j) {
+                float mg = kMaxFloor;
+#pragma unroll
+                for (int r = 0; r < NR; ++r) mg = fmaxf(mg, stage_m[((grp * NR + r) * RS + j) * 16 + lr]);
+                const float f = __builtin_amdgcn_exp2f(m_run[j] - mg);
+                l_run[j] *= f;
+#pragma unroll
+                for (int n = 0; n < 8; ++n) o[j][n] *= f;
+            }
+            for (int r = 0; r < NR - 1; ++r) {
+                if (res == r) {
+#pragma unroll
+                    for (int j = 0; j < RS; ++j) {
+                        float* s = stage + (grp * RS + j) * kStageFloats;
+#pragma unroll
+                        for (int n = 0; n < 8; ++n) {
+                            f32x4_t* p = reinterpret_cast<f32x4_t*>(s + (n * 64 + lane) * 4);
+                            if (r > 0) o[j][n] += *p;
+                            *p = o[j][n];
+                        }
+                        if (r > 0) l_run[j] += s[8 * 64 * 4 + lane];
+                        s[8 * 64 * 4 + lane] = l_run[j];
+                    }
+                }
+                lds_barrier();
+            }
+            if (res == NR - 1) {
+#pragma unroll
+                for (int j = 0; j < RS; ++j) {
+                    const float* s = stage + (grp * RS + j) * kStageFloats;
+#pragma unroll
+                    for (int n = 0; n < 8; ++n) o[j][n] += *reinterpret_cast<const f32x4_t*>(s + (n * 64 + lane) * 4);
+                    l_run[j] += s[8 * 64 * 4 + lane];
+                }
+            }
+        }
+        if (res == NR - 1) {
+#pragma unroll
+            for (int j = 0; j < RS; ++j) {
+                const float l = sum_xor16_32(l_run[j]);
+                if (!tok_ok) continue;
+                const float f = l > 0.f ? vs / l : 0.f;
+                __bf16* orow = P.out + (int64_t)(q_begin + tok) * P.o_stride +
+                               (int64_t)(kh * P.gqa + grp * RS + j) * kD + 32 * lp;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    u32x4_t w;
+                    w[0] = pack_bf16x2(o[j][0][e] * f, o[j][1][e] * f);
+                    w[1] = pack_bf16x2(o[j][2][e] * f, o[j][3][e] * f);
+                    w[2] = pack_bf16x2(o[j][4][e] * f, o[j][5][e] * f);
+                    w[3] = pack_bf16x2(o[j][6][e] * f, o[j][7][e] * f);
+                    *reinterpret_cast<u32x4_t*>(orow + 8 * e) = w;
+                }
+            }
+        }
+        // The next block's copies overwrite the ring, which holds the stage: every wave must be
+        // done with its final stage reads above.
+        if (ph + 1 < nphase) lds_barrier();
+    }
+}
+
 // Launch shapes: (waves, row-sets per wave, ring depth).  nb token blocks of 16 per workgroup is
 // the largest count whose nb * GQA row-sets fit waves * RS.
 struct Shape {
@@ -432,13 +808,27 @@ struct Shape {
 constexpr Shape kShapes[] = {{4, 3, 4, 0}, {4, 3, 6, 0}, {8, 2, 4, 0}, {4, 4, 4, 0}, {4, 2, 4, 0},
                              {4, 1, 4, 0}, {6, 2, 4, 1}, {8, 2, 4, 1}};
 constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
-int g_shape = -1;              // -1: choose by GQA
+
+// Key-split shapes (RS row-sets per wave, NG head groups) for gqa = RS * NG.
+struct SplitShape {
+    int rs, ng;
+};
+constexpr SplitShape kSplitShapes[] = {{3, 2}, {3, 4}, {2, 2}, {2, 4}, {2, 8}};
+constexpr int kNumSplitShapes = sizeof(kSplitShapes) / sizeof(kSplitShapes[0]);
+int g_shape = -1;              // -1: choose by GQA; kNumShapes + s: key-split shape s
+
+inline int split_shape_for(int gqa)
+{
+    for (int s = 0; s < kNumSplitShapes; ++s)
+        if (kSplitShapes[s].rs * kSplitShapes[s].ng == gqa) return s;
+    return -1;
+}
 
 // Default shape per GQA (measured at configs[3], GQA 6: 8 waves x 2 row-sets with paired token
 // blocks 184 us; 4 x 3 unpaired 251 us; 8 x 2 unpaired 190 us).
 inline int choose_shape(int gqa)
 {
-    if (g_shape >= 0) return g_shape;
+    if (g_shape >= 0 && g_shape < kNumShapes) return g_shape;
     if (gqa <= 1) return 5;                       // 4 waves x 1 row-set, 4 token blocks
     if (gqa <= 2) return 4;                       // 4 waves x 2 row-sets, 4 token blocks
     if (gqa <= 8) return 7;                       // 8 waves x 2 row-sets (paired blocks when nb = 2)
@@ -453,8 +843,42 @@ inline int plan_nb(int gqa, const Shape& s)
     return nb;
 }
 
+int launch_split(const Params& P0, int ss, int num_seqs, int max_query_len, hipStream_t stream)
+{
+    Params P = P0;
+    P.nb = 2;
+    P.paired = 1;
+    const int n16 = (max_query_len + 15) / 16;
+    int ntb = (n16 + 1) / 2;
+    if (ntb == 0) return FP8KV_OK;
+    P.xcd_map = (P.hkv <= 8 && 8 % P.hkv == 0) ? 1 : 0;
+    if (P.xcd_map) {
+        const int per = 8 / P.hkv;
+        ntb = (ntb + per - 1) / per * per;
+    }
+    P.ntb_grid = ntb;
+    const dim3 grid((unsigned)(ntb * P.hkv), 1u, (unsigned)num_seqs);
+    const dim3 block(64 * kSplitWaves);
+    begin_launch();
+    switch (ss) {
+        case 0: launch_kernel(prefill_split_kernel<3, 2, 2>, grid, block, 0, stream, P); break;
+        case 1: launch_kernel(prefill_split_kernel<3, 4, 2>, grid, block, 0, stream, P); break;
+        case 2: launch_kernel(prefill_split_kernel<2, 2, 2>, grid, block, 0, stream, P); break;
+        case 3: launch_kernel(prefill_split_kernel<2, 4, 2>, grid, block, 0, stream, P); break;
+        default: launch_kernel(prefill_split_kernel<2, 8, 2>, grid, block, 0, stream, P); break;
+    }
+    return finish_launch();
+}
+
 int launch(const Params& P0, int num_seqs, int max_query_len, hipStream_t stream)
 {
+    // Key-split kernel when the GQA has a split shape, unless the tuning hook forces another.
+    const int ss = split_shape_for(P0.gqa);
+    if (g_shape >= kNumShapes) {
+        if (g_shape - kNumShapes == ss) return launch_split(P0, ss, num_seqs, max_query_len, stream);
+    } else if (g_shape < 0 && ss >= 0) {
+        return launch_split(P0, ss, num_seqs, max_query_len, stream);
+    }
     Params P = P0;
     const int si = choose_shape(P.gqa);
     const Shape sh = kShapes[si];
@@ -573,7 +997,7 @@ extern "C" int fp8kv_prefill_attn(const void* q, int64_t q_row_stride,
 
 extern "C" void fp8kv_prefill_tune(int shape)
 {
-    g_shape = (shape >= 0 && shape < kNumShapes) ? shape : -1;
+    g_shape = (shape >= 0 && shape < kNumShapes + kNumSplitShapes) ? shape : -1;
 }
 
 extern "C" int fp8kv_prefill_attn_varlen(const void* q, int64_t q_row_stride,

@@ -178,6 +178,7 @@ def test_rejects_bad_arguments():
 
 
 SHAPE_CAP = [12, 12, 16, 16, 8, 4, 12, 16]      # waves x row-sets of each launch shape
+SPLIT_GQA = [6, 12, 4, 8, 16]                   # GQA of each key-split shape (tuning index 8 + s)
 
 
 @pytest.mark.parametrize("shape", [0, 1, 2, 3, 4, 5, 6, 7])
@@ -195,5 +196,21 @@ def test_every_launch_shape(shape):
             _check_single(200, 0, HQ=hq, HKV=4, seed=shape * 100 + hq + 1)     # odd block count
         cap = SHAPE_CAP[shape]
         _check_varlen([40, 97], [3, 200], seed=shape + 50, HQ=4 * min(6, cap), HKV=4)
+    finally:
+        lib.fp8kv_prefill_tune(-1)
+
+
+@pytest.mark.parametrize("split", range(len(SPLIT_GQA)))
+def test_every_split_shape(split):
+    """Each key-split shape (row-sets per wave x head groups, keys split over the rest of the 8
+    waves) at its GQA: odd and even token-block counts, a tail block, varlen, block size 32."""
+    lib = _lib.load()
+    gqa = SPLIT_GQA[split]
+    try:
+        lib.fp8kv_prefill_tune(8 + split)
+        _check_single(161, 45, HQ=4 * gqa, HKV=4, seed=split * 10)
+        _check_single(200, 0, HQ=4 * gqa, HKV=4, seed=split * 10 + 1)
+        _check_single(513, 1000, HQ=2 * gqa, HKV=2, seed=split * 10 + 2, PBLK=32, layout="engine")
+        _check_varlen([40, 97, 300], [3, 200, 0], seed=split + 60, HQ=4 * gqa, HKV=4)
     finally:
         lib.fp8kv_prefill_tune(-1)
