@@ -170,6 +170,40 @@ def bench_decode(ctx, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK=16, poo
     return r
 
 
+def cache_write_bytes(T: int, HKV: int, D: int) -> int:
+    """Algorithmic bytes of one KV-cache write: bf16 K and V in, fp8 K and V out, the slots."""
+    return T * HKV * D * (2 + 2 + 1 + 1) + 8 * T
+
+
+def bench_cache_write(T: int, steps: int, warmup: int, HKV=4, D=128, PBLK=16, pool_blocks=5060,
+                      seed=0):
+    """fp8 KV-cache write of T new tokens into rotated engine-layout layer pools."""
+    import torch
+    from fp8kv_amd import ops, workloads
+    dev = torch.device("cuda")
+    pool_bytes = pool_blocks * HKV * PBLK * 2 * D
+    n_sets = max(8, -(-2 * (256 << 20) // pool_bytes) + 1)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    pools = [workloads.engine_views(torch.empty(pool_blocks, HKV, PBLK, 2 * D, dtype=torch.uint8,
+                                                device=dev), D) for _ in range(n_sets)]
+    key = torch.randn(T, HKV, D, device=dev, generator=g).to(torch.bfloat16)
+    value = torch.randn(T, HKV, D, device=dev, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(pool_blocks * PBLK, device=dev, generator=g)[:T].to(torch.int64)
+    ks = torch.tensor([0.01], device=dev)
+    vs = torch.tensor([0.01], device=dev)
+
+    def launch(i):
+        kc, vc = pools[i]
+        ops.cache_write(key, value, kc, vc, slots, ks, vs)
+
+    wall, per = time_launches(launch, n_sets, steps, warmup)
+    del pools
+    torch.cuda.empty_cache()
+    r = _summary(wall, per, cache_write_bytes(T, HKV, D))
+    r["tokens"] = T
+    return r
+
+
 def bench_copy(steps: int, warmup: int, nbytes: int = 256 << 20):
     """A plain device-to-device copy of ``nbytes`` (torch's copy kernel): the practical HBM
     read+write rate beside the kernels, and the calibration launch for the traffic counters."""
@@ -296,8 +330,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--legs", default="w4,decode,prefill,copy",
-                    help="comma list of legs to run (w4, decode, prefill, copy)")
+    ap.add_argument("--legs", default="w4,decode,prefill,cache,copy",
+                    help="comma list of legs to run (w4, decode, prefill, cache, copy)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one GPU; "
@@ -329,6 +363,9 @@ def main():
         legs["prefill_cfg3"] = bench_prefill([2048], [2048], pf_steps, max(2, args.warmup // 4))
         legs["prefill_cfg3_varlen_4x512"] = bench_prefill([512] * 4, [0] * 4, pf_steps,
                                                           max(2, args.warmup // 4), seed=1)
+    if "cache" in legs_wanted:
+        legs["cache_write_2048"] = bench_cache_write(2048, max(5, args.steps // 4), max(2, args.warmup // 4))
+        legs["cache_write_8"] = bench_cache_write(8, args.steps, args.warmup)
     if "copy" in legs_wanted:
         legs["copy_256MiB"] = bench_copy(max(5, args.steps // 4), max(2, args.warmup // 4))
     cpu = None if (args.no_cpu_baseline or m1 is None) else cpu_baseline_w4(N, K)

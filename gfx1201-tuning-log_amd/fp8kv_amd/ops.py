@@ -229,3 +229,37 @@ def prefill_attention_varlen(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
         int(max_query_len), _stream_ptr(q))
     _lib.check("fp8kv_prefill_attn_varlen", st)
     return out
+
+
+# ------------------------------------------------------------------------------ fp8 KV-cache write
+
+def cache_write(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                v_cache: torch.Tensor, slot_mapping: torch.Tensor, k_scale, v_scale) -> None:
+    """Quantise key / value [T, HKV, D] bf16 to e4m3fn (x / scale, SATFINITE) and write token i
+    at slot_mapping[i] (negative: skipped) of the paged caches [NB, PBLK, HKV, D] (fp8 views with
+    any block / slot / head strides, the layouts the attention wrappers take).  The semantics of
+    vLLM's reshape_and_cache_flash with an fp8 cache."""
+    for t, n in ((key, "key"), (value, "value")):
+        _require(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 3 and t.stride(2) == 1
+                 and t.stride(1) == t.shape[2], f"{n} must be bf16 [T, HKV, D] with contiguous heads")
+    _require(key.shape == value.shape, "key and value must have the same shape")
+    _fp8_cache_check(k_cache, "k_cache")
+    _fp8_cache_check(v_cache, "v_cache")
+    _require(k_cache.shape[1:] == v_cache.shape[1:] and k_cache.shape[2:] == key.shape[1:],
+             "caches must be [NB, PBLK, HKV, D] matching key")
+    _require(slot_mapping.is_cuda and slot_mapping.dtype == torch.int64 and slot_mapping.dim() == 1
+             and slot_mapping.shape[0] == key.shape[0] and slot_mapping.stride(0) == 1,
+             "slot_mapping must be an int64 device tensor [T]")
+    dev = key.device
+    ks = _scale_tensor(k_scale, dev)
+    vs = _scale_tensor(v_scale, dev)
+    T, HKV, D = key.shape
+    lib = _lib.load()
+    st = lib.fp8kv_cache_write(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(),
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
+        slot_mapping.data_ptr(), ks.data_ptr(), vs.data_ptr(), T, HKV, D, k_cache.shape[1],
+        _stream_ptr(key))
+    _lib.check("fp8kv_cache_write", st)

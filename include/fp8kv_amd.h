@@ -158,6 +158,38 @@ int fp8kv_prefill_attn_varlen(const void* q, int64_t q_row_stride,
                               int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
                               int block_size, int max_query_len, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * fp8-e4m3 KV-cache write: quantise new K and V rows and scatter them into the paged cache.
+ *
+ *   k_cache[block, slot, h, d] = e4m3fn( float(key[i, h, d]) / k_scale )   (V likewise)
+ *   for token i whose s = slot_mapping[i] >= 0: block = s / block_size, slot = s % block_size;
+ *   negative slots are padding and write nothing.  The division is fp32 and correctly rounded,
+ *   the conversion rounds to nearest even, finite values and +-inf saturate to +-448, NaN stays
+ *   NaN (0x7F / 0xFF, sign kept).
+ *
+ *   key, value    bf16 [num_tokens, num_kv_heads, head_size], row strides key_row_stride /
+ *                 value_row_stride (elements, multiples of 8), heads contiguous, 16-byte aligned
+ *   k_cache       fp8 bytes at k_cache + block*sk0 + slot*sk1 + h*sk2 + d (strides in bytes,
+ *                 multiples of 16, cache 16-byte aligned); v_cache likewise with sv0..sv2
+ *                 (multiples of 8): the layouts fp8kv_decode_attn reads, standalone or engine
+ *   slot_mapping  int64 [num_tokens]; k_scale, v_scale fp32 device scalars
+ *   head_size % 16 == 0, block_size a power of two.
+ *
+ * Replaces: vLLM's reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping,
+ * "fp8", k_scale, v_scale) - the kernel reshape_and_cache_kernel_flash the reference's engine
+ * runs before each attention call (profiling/prof_h4mv.txt:9, profiling/prof_prefill.txt:23) -
+ * for the per-tensor fp8 cache that vllm-fp8kv/fp8kv_override.py:82-85 reads.
+ */
+int fp8kv_cache_write(const void* key, int64_t key_row_stride,
+                      const void* value, int64_t value_row_stride,
+                      void* k_cache, void* v_cache,
+                      int64_t sk0, int64_t sk1, int64_t sk2,
+                      int64_t sv0, int64_t sv1, int64_t sv2,
+                      const int64_t* slot_mapping,
+                      const float* k_scale, const float* v_scale,
+                      int num_tokens, int num_kv_heads, int head_size, int block_size,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -102,3 +102,31 @@ def test_decode_split_planner(lib):
     for ns, hkv, ctx in [(1, 1, 100000), (64, 8, 8192), (1, 4, 17), (300, 8, 4096)]:
         n = lib.fp8kv_decode_num_splits(ns, hkv, ctx)
         assert 1 <= n <= 256
+
+
+# fp8kv_cache_write: every call below is rejected before any HIP call (fake pointers).
+CW_OK = [A, 512, A, 512, A, A, 8192, 512, 128, 8192, 512, 128, A, A, A, 4, 4, 128, 16, None]
+
+
+@pytest.mark.parametrize("idx,val,code", [
+    (17, 120, 2),              # head_size % 16 != 0
+    (18, 24, 2),               # block size not a power of two
+    (6, 8200, 3),              # K block stride not a multiple of 16
+    (9, 8196, 3),              # V block stride not a multiple of 8
+    (0, A + 8, 3),             # key not 16-byte aligned
+    (1, 100, 3),               # key row stride not a multiple of 8
+    (1, 256, 1),               # key row stride shorter than a token row
+    (12, None, 1),             # no slot mapping
+    (15, -1, 1),               # negative token count
+    (16, 0, 1),                # no kv heads
+])
+def test_cache_write_rejects_before_launch(lib, idx, val, code):
+    args = list(CW_OK)
+    args[idx] = val
+    assert lib.fp8kv_cache_write(*args) == code
+
+
+def test_cache_write_zero_tokens_is_a_no_op(lib):
+    args = list(CW_OK)
+    args[15] = 0
+    assert lib.fp8kv_cache_write(*args) == 0
