@@ -204,6 +204,110 @@ def bench_cache_write(T: int, steps: int, warmup: int, HKV=4, D=128, PBLK=16, po
     return r
 
 
+# the 28-layer decode step at batch 8 (per layer: the four MXFP4 linears at M = 8 and
+# the fp8 decode attention over 8 sequences of 4096 tokens, 24/4 heads).
+STACK_LINEARS = [("qkv", 4096, 3584), ("o", 3584, 3072), ("gate_up", 37888, 3584), ("down", 3584, 18944)]
+STACK_LAYERS = 28
+
+
+def bench_stack(steps: int, warmup: int, layers: int = STACK_LAYERS, M: int = 8, ctx: int = 4096,
+                HQ: int = 24, HKV: int = 4, D: int = 128, PBLK: int = 16):
+    """Kernel-only decode step of configs[4]: for every layer the four matvecs and the decode
+    attention, each layer with its own weights and KV pool (4.4 GB in all, far above the MALL).
+    Inputs are synthetic and not chained (the elementwise glue between the kernels is not part of
+    the path), so a step is exactly the 5 x layers hot-path launches.  Timed eagerly and as one
+    captured HIP graph replayed per step; tokens/s = M / step time."""
+    import torch
+    from fp8kv_amd import ops
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(4)
+    nbl = ctx // PBLK
+    W, St, X, Y = [], [], {}, {}
+    for _, N, K in STACK_LINEARS:
+        X[(N, K)] = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        Y[(N, K)] = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    kv, bts = [], []
+    for _ in range(layers):
+        W.append([torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=dev, generator=g)
+                  for _, N, K in STACK_LINEARS])
+        St.append([torch.randint(119, 124, (N, K // 32), dtype=torch.uint8, device=dev, generator=g)
+                   for _, N, K in STACK_LINEARS])
+        pool = torch.randint(0, 256, (M * nbl, HKV, PBLK, 2 * D), dtype=torch.uint8, device=dev,
+                             generator=g)
+        pool[(pool & 0x7F) == 0x7F] = 0x3C
+        kv.append(pool)
+        bts.append(torch.randperm(M * nbl, device=dev, generator=g).to(torch.int32).view(M, nbl))
+    q = torch.randn(M, HQ, D, device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    qsl = torch.arange(M + 1, dtype=torch.int32, device=dev)
+    sl = torch.full((M,), ctx, dtype=torch.int32, device=dev)
+    ks = torch.tensor([0.01], device=dev)
+    vs = torch.tensor([0.01], device=dev)
+    nsplit = ops.decode_num_splits(M, HKV, ctx)
+    scratch = ops.decode_scratch(ops.decode_scratch_bytes(M, HQ, HKV, nsplit, D), dev)
+    views = [(pool[:, :, :, :D].transpose(1, 2).view(torch.float8_e4m3fn),
+              pool[:, :, :, D:].transpose(1, 2).view(torch.float8_e4m3fn)) for pool in kv]
+
+    def step():
+        for li in range(layers):
+            for j, (_, N, K) in enumerate(STACK_LINEARS):
+                ops.h4mv(X[(N, K)], W[li][j], St[li][j], out=Y[(N, K)])
+                if j == 0:
+                    kc, vc = views[li]
+                    ops.decode_attention(q, kc, vc, out, qsl, sl, bts[li], ks, vs, 1 / math.sqrt(D),
+                                         num_splits=nsplit, scratch=scratch)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    eager_ms = t0.elapsed_time(t1) / steps
+
+    def attention_only():
+        for li in range(layers):
+            kc, vc = views[li]
+            ops.decode_attention(q, kc, vc, out, qsl, sl, bts[li], ks, vs, 1 / math.sqrt(D),
+                                 num_splits=nsplit, scratch=scratch)
+
+    def graph_ms_of(fn):
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            fn()                                        # warm the capture stream once
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=cap):
+                fn()
+        torch.cuda.current_stream().wait_stream(cap)
+        torch.cuda.synchronize()
+        for _ in range(max(1, warmup // 2)):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0.record()
+        for _ in range(steps):
+            graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        del graph
+        return t0.elapsed_time(t1) / steps
+
+    graph_ms = graph_ms_of(step)
+    attn_ms = graph_ms_of(attention_only)
+    nbytes = layers * (sum(w4_bytes(N, K, M) for _, N, K in STACK_LINEARS)
+                       + decode_bytes([ctx] * M, HQ, HKV, D, PBLK))
+    return {"layers": layers, "batch": M, "launches_per_step": 5 * layers,
+            "us_step_eager": round(eager_ms * 1e3, 1), "us_step_graph": round(graph_ms * 1e3, 1),
+            "tok_s_graph": round(M / (graph_ms * 1e-3), 1), "tok_s_eager": round(M / (eager_ms * 1e-3), 1),
+            "us_per_layer_decode_attention_graph": round(attn_ms * 1e3 / layers, 3),
+            "bytes": nbytes, "GBps_graph": round(nbytes / (graph_ms * 1e-3) / 1e9, 1),
+            "frac_graph": round(nbytes / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_copy(steps: int, warmup: int, nbytes: int = 256 << 20):
     """A plain device-to-device copy of ``nbytes`` (torch's copy kernel): the practical HBM
     read+write rate beside the kernels, and the calibration launch for the traffic counters."""
@@ -330,8 +434,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--legs", default="w4,decode,prefill,cache,copy",
-                    help="comma list of legs to run (w4, decode, prefill, cache, copy)")
+    ap.add_argument("--legs", default="w4,decode,prefill,cache,stack,copy",
+                    help="comma list of legs to run (w4, decode, prefill, cache, stack, copy)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one GPU; "
@@ -366,10 +470,16 @@ def main():
     if "cache" in legs_wanted:
         legs["cache_write_2048"] = bench_cache_write(2048, max(5, args.steps // 4), max(2, args.warmup // 4))
         legs["cache_write_8"] = bench_cache_write(8, args.steps, args.warmup)
+    if "stack" in legs_wanted:
+        legs["stack_cfg4_28_layers_b8"] = bench_stack(max(3, args.steps // 20), max(2, args.warmup // 10))
     if "copy" in legs_wanted:
         legs["copy_256MiB"] = bench_copy(max(5, args.steps // 4), max(2, args.warmup // 4))
     cpu = None if (args.no_cpu_baseline or m1 is None) else cpu_baseline_w4(N, K)
     head = m1 if m1 is not None else dec
+    if head is None:                     # only auxiliary legs asked for: report them alone
+        print(json.dumps({"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup, "legs": legs}))
+        return
     line = {
         "metric": METRIC,
         "value": head["GBps_step"],

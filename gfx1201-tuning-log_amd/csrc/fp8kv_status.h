@@ -29,13 +29,18 @@ inline int finish_launch() {
 extern thread_local hipEvent_t g_time_start;
 extern thread_local hipEvent_t g_time_stop;
 
-// Every kernel of the library is launched through here.  hipExtLaunchKernel stamps the armed
-// events with the dispatch's own start and end, so a timed launch reports the kernel's execution
-// time (what a kernel trace reports), not the time between two markers queued around it.
+// Every kernel of the library is launched through here: an ordinary launch, or, when events are
+// armed, hipExtLaunchKernel, which stamps them with the dispatch's own start and end, so a timed
+// launch reports the kernel's execution time (what a kernel trace reports), not the time between
+// two markers queued around it.
 template <typename... KArgs, typename... Args>
 inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes,
                           hipStream_t stream, Args... args) {
     hipEvent_t a = g_time_start, b = g_time_stop;
+    if (a == nullptr && b == nullptr) {
+        hipLaunchKernelGGL(kernel, grid, block, lds_bytes, stream, static_cast<KArgs>(args)...);
+        return;
+    }
     g_time_start = g_time_stop = nullptr;
     hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, stream, a, b, 0, static_cast<KArgs>(args)...);
 }

@@ -27,6 +27,7 @@ SIGNATURES: dict[str, tuple] = {
     "h4mv_launch": (None, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
     "h4mv_launch_status": (_c_i, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
     "h4mv_f32_launch_status": (_c_i, [_c_vp] * 4 + [_c_i] * 3 + [_c_vp]),
+    "h4mv_repack_scales": (_c_i, [_c_vp, _c_vp, _c_i, _c_i, _c_vp]),
     # paged fp8 decode attention (csrc/decode_attn.hip)
     "fp8kv_decode_num_splits": (_c_i, [_c_i] * 3),
     "fp8kv_decode_scratch_bytes": (_c_sz, [_c_i] * 5),

@@ -19,9 +19,21 @@ def _require(cond: bool, msg: str) -> None:
         raise ValueError(msg)
 
 
-def repack_scales(weight_scale: torch.Tensor) -> torch.Tensor:
-    """Checkpoint scales [K/32, N] -> kernel layout [N, K/32] (h4mv/fp8kv_hipw4.py:32-43)."""
-    return weight_scale.t().contiguous()
+def repack_scales(weight_scale: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Checkpoint scales uint8 [K/32, N] -> kernel layout [N, K/32] on the device
+    (h4mv_repack_scales; the reference's weight_scale.t().contiguous(), h4mv/fp8kv_hipw4.py:32-43)."""
+    _require(weight_scale.is_cuda and weight_scale.dim() == 2 and weight_scale.is_contiguous()
+             and weight_scale.element_size() == 1, "weight_scale must be a contiguous 1-byte [K/32, N] device tensor")
+    G, N = weight_scale.shape
+    if out is None:
+        out = torch.empty((N, G), dtype=weight_scale.dtype, device=weight_scale.device)
+    _require(out.shape == (N, G) and out.is_contiguous() and out.element_size() == 1
+             and out.device == weight_scale.device, "out must be a contiguous [N, K/32] byte tensor")
+    lib = _lib.load()
+    st = lib.h4mv_repack_scales(weight_scale.data_ptr(), out.data_ptr(), N, 32 * G,
+                                _stream_ptr(weight_scale))
+    _lib.check("h4mv_repack_scales", st)
+    return out
 
 
 def h4mv(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor,

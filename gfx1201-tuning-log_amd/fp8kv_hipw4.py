@@ -8,8 +8,9 @@ attribute instead would recurse - and re-registers the op's CUDA implementation 
 implementation takes the fast path when the reference's gate holds (:70-76): x is a contiguous
 2-D bf16 tensor with 1 <= M <= FP8KV_HIPW4_MAX_M (default 4; the kernel accepts up to 16),
 K % 32 == 0, N >= 8, weight_scale has K / 32 rows and the weight pointer is 16-byte aligned.  It
-then repacks weight_scale [K/32, N] -> [N, K/32] once per tensor (cached by data pointer and
-shape, cache cleared above 512 entries, never during graph capture: :32-43) and calls
+then repacks weight_scale [K/32, N] -> [N, K/32] once per tensor with the library's
+h4mv_repack_scales (cached by data pointer and shape, cache cleared above 512 entries, never
+during graph capture: :32-43) and calls
 ``h4mv_launch`` of libfp8kv_amd.so through ctypes with the reference's exact binding (:21-23,
 81-83), returning a fresh bf16 [M, N] tensor (bias is applied outside, :9-10).  Anything else,
 or any exception, runs the stolen body (:91-94).
@@ -50,13 +51,22 @@ def load_launcher(path: str | None = None):
     return lib.h4mv_launch
 
 
-class ScaleRepack:
-    """weight_scale [K/32, N] -> contiguous [N, K/32], cached by (data_ptr, shape)."""
+def _device_repack(s):
+    from fp8kv_amd import ops
+    return ops.repack_scales(s)
 
-    def __init__(self, is_capturing, limit: int = 512):
+
+class ScaleRepack:
+    """weight_scale [K/32, N] -> contiguous [N, K/32], cached by (data_ptr, shape).
+
+    ``transpose`` does the repack: the library's h4mv_repack_scales (a device kernel, the default)
+    or, in tests on fake tensors, any callable with the same result."""
+
+    def __init__(self, is_capturing, limit: int = 512, transpose=_device_repack):
         self.cache: dict = {}
         self.is_capturing = is_capturing
         self.limit = limit
+        self.transpose = transpose
 
     def __call__(self, s):
         key = (s.data_ptr(), tuple(s.shape))
@@ -65,7 +75,7 @@ class ScaleRepack:
             return ent
         if self.is_capturing():
             return None                      # never allocate or launch helper work during capture
-        st = s.t().contiguous()
+        st = self.transpose(s)
         if len(self.cache) > self.limit:
             self.cache.clear()
         self.cache[key] = st

@@ -65,6 +65,12 @@ int h4mv_launch_status(const void* W, const void* St, const void* Xb, void* Out,
 int h4mv_f32_launch_status(const void* W, const void* St, const void* Xb, void* Out,
                            int N, int K, int M, void* stream);
 
+/* Load-time repack of the block scales for h4mv_launch: scale_nk[n, g] = scale_kn[g, n] for the
+ * checkpoint's weight_scale uint8 [K/32, N] (contiguous) into uint8 [N, K/32] (contiguous).
+ * K % 32 == 0.  Run it once per weight, outside graph capture.
+ * Replaces: the scale repack of h4mv/fp8kv_hipw4.py:32-43 (_st_for: weight_scale.t().contiguous()). */
+int h4mv_repack_scales(const void* scale_kn, void* scale_nk, int N, int K, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Paged fp8-e4m3 KV decode attention (one query token per sequence, split-context, one launch).
  *

@@ -130,3 +130,12 @@ def test_cache_write_zero_tokens_is_a_no_op(lib):
     args = list(CW_OK)
     args[15] = 0
     assert lib.fp8kv_cache_write(*args) == 0
+
+
+@pytest.mark.parametrize("args,code", [
+    ((0, A, 64, 64, None), 1),            # null input
+    ((A, A, 0, 64, None), 1),             # N = 0
+    ((A, A, 64, 48, None), 2),            # K % 32 != 0
+])
+def test_repack_scales_rejects_before_launch(lib, args, code):
+    assert lib.h4mv_repack_scales(*args) == code

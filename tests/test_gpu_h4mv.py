@@ -208,3 +208,29 @@ def test_oracle_and_kernel_against_reference_kernel(M):
     assert matvec.bf16_excess_error(y_ref_kernel, oracle_y) < BF16_EXCESS
     y = _run(case)
     assert np.all(np.abs(y - y_ref_kernel) <= matvec.bf16_ulp(oracle_y) * 1.0001)
+
+
+# --- load-time scale repack (h4mv_repack_scales) ------------------------------------------------
+
+@pytest.mark.parametrize("N,K", [(28672, 4096), (4096, 3584), (3584, 18944), (100, 96), (65, 32),
+                                 (1, 2048), (64, 64 * 32)])
+def test_repack_scales_is_the_transpose(N, K):
+    """Byte-exact against the oracle's restatement of weight_scale.t().contiguous()
+    (h4mv/fp8kv_hipw4.py:32-43); tile-edge shapes (N, K/32 not multiples of 64) included."""
+    g = torch.Generator().manual_seed(N + K)
+    S = torch.randint(0, 256, (K // 32, N), dtype=torch.uint8, generator=g)
+    out = ops.repack_scales(S.to(DEV))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), matvec.repack_scales(S.numpy()))
+
+
+def test_repack_then_matvec_matches_checkpoint_layout():
+    """The hook's path end to end: checkpoint scales [K/32, N] -> device repack -> h4mv equals the
+    oracle on the same checkpoint tensors."""
+    case = workloads.w4_case(N=1024, K=2048, M=4, seed=21)
+    S_kn = torch.from_numpy(np.ascontiguousarray(case["St"].numpy().T))   # checkpoint layout
+    st = ops.repack_scales(S_kn.to(DEV))
+    y = ops.h4mv(case["X"].to(DEV), case["W"].to(DEV), st, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = _oracle(case)
+    assert matvec.rel_to_max_error(y.cpu().numpy(), ref) < TOL

@@ -401,7 +401,7 @@ def test_hipw4_gate_rejections(monkeypatch, case):
 def test_hipw4_fast_path_and_repack_cache(monkeypatch):
     h = _hipw4(monkeypatch)
     launch = FakeLaunch()
-    repack = h.ScaleRepack(lambda: False)
+    repack = h.ScaleRepack(lambda: False, transpose=lambda t: t.t().contiguous())
     body_calls = []
     patched = h.make_patched(lambda *a: body_calls.append(a) or "body", launch, repack, 4, torch,
                              lambda: 1234)
@@ -420,7 +420,7 @@ def test_hipw4_fast_path_and_repack_cache(monkeypatch):
 def test_hipw4_capture_refuses_repack_and_falls_back(monkeypatch):
     h = _hipw4(monkeypatch)
     launch = FakeLaunch()
-    patched = h.make_patched(lambda *a: "body", launch, h.ScaleRepack(lambda: True), 4, torch, lambda: 0)
+    patched = h.make_patched(lambda *a: "body", launch, h.ScaleRepack(lambda: True, transpose=lambda t: t.t().contiguous()), 4, torch, lambda: 0)
     x, w, s = _lin()
     assert patched(x, w, s, None) == "body" and launch.calls == []
 
@@ -430,14 +430,16 @@ def test_hipw4_exception_falls_back(monkeypatch):
 
     def boom(*a):
         raise RuntimeError("launch failed")
-    patched = h.make_patched(lambda *a: "body", boom, h.ScaleRepack(lambda: False), 4, torch, lambda: 0)
+    patched = h.make_patched(lambda *a: "body", boom,
+                             h.ScaleRepack(lambda: False, transpose=lambda t: t.t().contiguous()),
+                             4, torch, lambda: 0)
     x, w, s = _lin()
     assert patched(x, w, s, None) == "body"
 
 
 def test_hipw4_repack_cache_limit(monkeypatch):
     h = _hipw4(monkeypatch)
-    rp = h.ScaleRepack(lambda: False, limit=3)
+    rp = h.ScaleRepack(lambda: False, limit=3, transpose=lambda t: t.t().contiguous())
     keep = [torch.zeros(2, 8, dtype=torch.uint8) for _ in range(6)]
     for t in keep:
         rp(t)
