@@ -198,33 +198,35 @@ constexpr int kDmaAux = 2;                    // streaming cache policy for the 
 struct WaveLds {
     int slot;        // bytes per ring slot
     int ring;        // DEPTH * slot
-    int scales;      // 16 rows * per * 16
+    int scales;      // 16 rt rows * per * 16
     int xs;          // staged activations (XSTAGE) or 0
     int total;
 };
 
-__host__ __device__ inline WaveLds wave_lds(int mmax, bool xstage, int depth, int per)
+__host__ __device__ inline WaveLds wave_lds(int mmax, bool xstage, int depth, int per, int rt)
 {
     WaveLds w;
-    w.slot = kStepCodeBytes + (xstage ? 0 : mmax * 1024);
+    w.slot = rt * kStepCodeBytes + (xstage ? 0 : mmax * 1024);
     w.ring = depth * w.slot;
-    w.scales = 16 * per * 16;
+    w.scales = 16 * rt * per * 16;
     w.xs = xstage ? mmax * per * 1024 : 0;
     w.total = w.ring + w.scales + w.xs;
     return w;
 }
 
 // ---- index math shared by the kernel and the host-side address audit --------------------------
-// Code copy instruction i (0..3) of a step: lane -> row 4 i + lane / 16 of the tile (clamped to
-// N - 1) and the 16-byte piece (lane % 16) ^ (row & 7); byte offset from the tile's first code byte.
+// Code copy instruction i (0 .. 4 rt - 1) of a step: lane -> row 4 i + lane / 16 of the
+// workgroup's 16 rt rows (clamped to N - 1) and the 16-byte piece (lane % 16) ^ (row & 7); byte
+// offset from the workgroup's first code byte.  Instruction i lands at 1024 i in the slot, so
+// row-tile t of the workgroup occupies bytes [4096 t, 4096 t + 4096) of it.
 __host__ __device__ inline uint32_t stream_w_lane_off(int n0, int N, int K, int lane, int i)
 {
     const int rr = 4 * i + (lane >> 4);
     const int rowc = (n0 + rr < N ? n0 + rr : N - 1) - n0;
     return (uint32_t)rowc * (uint32_t)(K >> 1) + 16u * (uint32_t)((lane & 15) ^ (rr & 7));
 }
-// Scale copy: segment t (0 .. 16 per - 1) = row t / per, step t % per of the wave's slice; byte
-// offset from St.  Segment t lands at 16 t in the wave's scale area.
+// Scale copy: segment t (0 .. 16 rt per - 1) = row t / per, step t % per of the wave's slice;
+// byte offset from St.  Segment t lands at 16 t in the wave's scale area.
 __host__ __device__ inline size_t stream_s_seg_off(int n0, int N, int K, int per, int step0, int t)
 {
     const int row = t / per, st = t % per;
@@ -242,46 +244,50 @@ __host__ __device__ inline size_t stream_x_off(int K, int M, int m, int gs, int 
 __host__ __device__ inline int stream_w_read_off(int r, int q, int u) { return 256 * r + 16 * ((q + 4 * u) ^ (r & 7)); }
 __host__ __device__ inline int stream_x_frag_off(int q, int u, int j) { return q * 64 + u * 256 + j * 16; }
 
-template <int MMAX, bool XSTAGE>
-constexpr int copies_per_step() { return 4 + (XSTAGE ? 0 : MMAX); }
+template <int MMAX, bool XSTAGE, int RT>
+constexpr int copies_per_step() { return 4 * RT + (XSTAGE ? 0 : MMAX); }
 
 // Wait until the oldest outstanding step has landed, leaving `ahead` younger steps in flight.
-template <int MMAX, bool XSTAGE, int A>
+template <int MMAX, bool XSTAGE, int RT, int A>
 __device__ __forceinline__ void wait_ahead_ct(int ahead)
 {
     if constexpr (A == 0) {
         wait_vmcnt<0>();
     } else {
-        if (ahead >= A) wait_vmcnt<A * copies_per_step<MMAX, XSTAGE>()>();
-        else wait_ahead_ct<MMAX, XSTAGE, A - 1>(ahead);
+        if (ahead >= A) wait_vmcnt<A * copies_per_step<MMAX, XSTAGE, RT>()>();
+        else wait_ahead_ct<MMAX, XSTAGE, RT, A - 1>(ahead);
     }
 }
 
-template <int MMAX, bool XSTAGE>
+template <int MMAX, bool XSTAGE, int RT>
 __device__ __forceinline__ void issue_step(unsigned char* slot, const uint8_t* wtile,
-                                           const unsigned char* xbytes, const uint32_t (&woff)[4],
+                                           const unsigned char* xbytes, const uint32_t (&woff)[4 * RT],
                                            int gs, int K, int M, int lane)
 {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4 * RT; ++i)
         __builtin_amdgcn_global_load_lds((const void*)(wtile + (size_t)gs * 16 + woff[i]),
                                          (lds_void_t*)(slot + i * 1024), 16, 0, kDmaAux);
     if constexpr (!XSTAGE) {
 #pragma unroll
         for (int m = 0; m < MMAX; ++m)
-            dma16_to_lds(xbytes + stream_x_off(K, M, m, gs, lane), slot + kStepCodeBytes + m * 1024);
+            dma16_to_lds(xbytes + stream_x_off(K, M, m, gs, lane), slot + RT * kStepCodeBytes + m * 1024);
     }
 }
 
-template <int MMAX, bool XSTAGE, int DEPTH, typename OutT>
-__global__ void __launch_bounds__(1024)
+// Several row tiles per workgroup need more registers than 16 waves per workgroup allow (128),
+// so those variants are launched with at most kMaxWavesRT waves.
+constexpr int kMaxWavesRT = 4;
+
+template <int MMAX, bool XSTAGE, int DEPTH, int RT, typename OutT>
+__global__ void __launch_bounds__(RT == 1 ? 1024 : 64 * kMaxWavesRT)
 h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
                    const __bf16* __restrict__ X, OutT* __restrict__ Out,
                    int N, int K, int M, int per)
 {
-    static_assert((DEPTH - 1) * copies_per_step<MMAX, XSTAGE>() < 64, "vmcnt holds at most 63");
+    static_assert((DEPTH - 1) * copies_per_step<MMAX, XSTAGE, RT>() < 64, "vmcnt holds at most 63");
     extern __shared__ __align__(16) unsigned char smem[];
-    const WaveLds L = wave_lds(MMAX, XSTAGE, DEPTH, per);
+    const WaveLds L = wave_lds(MMAX, XSTAGE, DEPTH, per, RT);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -289,7 +295,7 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
     const int r = lane & 15;
     const int q = lane >> 4;
     const int steps_total = K >> 9;
-    const int n0 = blockIdx.x * kRowsPerWG;
+    const int n0 = blockIdx.x * kRowsPerWG * RT;
     const bool col_ok = r < M;
 
     unsigned char* base = smem + wave * L.total;
@@ -301,15 +307,15 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
 
     const uint8_t* wtile = W + (size_t)n0 * (size_t)(K >> 1);
     const unsigned char* xbytes = reinterpret_cast<const unsigned char*>(X);
-    uint32_t woff[4];
+    uint32_t woff[4 * RT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) woff[i] = stream_w_lane_off(n0, N, K, lane, i);
+    for (int i = 0; i < 4 * RT; ++i) woff[i] = stream_w_lane_off(n0, N, K, lane, i);
 
     // ---- one-time copies: the wave's scale slice (and activation slice) ------------------------
     if (nsteps > 0) {
-        for (int t0 = 0; t0 < 16 * per; t0 += 64) {
+        for (int t0 = 0; t0 < 16 * RT * per; t0 += 64) {
             const int t = t0 + lane;
-            if (t < 16 * per && (t % per) < nsteps)
+            if (t < 16 * RT * per && (t % per) < nsteps)
                 dma16_to_lds(St + stream_s_seg_off(n0, N, K, per, step0, t), sarea + t0 * 16);
         }
         if constexpr (XSTAGE) {
@@ -323,15 +329,19 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
 #pragma unroll
     for (int s = 0; s < DEPTH; ++s)
         if (s < nsteps)
-            issue_step<MMAX, XSTAGE>(ring + s * L.slot, wtile, xbytes, woff, (step0 + s) * kStepGroups,
-                                     K, M, lane);
+            issue_step<MMAX, XSTAGE, RT>(ring + s * L.slot, wtile, xbytes, woff, (step0 + s) * kStepGroups,
+                                         K, M, lane);
 
     int rdoff[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) rdoff[u] = stream_w_read_off(r, q, u);
 
-    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f};
-    f32x4_t acc1 = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc0[RT], acc1[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        acc0[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        acc1[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    }
     u32x4_t xv[4][4];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -341,14 +351,19 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
     for (int s = 0; s < nsteps; ++s) {
         const int slot = s % DEPTH;
         unsigned char* sl = ring + slot * L.slot;
-        wait_ahead_ct<MMAX, XSTAGE, DEPTH - 1>(min(nsteps - 1 - s, DEPTH - 1));
-        const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(sarea + (r * per + s) * 16);
-        u32x4_t wv[4];
+        wait_ahead_ct<MMAX, XSTAGE, RT, DEPTH - 1>(min(nsteps - 1 - s, DEPTH - 1));
+        u32x4_t sv[RT];
+        u32x4_t wv[RT][4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) wv[u] = *reinterpret_cast<const u32x4_t*>(sl + rdoff[u]);
+        for (int t = 0; t < RT; ++t) {
+            sv[t] = *reinterpret_cast<const u32x4_t*>(sarea + ((16 * t + r) * per + s) * 16);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                wv[t][u] = *reinterpret_cast<const u32x4_t*>(sl + t * kStepCodeBytes + rdoff[u]);
+        }
         if (col_ok) {
             const unsigned char* xrow = XSTAGE ? xarea + (r * per + s) * 1024
-                                               : sl + kStepCodeBytes + r * 1024;
+                                               : sl + RT * kStepCodeBytes + r * 1024;
 #pragma unroll
             for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -358,61 +373,72 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
         // All fragments of this slot are in registers: refill it before the math.
         __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0)
         if (s + DEPTH < nsteps)
-            issue_step<MMAX, XSTAGE>(sl, wtile, xbytes, woff, (step0 + s + DEPTH) * kStepGroups,
-                                     K, M, lane);
+            issue_step<MMAX, XSTAGE, RT>(sl, wtile, xbytes, woff, (step0 + s + DEPTH) * kStepGroups,
+                                         K, M, lane);
+        // The activation fragments of this step serve every row tile of the workgroup.
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float sc = e8m0_to_f32((sv[u] >> (8 * q)) & 0xFFu);   // group q + 4u of row r
+        for (int t = 0; t < RT; ++t)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const bf16x8_t a = fp4x8_to_bf16x8(wv[u][j], sc);
-                if (u & 1) acc1 = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), acc1);
-                else       acc0 = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), acc0);
+            for (int u = 0; u < 4; ++u) {
+                const float sc = e8m0_to_f32((sv[t][u] >> (8 * q)) & 0xFFu);   // group q + 4u of row r
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bf16x8_t a = fp4x8_to_bf16x8(wv[t][u][j], sc);
+                    if (u & 1) acc1[t] = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), acc1[t]);
+                    else       acc0[t] = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), acc0[t]);
+                }
             }
-        }
     }
-    f32x4_t acc = acc0 + acc1;
+    f32x4_t acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = acc0[t] + acc1[t];
 
     // ---- reduce over the waves of the workgroup ------------------------------------------------
     if (nwaves > 1) {
         __syncthreads();                                   // every wave is done with its LDS
-        if (wave > 0) reinterpret_cast<f32x4_t*>(base)[lane] = acc;
+        if (wave > 0) {
+#pragma unroll
+            for (int t = 0; t < RT; ++t) reinterpret_cast<f32x4_t*>(base)[t * 64 + lane] = acc[t];
+        }
         __syncthreads();
         if (wave != 0) return;
         for (int w = 1; w < nwaves; ++w)
-            acc += reinterpret_cast<const f32x4_t*>(smem + w * L.total)[lane];
+#pragma unroll
+            for (int t = 0; t < RT; ++t)
+                acc[t] += reinterpret_cast<const f32x4_t*>(smem + w * L.total)[t * 64 + lane];
     }
 
     const int m = r;
     if (m >= M) return;
-    const int n = n0 + 4 * q;
     OutT* orow = Out + (size_t)m * (size_t)N;
-    const bool vec = n + 3 < N && ((N & 3) == 0) && aligned(Out, 4 * sizeof(OutT));
-    if constexpr (sizeof(OutT) == 2) {
-        if (vec) {
-            u32x2_t v = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
-            *reinterpret_cast<u32x2_t*>(orow + n) = v;
-            return;
-        }
-    } else {
-        if (vec) {
-            *reinterpret_cast<f32x4_t*>(orow + n) = acc;
-            return;
+    const bool vec_ok = ((N & 3) == 0) && aligned(Out, 4 * sizeof(OutT));
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        const int n = n0 + 16 * t + 4 * q;
+        if (n >= N) continue;
+        if (vec_ok && n + 3 < N) {
+            if constexpr (sizeof(OutT) == 2) {
+                u32x2_t v = {pack_bf16x2(acc[t][0], acc[t][1]), pack_bf16x2(acc[t][2], acc[t][3])};
+                *reinterpret_cast<u32x2_t*>(orow + n) = v;
+            } else {
+                *reinterpret_cast<f32x4_t*>(orow + n) = acc[t];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (n + i < N) orow[n + i] = (OutT)acc[t][i];
         }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (n + i < N) orow[n + i] = (OutT)acc[i];
 }
 
 // Waves per tile: enough tiles x waves to cover the GPU, at most 16 per workgroup and at most one
 // per step.
-inline int stream_waves(int N, int K, int target_waves)
+inline int stream_waves(int N, int K, int target_waves, int rt)
 {
-    const int tiles = (N + kRowsPerWG - 1) / kRowsPerWG;
+    const int tiles = (N + kRowsPerWG * rt - 1) / (kRowsPerWG * rt);
     const int steps = (K >> 5) / kStepGroups;
     int nw = (target_waves + tiles - 1) / tiles;
-    nw = max(1, min(nw, min(16, steps)));
+    nw = max(1, min(nw, min(rt == 1 ? 16 : kMaxWavesRT, steps)));
     return nw;
 }
 
@@ -461,39 +487,60 @@ constexpr size_t kLdsPerCU = 160 * 1024;
 // a two-slot ring (deeper rings measured slower at every cfg1/cfg4 shape).
 int g_target_waves = 0;
 int g_depth_override = 0;
+int g_rt_override = 0;
 
 inline int stream_mmax(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
 struct StreamPlan {
-    int mmax, depth, nw, per;
+    int mmax, depth, nw, per, rt;
     bool xstage;
     size_t lds;
 };
+
+// Row tiles (of 16) per workgroup: the activation copies of a step (M KB) then serve rt x 4 KB of
+// codes.  Two tiles for M >= 4 when that still gives >= 256 single-wave workgroups that all fit
+// on the GPU at once (LDS-limited); otherwise one (measured at cfg1: M = 8 18.9 -> 14.7 us,
+// M = 4 14.5 -> 13.8 us; two rounds of workgroups or fewer than 256 lose: gate+up 20.7 -> 21.4,
+// qkv 4.6 -> 5.8 us).  Four tiles measured slower at every shape (tuning hook only).
+inline int stream_rt(int N, int K, int M)
+{
+    if (g_rt_override) return g_rt_override;
+    if (M < 4) return 1;
+    const int tiles2 = (N + 2 * kRowsPerWG - 1) / (2 * kRowsPerWG);
+    if (tiles2 < 256) return 1;
+    const WaveLds w = wave_lds(stream_mmax(M), false, 2, K >> 9, 2);
+    const int per_cu = (int)(kLdsPerCU / (size_t)w.total);
+    return tiles2 <= 256 * per_cu ? 2 : 1;
+}
 
 // Plan for the streaming kernel, or false when (K, M) needs the register-path kernel.
 inline bool stream_plan(int N, int K, int M, StreamPlan& p)
 {
     if ((K & 511) != 0 || M > 8) return false;
     p.mmax = stream_mmax(M);
+    p.rt = stream_rt(N, K, M);
     const int steps_total = K >> 9;
-    const int tiles = (N + kRowsPerWG - 1) / kRowsPerWG;
-    const int target = g_target_waves > 0 ? g_target_waves : (tiles >= 1024 ? tiles : 4096);
-    int nreq = stream_waves(N, K, target);
+    const int tiles = (N + kRowsPerWG * p.rt - 1) / (kRowsPerWG * p.rt);
+    // Defaults (measured at cfg1 / cfg4): one tile per wave when the tiles alone fill the GPU
+    // (>= 1024 with one row tile, >= 256 with several), else a K split aiming at 4096 / rt waves.
+    const int target = g_target_waves > 0 ? g_target_waves
+                     : (tiles >= (p.rt == 1 ? 1024 : 256) ? tiles : 4096 / p.rt);
+    int nreq = stream_waves(N, K, target, p.rt);
     for (;;) {
         p.per = (steps_total + nreq - 1) / nreq;
         p.nw = (steps_total + p.per - 1) / p.per;
         p.xstage = p.mmax * p.per * 1024 <= kXStageMaxBytes;
-        const WaveLds w2 = wave_lds(p.mmax, p.xstage, 2, p.per);
+        const WaveLds w2 = wave_lds(p.mmax, p.xstage, 2, p.per, p.rt);
         if ((size_t)p.nw * w2.total <= kLdsPerCU || nreq == 1) break;
         nreq = std::max(1, nreq - 1);
     }
-    const int copies = 4 + (p.xstage ? 0 : p.mmax);
+    const int copies = 4 * p.rt + (p.xstage ? 0 : p.mmax);
     int depth = 2;
-    if (g_depth_override) depth = std::max(2, std::min(4, g_depth_override));
+    if (g_depth_override && p.rt == 1) depth = std::max(2, std::min(4, g_depth_override));
     while (depth > 2 && ((depth - 1) * copies >= 64 ||
-                         (size_t)p.nw * wave_lds(p.mmax, p.xstage, depth, p.per).total > kLdsPerCU))
+                         (size_t)p.nw * wave_lds(p.mmax, p.xstage, depth, p.per, p.rt).total > kLdsPerCU))
         --depth;
-    const WaveLds w = wave_lds(p.mmax, p.xstage, depth, p.per);
+    const WaveLds w = wave_lds(p.mmax, p.xstage, depth, p.per, p.rt);
     p.depth = depth;
     p.lds = (size_t)p.nw * w.total;
     return p.lds <= kLdsPerCU;
@@ -503,16 +550,22 @@ template <int MMAX, bool XSTAGE, typename OutT>
 void launch_stream_x(const StreamPlan& p, const void* W, const void* St, const void* Xb, void* Out,
                      int N, int K, int M, hipStream_t s)
 {
-    const dim3 grid((unsigned)((N + kRowsPerWG - 1) / kRowsPerWG));
+    const dim3 grid((unsigned)((N + kRowsPerWG * p.rt - 1) / (kRowsPerWG * p.rt)));
     const dim3 block(64 * p.nw);
-#define FP8KV_D(D) \
-    case D: launch_kernel(h4mv_stream_kernel<MMAX, XSTAGE, D, OutT>, grid, block, p.lds, s, \
-                               static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
-                               static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M, p.per); \
-            break;
-    switch (p.depth) {
-        FP8KV_D(2) FP8KV_D(3) FP8KV_D(4)
-        default: break;
+#define FP8KV_D(D, RT) \
+    launch_kernel(h4mv_stream_kernel<MMAX, XSTAGE, D, RT, OutT>, grid, block, p.lds, s, \
+                  static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
+                  static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M, p.per)
+    if (p.rt == 4) {
+        FP8KV_D(2, 4);
+    } else if (p.rt == 2) {
+        FP8KV_D(2, 2);
+    } else {
+        switch (p.depth) {
+            case 3: FP8KV_D(3, 1); break;
+            case 4: FP8KV_D(4, 1); break;
+            default: FP8KV_D(2, 1); break;
+        }
     }
 #undef FP8KV_D
 }
@@ -521,20 +574,14 @@ template <typename OutT>
 void launch_stream_m(const StreamPlan& p, const void* W, const void* St, const void* Xb, void* Out,
                      int N, int K, int M, hipStream_t s)
 {
-    if (p.xstage) {
-        switch (p.mmax) {
-            case 1: launch_stream_x<1, true, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-            case 2: launch_stream_x<2, true, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-            case 4: launch_stream_x<4, true, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-            default: launch_stream_x<8, true, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-        }
-    } else {
-        switch (p.mmax) {
-            case 1: launch_stream_x<1, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-            case 2: launch_stream_x<2, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-            case 4: launch_stream_x<4, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-            default: launch_stream_x<8, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-        }
+    // Activation staging (xstage) is planned only when kXStageMaxBytes allows it, which it
+    // currently does not, so only the per-step-copy variants are instantiated.
+    static_assert(kXStageMaxBytes == 0, "instantiate the xstage variants before enabling them");
+    switch (p.mmax) {
+        case 1: launch_stream_x<1, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+        case 2: launch_stream_x<2, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+        case 4: launch_stream_x<4, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+        default: launch_stream_x<8, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
     }
 }
 
@@ -573,22 +620,24 @@ namespace fp8kv { namespace h4mv_detail {
 int audit_stream(int N, int K, int M, const StreamPlan& p)
 {
     const int steps_total = K >> 9;
-    const int per = p.per, nw = p.nw, depth = p.depth, MMAX = p.mmax;
-    if (nw > 16 || nw * per < steps_total || (nw - 1) * per >= steps_total) return 2;
-    if (p.lds > kLdsPerCU || depth < 2 || depth > 4) return 3;
-    if ((depth - 1) * (4 + (p.xstage ? 0 : MMAX)) >= 64) return 3;
-    const WaveLds L = wave_lds(MMAX, p.xstage, depth, per);
+    const int per = p.per, nw = p.nw, depth = p.depth, MMAX = p.mmax, RT = p.rt;
+    if (RT != 1 && RT != 2 && RT != 4) return 3;
+    if (nw > (RT == 1 ? 16 : kMaxWavesRT) || nw * per < steps_total || (nw - 1) * per >= steps_total) return 2;
+    if (p.lds > kLdsPerCU || depth < 2 || depth > 4 || (RT > 1 && depth != 2)) return 3;
+    if ((depth - 1) * (4 * RT + (p.xstage ? 0 : MMAX)) >= 64) return 3;
+    const WaveLds L = wave_lds(MMAX, p.xstage, depth, per, RT);
     if ((size_t)nw * L.total != p.lds) return 3;
     const size_t wbytes = (size_t)N * (size_t)(K >> 1), sbytes = (size_t)N * (size_t)(K >> 5);
     const size_t xbytes = (size_t)M * (size_t)K * 2;
-    for (int tile = 0; tile * kRowsPerWG < N; ++tile) {
-        const int n0 = tile * kRowsPerWG;
+    const int rows = kRowsPerWG * RT;
+    for (int wg = 0; wg * rows < N; ++wg) {
+        const int n0 = wg * rows;
         for (int w = 0; w < nw; ++w) {
             const size_t wb = (size_t)w * L.total;
             const int step0 = w * per;
             const int nsteps = std::max(0, std::min(per, steps_total - step0));
             if (nsteps > 0) {
-                for (int t = 0; t < 16 * per; ++t) {          // one-time scale copies
+                for (int t = 0; t < 16 * RT * per; ++t) {     // one-time scale copies
                     if ((t % per) >= nsteps) continue;
                     if (stream_s_seg_off(n0, N, K, per, step0, t) + 16 > sbytes) return 6;
                     if (wb + L.ring + 16 * (size_t)t + 16 > wb + L.ring + L.scales) return 7;
@@ -605,31 +654,33 @@ int audit_stream(int N, int K, int M, const StreamPlan& p)
                 const int gs = (step0 + s) * kStepGroups;
                 const size_t slot = wb + (size_t)(s % depth) * L.slot;
                 for (int lane = 0; lane < 64; ++lane) {
-                    for (int i = 0; i < 4; ++i) {
+                    for (int i = 0; i < 4 * RT; ++i) {
                         const size_t g = (size_t)n0 * (K >> 1) + (size_t)gs * 16 + stream_w_lane_off(n0, N, K, lane, i);
                         if (g + 16 > wbytes) return 4;
-                        if (slot + i * 1024 + 16 * lane + 16 > slot + kStepCodeBytes) return 5;
+                        if (slot + i * 1024 + 16 * lane + 16 > slot + RT * kStepCodeBytes) return 5;
                     }
                     if (!p.xstage)
                         for (int m = 0; m < MMAX; ++m) {
                             if (stream_x_off(K, M, m, gs, lane) + 16 > xbytes) return 8;
-                            if (kStepCodeBytes + m * 1024 + 16 * lane + 16 > L.slot) return 9;
+                            if (RT * kStepCodeBytes + m * 1024 + 16 * lane + 16 > L.slot) return 9;
                         }
                     const int r = lane & 15, q = lane >> 4;
-                    if (L.ring + (size_t)(r * per + s) * 16 + 16 > (size_t)(L.ring + L.scales)) return 10;
-                    for (int u = 0; u < 4; ++u) {
-                        if (stream_w_read_off(r, q, u) + 16 > kStepCodeBytes) return 11;
+                    for (int t = 0; t < RT; ++t) {
+                        if (L.ring + (size_t)((16 * t + r) * per + s) * 16 + 16 > (size_t)(L.ring + L.scales)) return 10;
+                        for (int u = 0; u < 4; ++u)
+                            if (t * kStepCodeBytes + stream_w_read_off(r, q, u) + 16 > RT * kStepCodeBytes) return 11;
+                    }
+                    for (int u = 0; u < 4; ++u)
                         for (int j = 0; j < 4; ++j) {
                             if (r >= M) continue;
                             const size_t xo = p.xstage ? L.ring + L.scales + (size_t)(r * per + s) * 1024
-                                                       : (size_t)(s % depth) * L.slot + kStepCodeBytes + r * 1024;
+                                                       : (size_t)(s % depth) * L.slot + RT * kStepCodeBytes + r * 1024;
                             const size_t end = p.xstage ? (size_t)L.total : (size_t)(s % depth) * L.slot + L.slot;
                             if (xo + stream_x_frag_off(q, u, j) + 16 > end) return 12;
                         }
-                    }
                 }
             }
-            if (wb + 64 * 16 > p.lds) return 13;                // partial-tile exchange
+            if (wb + (size_t)RT * 64 * 16 > p.lds) return 13;    // partial-tile exchange
         }
     }
     return 0;
@@ -646,8 +697,9 @@ extern "C" int fp8kv_h4mv_audit(int N, int K, int M)
     return audit_stream(N, K, M, p);
 }
 
-extern "C" void fp8kv_h4mv_tune(int target_waves, int depth)
+extern "C" void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles)
 {
+    fp8kv::h4mv_detail::g_rt_override = (row_tiles == 1 || row_tiles == 2 || row_tiles == 4) ? row_tiles : 0;
     fp8kv::h4mv_detail::g_target_waves = target_waves > 0 ? target_waves : 0;
     fp8kv::h4mv_detail::g_depth_override = depth;
 }

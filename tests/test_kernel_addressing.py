@@ -29,3 +29,22 @@ def test_h4mv_stream_in_bounds_random_shapes(lib):
 def test_h4mv_register_path_shapes_are_reported(lib):
     for N, K, M in itertools.product([1, 64], [32, 96, 4128], [1, 9, 16]):
         assert lib.fp8kv_h4mv_audit(N, K, M) == 1
+
+
+@pytest.mark.parametrize("rt", [1, 2, 4])
+def test_h4mv_stream_in_bounds_every_row_tile_count(lib, rt):
+    """Every row-tile count the planner can pick (forced through the tuning hook), on the model
+    shapes and on random ones, including N not a multiple of 16 rt."""
+    rng = random.Random(rt)
+    try:
+        lib.fp8kv_h4mv_tune(0, 0, rt)
+        for N, K in CFG4_SHAPES:
+            for M in (1, 3, 8):
+                assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
+        for _ in range(120):
+            N = rng.choice([1, 15, 17, 33, 63, 65, 100, 1000, 4097]) + rng.randrange(0, 3)
+            K = 512 * rng.randrange(1, 41)
+            M = rng.randrange(1, 9)
+            assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
+    finally:
+        lib.fp8kv_h4mv_tune(0, 0, 0)
