@@ -12,9 +12,10 @@ extern "C" {
 int fp8kv_h4mv_audit(int N, int K, int M);
 
 /* Tuning hook for sweeps: waves per launch the matvec's K split aims for, a forced LDS ring depth
- * (one row tile only) and a forced row-tile count per workgroup (1, 2 or 4); 0 = the built-in
- * defaults.  Affects later launches and audits. */
-void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles);
+ * (one row tile only), a forced row-tile count per workgroup (1, 2 or 4) and the activation path
+ * (1: copies through LDS, 2: direct loads); 0 = the built-in defaults.  Affects later launches
+ * and audits. */
+void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode);
 
 /* Tuning hook for sweeps of the decode attention launch: kernel variant index (0 = default: 8 waves,
  * 4 groups of 16 keys per wave) and the workgroup count its split planner aims for (0 = default

@@ -177,21 +177,21 @@ h4mv_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
 //   * the wave's scale bytes (16 rows x per x 16 B) are copied once at the start, row by row, so
 //     consecutive lanes read consecutive bytes (per-step 16-byte scale pieces from 16 rows cost a
 //     measured 1 us per launch at cfg1);
-//   * activations: copied once per wave for all its steps when they fit (XSTAGE), else each slot
-//     carries MMAX KB of activation rows next to its codes;
+//   * activations: each slot carries MMAX KB of activation rows next to its codes; alternatively
+//     (XG, a tuning option, measured slower) every lane loads its activation fragments for step
+//     s + 1 straight from L2 into registers at the end of step s;
 //   * the waves of the workgroup meet once in LDS to add their partial tiles;
 //   * LDS code layout: row r at 256 r, 16-byte piece p at slot p ^ (r & 7), so the 16 lanes that
 //     read one piece index of 16 rows hit distinct bank groups;
 //   * copies complete out of the compiler's sight, so every wait is an explicit s_waitcnt vmcnt
 //     with the exact number of copy instructions still allowed in flight;
 //   * columns m >= M of the B operand only feed output columns that are never stored, so lanes
-//     r >= M neither read activations nor zero their registers.
+//     r >= M do not read activations from LDS (XG: they load row M - 1 again, so every wave issues
+//     the same number of loads per step and the explicit vmcnt counts stay exact).
 // ---------------------------------------------------------------------------------------------
 constexpr int kStepGroups = 16;
 constexpr int kStepCodeBytes = 16 * 256;
-constexpr int kXStageMaxBytes = 0;           // activation bytes per wave staged once (XSTAGE);
-                                             // measured: per-step copies from L2 cost less than
-                                             // the LDS (and so the waves per CU) staging takes
+constexpr int kXgLoads = 16;                 // XG: activation fragment loads per step and lane
 constexpr int kDmaAux = 2;                    // streaming cache policy for the code copies
 
 // LDS layout of one wave (bytes), shared by kernel, planner and audit.
@@ -199,18 +199,16 @@ struct WaveLds {
     int slot;        // bytes per ring slot
     int ring;        // DEPTH * slot
     int scales;      // 16 rt rows * per * 16
-    int xs;          // staged activations (XSTAGE) or 0
     int total;
 };
 
-__host__ __device__ inline WaveLds wave_lds(int mmax, bool xstage, int depth, int per, int rt)
+__host__ __device__ inline WaveLds wave_lds(int mmax, bool xg, int depth, int per, int rt)
 {
     WaveLds w;
-    w.slot = rt * kStepCodeBytes + (xstage ? 0 : mmax * 1024);
+    w.slot = rt * kStepCodeBytes + (xg ? 0 : mmax * 1024);
     w.ring = depth * w.slot;
     w.scales = 16 * rt * per * 16;
-    w.xs = xstage ? mmax * per * 1024 : 0;
-    w.total = w.ring + w.scales + w.xs;
+    w.total = w.ring + w.scales;
     return w;
 }
 
@@ -244,22 +242,24 @@ __host__ __device__ inline size_t stream_x_off(int K, int M, int m, int gs, int 
 __host__ __device__ inline int stream_w_read_off(int r, int q, int u) { return 256 * r + 16 * ((q + 4 * u) ^ (r & 7)); }
 __host__ __device__ inline int stream_x_frag_off(int q, int u, int j) { return q * 64 + u * 256 + j * 16; }
 
-template <int MMAX, bool XSTAGE, int RT>
-constexpr int copies_per_step() { return 4 * RT + (XSTAGE ? 0 : MMAX); }
+template <int MMAX, bool XG, int RT>
+constexpr int copies_per_step() { return 4 * RT + (XG ? 0 : MMAX); }
 
-// Wait until the oldest outstanding step has landed, leaving `ahead` younger steps in flight.
-template <int MMAX, bool XSTAGE, int RT, int A>
+// Wait until the oldest outstanding step has landed, leaving `ahead` younger steps in flight (and,
+// with XG, the activation loads of the current step, issued after all of them).
+template <int MMAX, bool XG, int RT, int A>
 __device__ __forceinline__ void wait_ahead_ct(int ahead)
 {
+    constexpr int extra = XG ? kXgLoads : 0;
     if constexpr (A == 0) {
-        wait_vmcnt<0>();
+        wait_vmcnt<extra>();
     } else {
-        if (ahead >= A) wait_vmcnt<A * copies_per_step<MMAX, XSTAGE, RT>()>();
-        else wait_ahead_ct<MMAX, XSTAGE, RT, A - 1>(ahead);
+        if (ahead >= A) wait_vmcnt<A * copies_per_step<MMAX, XG, RT>() + extra>();
+        else wait_ahead_ct<MMAX, XG, RT, A - 1>(ahead);
     }
 }
 
-template <int MMAX, bool XSTAGE, int RT>
+template <int MMAX, bool XG, int RT>
 __device__ __forceinline__ void issue_step(unsigned char* slot, const uint8_t* wtile,
                                            const unsigned char* xbytes, const uint32_t (&woff)[4 * RT],
                                            int gs, int K, int M, int lane)
@@ -268,7 +268,7 @@ __device__ __forceinline__ void issue_step(unsigned char* slot, const uint8_t* w
     for (int i = 0; i < 4 * RT; ++i)
         __builtin_amdgcn_global_load_lds((const void*)(wtile + (size_t)gs * 16 + woff[i]),
                                          (lds_void_t*)(slot + i * 1024), 16, 0, kDmaAux);
-    if constexpr (!XSTAGE) {
+    if constexpr (!XG) {
 #pragma unroll
         for (int m = 0; m < MMAX; ++m)
             dma16_to_lds(xbytes + stream_x_off(K, M, m, gs, lane), slot + RT * kStepCodeBytes + m * 1024);
@@ -279,15 +279,16 @@ __device__ __forceinline__ void issue_step(unsigned char* slot, const uint8_t* w
 // so those variants are launched with at most kMaxWavesRT waves.
 constexpr int kMaxWavesRT = 4;
 
-template <int MMAX, bool XSTAGE, int DEPTH, int RT, typename OutT>
+template <int MMAX, bool XG, int DEPTH, int RT, typename OutT>
 __global__ void __launch_bounds__(RT == 1 ? 1024 : 64 * kMaxWavesRT)
 h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
                    const __bf16* __restrict__ X, OutT* __restrict__ Out,
                    int N, int K, int M, int per)
 {
-    static_assert((DEPTH - 1) * copies_per_step<MMAX, XSTAGE, RT>() < 64, "vmcnt holds at most 63");
+    static_assert((DEPTH - 1) * copies_per_step<MMAX, XG, RT>() + (XG ? kXgLoads : 0) < 64,
+                  "vmcnt holds at most 63");
     extern __shared__ __align__(16) unsigned char smem[];
-    const WaveLds L = wave_lds(MMAX, XSTAGE, DEPTH, per, RT);
+    const WaveLds L = wave_lds(MMAX, XG, DEPTH, per, RT);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -301,7 +302,6 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
     unsigned char* base = smem + wave * L.total;
     unsigned char* ring = base;
     unsigned char* sarea = base + L.ring;
-    unsigned char* xarea = sarea + L.scales;
     const int step0 = wave * per;
     const int nsteps = max(0, min(per, steps_total - step0));
 
@@ -311,26 +311,20 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
 #pragma unroll
     for (int i = 0; i < 4 * RT; ++i) woff[i] = stream_w_lane_off(n0, N, K, lane, i);
 
-    // ---- one-time copies: the wave's scale slice (and activation slice) ------------------------
+    // ---- one-time copies: the wave's scale slice ------------------------------------------------
     if (nsteps > 0) {
         for (int t0 = 0; t0 < 16 * RT * per; t0 += 64) {
             const int t = t0 + lane;
             if (t < 16 * RT * per && (t % per) < nsteps)
                 dma16_to_lds(St + stream_s_seg_off(n0, N, K, per, step0, t), sarea + t0 * 16);
         }
-        if constexpr (XSTAGE) {
-            for (int s = 0; s < nsteps; ++s)
-                for (int m = 0; m < M; ++m)
-                    dma16_to_lds(xbytes + stream_x_off(K, M, m, (step0 + s) * kStepGroups, lane),
-                                 xarea + (m * per + s) * 1024);
-        }
     }
     // ---- fill the ring ------------------------------------------------------------------------
 #pragma unroll
     for (int s = 0; s < DEPTH; ++s)
         if (s < nsteps)
-            issue_step<MMAX, XSTAGE, RT>(ring + s * L.slot, wtile, xbytes, woff, (step0 + s) * kStepGroups,
-                                         K, M, lane);
+            issue_step<MMAX, XG, RT>(ring + s * L.slot, wtile, xbytes, woff, (step0 + s) * kStepGroups,
+                                     K, M, lane);
 
     int rdoff[4];
 #pragma unroll
@@ -343,15 +337,28 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
         acc1[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     }
     u32x4_t xv[4][4];
+    // XG: this lane's activation row (row M - 1 again for r >= M) and its loads of step s.
+    const unsigned char* xg_row = xbytes + (size_t)(r < M ? r : M - 1) * (size_t)K * 2;
+    auto load_x = [&](int s) {
+        const unsigned char* b = xg_row + (size_t)(step0 + s) * kStepGroups * 64;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) asm volatile("" : "=v"(xv[u][j]));   // columns m >= M: any value
+            for (int j = 0; j < 4; ++j) xv[u][j] = load_16(b + stream_x_frag_off(q, u, j));
+    };
+    if constexpr (XG) {
+        if (nsteps > 0) load_x(0);
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) asm volatile("" : "=v"(xv[u][j]));   // columns m >= M: any value
+    }
 
     for (int s = 0; s < nsteps; ++s) {
         const int slot = s % DEPTH;
         unsigned char* sl = ring + slot * L.slot;
-        wait_ahead_ct<MMAX, XSTAGE, RT, DEPTH - 1>(min(nsteps - 1 - s, DEPTH - 1));
+        wait_ahead_ct<MMAX, XG, RT, DEPTH - 1>(min(nsteps - 1 - s, DEPTH - 1));
         u32x4_t sv[RT];
         u32x4_t wv[RT][4];
 #pragma unroll
@@ -361,9 +368,8 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
             for (int u = 0; u < 4; ++u)
                 wv[t][u] = *reinterpret_cast<const u32x4_t*>(sl + t * kStepCodeBytes + rdoff[u]);
         }
-        if (col_ok) {
-            const unsigned char* xrow = XSTAGE ? xarea + (r * per + s) * 1024
-                                               : sl + RT * kStepCodeBytes + r * 1024;
+        if (!XG && col_ok) {
+            const unsigned char* xrow = sl + RT * kStepCodeBytes + r * 1024;
 #pragma unroll
             for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -373,8 +379,8 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
         // All fragments of this slot are in registers: refill it before the math.
         __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0)
         if (s + DEPTH < nsteps)
-            issue_step<MMAX, XSTAGE, RT>(sl, wtile, xbytes, woff, (step0 + s + DEPTH) * kStepGroups,
-                                         K, M, lane);
+            issue_step<MMAX, XG, RT>(sl, wtile, xbytes, woff, (step0 + s + DEPTH) * kStepGroups,
+                                     K, M, lane);
         // The activation fragments of this step serve every row tile of the workgroup.
 #pragma unroll
         for (int t = 0; t < RT; ++t)
@@ -388,6 +394,9 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
                     else       acc0[t] = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), acc0[t]);
                 }
             }
+        if constexpr (XG) {
+            if (s + 1 < nsteps) load_x(s + 1);
+        }
     }
     f32x4_t acc[RT];
 #pragma unroll
@@ -488,14 +497,24 @@ constexpr size_t kLdsPerCU = 160 * 1024;
 int g_target_waves = 0;
 int g_depth_override = 0;
 int g_rt_override = 0;
+int g_xg_override = 0;          // 1: activation copies through LDS, 2: direct activation loads
 
 inline int stream_mmax(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
 struct StreamPlan {
     int mmax, depth, nw, per, rt;
-    bool xstage;
+    bool xg;                    // activation fragments loaded straight from L2 (no LDS copies)
     size_t lds;
 };
+
+// Activation path: LDS copies by default.  Direct loads free the LDS the copies take, but measured
+// slower at every cfg1 / cfg4 shape (cfg1 M = 8: 18.6 -> 23.4 us, gate+up 20.4 -> 28.6 us: 16
+// per-lane loads per step cost more than M 1 KB copies), so they stay a tuning option.
+inline bool stream_xg(int M)
+{
+    (void)M;
+    return g_xg_override == 2;
+}
 
 // Row tiles (of 16) per workgroup: the activation copies of a step (M KB) then serve rt x 4 KB of
 // codes.  Two tiles for M >= 4 when that still gives >= 256 single-wave workgroups that all fit
@@ -508,7 +527,7 @@ inline int stream_rt(int N, int K, int M)
     if (M < 4) return 1;
     const int tiles2 = (N + 2 * kRowsPerWG - 1) / (2 * kRowsPerWG);
     if (tiles2 < 256) return 1;
-    const WaveLds w = wave_lds(stream_mmax(M), false, 2, K >> 9, 2);
+    const WaveLds w = wave_lds(stream_mmax(M), stream_xg(M), 2, K >> 9, 2);
     const int per_cu = (int)(kLdsPerCU / (size_t)w.total);
     return tiles2 <= 256 * per_cu ? 2 : 1;
 }
@@ -519,6 +538,7 @@ inline bool stream_plan(int N, int K, int M, StreamPlan& p)
     if ((K & 511) != 0 || M > 8) return false;
     p.mmax = stream_mmax(M);
     p.rt = stream_rt(N, K, M);
+    p.xg = stream_xg(M);
     const int steps_total = K >> 9;
     const int tiles = (N + kRowsPerWG * p.rt - 1) / (kRowsPerWG * p.rt);
     // Defaults (measured at cfg1 / cfg4): one tile per wave when the tiles alone fill the GPU
@@ -529,31 +549,31 @@ inline bool stream_plan(int N, int K, int M, StreamPlan& p)
     for (;;) {
         p.per = (steps_total + nreq - 1) / nreq;
         p.nw = (steps_total + p.per - 1) / p.per;
-        p.xstage = p.mmax * p.per * 1024 <= kXStageMaxBytes;
-        const WaveLds w2 = wave_lds(p.mmax, p.xstage, 2, p.per, p.rt);
+        const WaveLds w2 = wave_lds(p.mmax, p.xg, 2, p.per, p.rt);
         if ((size_t)p.nw * w2.total <= kLdsPerCU || nreq == 1) break;
         nreq = std::max(1, nreq - 1);
     }
-    const int copies = 4 * p.rt + (p.xstage ? 0 : p.mmax);
+    const int copies = 4 * p.rt + (p.xg ? 0 : p.mmax);
+    const int extra = p.xg ? kXgLoads : 0;
     int depth = 2;
     if (g_depth_override && p.rt == 1) depth = std::max(2, std::min(4, g_depth_override));
-    while (depth > 2 && ((depth - 1) * copies >= 64 ||
-                         (size_t)p.nw * wave_lds(p.mmax, p.xstage, depth, p.per, p.rt).total > kLdsPerCU))
+    while (depth > 2 && ((depth - 1) * copies + extra >= 64 ||
+                         (size_t)p.nw * wave_lds(p.mmax, p.xg, depth, p.per, p.rt).total > kLdsPerCU))
         --depth;
-    const WaveLds w = wave_lds(p.mmax, p.xstage, depth, p.per, p.rt);
+    const WaveLds w = wave_lds(p.mmax, p.xg, depth, p.per, p.rt);
     p.depth = depth;
     p.lds = (size_t)p.nw * w.total;
     return p.lds <= kLdsPerCU;
 }
 
-template <int MMAX, bool XSTAGE, typename OutT>
+template <int MMAX, bool XG, typename OutT>
 void launch_stream_x(const StreamPlan& p, const void* W, const void* St, const void* Xb, void* Out,
                      int N, int K, int M, hipStream_t s)
 {
     const dim3 grid((unsigned)((N + kRowsPerWG * p.rt - 1) / (kRowsPerWG * p.rt)));
     const dim3 block(64 * p.nw);
 #define FP8KV_D(D, RT) \
-    launch_kernel(h4mv_stream_kernel<MMAX, XSTAGE, D, RT, OutT>, grid, block, p.lds, s, \
+    launch_kernel(h4mv_stream_kernel<MMAX, XG, D, RT, OutT>, grid, block, p.lds, s, \
                   static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
                   static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M, p.per)
     if (p.rt == 4) {
@@ -574,9 +594,10 @@ template <typename OutT>
 void launch_stream_m(const StreamPlan& p, const void* W, const void* St, const void* Xb, void* Out,
                      int N, int K, int M, hipStream_t s)
 {
-    // Activation staging (xstage) is planned only when kXStageMaxBytes allows it, which it
-    // currently does not, so only the per-step-copy variants are instantiated.
-    static_assert(kXStageMaxBytes == 0, "instantiate the xstage variants before enabling them");
+    if (p.xg) {                             // MMAX only sizes the LDS copies: one variant
+        launch_stream_x<8, true, OutT>(p, W, St, Xb, Out, N, K, M, s);
+        return;
+    }
     switch (p.mmax) {
         case 1: launch_stream_x<1, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
         case 2: launch_stream_x<2, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
@@ -624,8 +645,8 @@ int audit_stream(int N, int K, int M, const StreamPlan& p)
     if (RT != 1 && RT != 2 && RT != 4) return 3;
     if (nw > (RT == 1 ? 16 : kMaxWavesRT) || nw * per < steps_total || (nw - 1) * per >= steps_total) return 2;
     if (p.lds > kLdsPerCU || depth < 2 || depth > 4 || (RT > 1 && depth != 2)) return 3;
-    if ((depth - 1) * (4 * RT + (p.xstage ? 0 : MMAX)) >= 64) return 3;
-    const WaveLds L = wave_lds(MMAX, p.xstage, depth, per, RT);
+    if ((depth - 1) * (4 * RT + (p.xg ? 0 : MMAX)) + (p.xg ? kXgLoads : 0) >= 64) return 3;
+    const WaveLds L = wave_lds(MMAX, p.xg, depth, per, RT);
     if ((size_t)nw * L.total != p.lds) return 3;
     const size_t wbytes = (size_t)N * (size_t)(K >> 1), sbytes = (size_t)N * (size_t)(K >> 5);
     const size_t xbytes = (size_t)M * (size_t)K * 2;
@@ -642,13 +663,6 @@ int audit_stream(int N, int K, int M, const StreamPlan& p)
                     if (stream_s_seg_off(n0, N, K, per, step0, t) + 16 > sbytes) return 6;
                     if (wb + L.ring + 16 * (size_t)t + 16 > wb + L.ring + L.scales) return 7;
                 }
-                if (p.xstage)
-                    for (int s = 0; s < nsteps; ++s)
-                        for (int m = 0; m < M; ++m)
-                            for (int lane = 0; lane < 64; ++lane) {
-                                if (stream_x_off(K, M, m, (step0 + s) * kStepGroups, lane) + 16 > xbytes) return 8;
-                                if (L.ring + L.scales + (size_t)(m * per + s) * 1024 + 16 * lane + 16 > (size_t)L.total) return 9;
-                            }
             }
             for (int s = 0; s < nsteps; ++s) {
                 const int gs = (step0 + s) * kStepGroups;
@@ -659,7 +673,7 @@ int audit_stream(int N, int K, int M, const StreamPlan& p)
                         if (g + 16 > wbytes) return 4;
                         if (slot + i * 1024 + 16 * lane + 16 > slot + RT * kStepCodeBytes) return 5;
                     }
-                    if (!p.xstage)
+                    if (!p.xg)
                         for (int m = 0; m < MMAX; ++m) {
                             if (stream_x_off(K, M, m, gs, lane) + 16 > xbytes) return 8;
                             if (RT * kStepCodeBytes + m * 1024 + 16 * lane + 16 > L.slot) return 9;
@@ -672,10 +686,15 @@ int audit_stream(int N, int K, int M, const StreamPlan& p)
                     }
                     for (int u = 0; u < 4; ++u)
                         for (int j = 0; j < 4; ++j) {
+                            if (p.xg) {                    // direct loads, row M - 1 for r >= M
+                                const size_t xo = (size_t)(r < M ? r : M - 1) * (size_t)K * 2 +
+                                                  (size_t)gs * 64 + stream_x_frag_off(q, u, j);
+                                if (xo + 16 > xbytes) return 14;
+                                continue;
+                            }
                             if (r >= M) continue;
-                            const size_t xo = p.xstage ? L.ring + L.scales + (size_t)(r * per + s) * 1024
-                                                       : (size_t)(s % depth) * L.slot + RT * kStepCodeBytes + r * 1024;
-                            const size_t end = p.xstage ? (size_t)L.total : (size_t)(s % depth) * L.slot + L.slot;
+                            const size_t xo = (size_t)(s % depth) * L.slot + RT * kStepCodeBytes + r * 1024;
+                            const size_t end = (size_t)(s % depth) * L.slot + L.slot;
                             if (xo + stream_x_frag_off(q, u, j) + 16 > end) return 12;
                         }
                 }
@@ -697,8 +716,9 @@ extern "C" int fp8kv_h4mv_audit(int N, int K, int M)
     return audit_stream(N, K, M, p);
 }
 
-extern "C" void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles)
+extern "C" void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode)
 {
+    fp8kv::h4mv_detail::g_xg_override = (x_mode == 1 || x_mode == 2) ? x_mode : 0;
     fp8kv::h4mv_detail::g_rt_override = (row_tiles == 1 || row_tiles == 2 || row_tiles == 4) ? row_tiles : 0;
     fp8kv::h4mv_detail::g_target_waves = target_waves > 0 ? target_waves : 0;
     fp8kv::h4mv_detail::g_depth_override = depth;

@@ -45,7 +45,7 @@ SIGNATURES: dict[str, tuple] = {
                           + [_c_vp] * 3 + [_c_i] * 4 + [_c_vp]),
     # host-only diagnostics (csrc/fp8kv_diag.h)
     "fp8kv_h4mv_audit": (_c_i, [_c_i] * 3),
-    "fp8kv_h4mv_tune": (None, [_c_i] * 3),
+    "fp8kv_h4mv_tune": (None, [_c_i] * 4),
     "fp8kv_decode_tune": (None, [_c_i] * 2),
     "fp8kv_prefill_tune": (None, [_c_i]),
     "fp8kv_time_next_launch": (None, [_c_vp, _c_vp]),

@@ -236,15 +236,17 @@ def test_repack_then_matvec_matches_checkpoint_layout():
     assert matvec.rel_to_max_error(y.cpu().numpy(), ref) < TOL
 
 
+@pytest.mark.parametrize("x_mode", [1, 2])
 @pytest.mark.parametrize("rt", [1, 2, 4])
 @pytest.mark.parametrize("N,K", [(4096, 3584), (100, 1024), (65, 512)])
-def test_row_tile_variants(rt, N, K):
-    """Each row-tile count of the streaming kernel (forced through the tuning hook) meets the same
-    bars at M = 1, 3, 8, including tiles that run past N."""
+def test_row_tile_variants(rt, N, K, x_mode):
+    """Each row-tile count and activation path (LDS copies or direct loads) of the streaming
+    kernel, forced through the tuning hook, meets the same bars at M = 1, 3, 8, including tiles
+    that run past N."""
     lib = _lib.load()
     try:
-        lib.fp8kv_h4mv_tune(0, 0, rt)
+        lib.fp8kv_h4mv_tune(0, 0, rt, x_mode)
         for M in (1, 3, 8):
             _check(workloads.w4_case(N=N, K=K, M=M, seed=N + K + M + rt))
     finally:
-        lib.fp8kv_h4mv_tune(0, 0, 0)
+        lib.fp8kv_h4mv_tune(0, 0, 0, 0)

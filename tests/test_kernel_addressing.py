@@ -31,13 +31,14 @@ def test_h4mv_register_path_shapes_are_reported(lib):
         assert lib.fp8kv_h4mv_audit(N, K, M) == 1
 
 
+@pytest.mark.parametrize("x_mode", [1, 2])
 @pytest.mark.parametrize("rt", [1, 2, 4])
-def test_h4mv_stream_in_bounds_every_row_tile_count(lib, rt):
-    """Every row-tile count the planner can pick (forced through the tuning hook), on the model
-    shapes and on random ones, including N not a multiple of 16 rt."""
-    rng = random.Random(rt)
+def test_h4mv_stream_in_bounds_every_row_tile_count(lib, rt, x_mode):
+    """Every row-tile count and activation path the planner can pick (forced through the tuning
+    hook), on the model shapes and on random ones, including N not a multiple of 16 rt."""
+    rng = random.Random(rt + 10 * x_mode)
     try:
-        lib.fp8kv_h4mv_tune(0, 0, rt)
+        lib.fp8kv_h4mv_tune(0, 0, rt, x_mode)
         for N, K in CFG4_SHAPES:
             for M in (1, 3, 8):
                 assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
@@ -47,4 +48,4 @@ def test_h4mv_stream_in_bounds_every_row_tile_count(lib, rt):
             M = rng.randrange(1, 9)
             assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
     finally:
-        lib.fp8kv_h4mv_tune(0, 0, 0)
+        lib.fp8kv_h4mv_tune(0, 0, 0, 0)
