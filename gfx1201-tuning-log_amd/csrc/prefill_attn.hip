@@ -684,6 +684,17 @@ prefill_split_kernel(Params P)
                         kf[kg][st] = __builtin_bit_cast(u32x4_t, fp8x8_to_bf16x8(raw[0], raw[1]));
                     }
                 }
+                // V^T raw rows (lane (c, p) transposes d = 8c .. 8c+7) and their widening go ahead
+                // of S^T = K.Q^T, so the VALU work can run between the MFMAs.
+                u32x2_t vr[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int row = (jj < 4 ? 0 : 16) + 4 * lp + (jj & 3);
+                    const unsigned char* vb = buf + 4096 + (row >> 3) * 1024;
+                    vr[jj] = *reinterpret_cast<const u32x2_t*>(vb + 16 * v_slot(row & 7, lr >> 1) + 8 * (lr & 1));
+                }
+                u32x4_t vf[8];
+                v_fragments(vr, vf);
                 f32x4_t sc[RS][2];
 #pragma unroll
                 for (int j = 0; j < RS; ++j)
@@ -695,6 +706,12 @@ prefill_split_kernel(Params P)
                             acc = mfma16x16x32_bf16(as_bf16x8(kf[kg][st]), as_bf16x8(qf[j][st]), acc);
                         sc[j][kg] = acc;
                     }
+                // Interleave: one MFMA, then up to three VALU (the V widening, 48 instructions).
+#pragma unroll
+                for (int g = 0; g < 8 * RS; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
                 if (k0 + kBN - 1 > qpos0) {                        // tile reaches past the first row
                     const int qpos = qpos0 + lr;
 #pragma unroll
@@ -707,35 +724,11 @@ prefill_split_kernel(Params P)
                 }
                 u32x4_t pb[RS];
                 softmax_tile<RS>(sc, m_run, l_run, o, qk, pb);
-
-                // V^T fragments in two halves (fragment 4w + i comes from dword w of each row)
-                // to keep the register peak low; lane (c, p) transposes d = 8c .. 8c+7.
-                u32x2_t vr[8];
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const int row = (jj < 4 ? 0 : 16) + 4 * lp + (jj & 3);
-                    const unsigned char* vb = buf + 4096 + (row >> 3) * 1024;
-                    vr[jj] = *reinterpret_cast<const u32x2_t*>(vb + 16 * v_slot(row & 7, lr >> 1) + 8 * (lr & 1));
-                }
+                for (int j = 0; j < RS; ++j)
 #pragma unroll
-                for (int w = 0; w < 2; ++w) {
-                    u32x4_t vf[4];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const uint32_t a = vr[2 * k][w], b = vr[2 * k + 1][w];
-                        const uint32_t x = __builtin_amdgcn_perm(b, a, 0x05010400u);
-                        const uint32_t y = __builtin_amdgcn_perm(b, a, 0x07030602u);
-                        vf[0][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, false));
-                        vf[1][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, true));
-                        vf[2][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(y, 1.0f, false));
-                        vf[3][k] = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(y, 1.0f, true));
-                    }
-#pragma unroll
-                    for (int j = 0; j < RS; ++j)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            o[j][4 * w + q] = mfma16x16x32_bf16(as_bf16x8(vf[q]), as_bf16x8(pb[j]), o[j][4 * w + q]);
-                }
+                    for (int n = 0; n < 8; ++n)
+                        o[j][n] = mfma16x16x32_bf16(as_bf16x8(vf[n]), as_bf16x8(pb[j]), o[j][n]);
             }
             // Block ids for the next window's copies, after this iteration's LDS reads so that
             // no LDS wait in the tile work has to cover the scalar loads.
