@@ -129,32 +129,46 @@ __device__ __forceinline__ LaneOffsets lane_offsets(const Params& P, int lr, int
 // Request every K and V byte of the chunk starting at token c0 (tokens >= hi are zero-filled and
 // never read).  Wave-uniform branches per 16-token group: full groups load unconditionally, the
 // group holding hi masks per lane.  Group g's block id is lane NG kb_idx + g of `bids`; the
-// group's base address is scalar, the per-lane part a 32-bit offset.
-template <int NG>
+// group's base address is scalar, the per-lane part a 32-bit offset.  KF requests the K bytes of
+// every group before any V byte, so the S^T MFMAs and the softmax of the chunk can start while
+// its V bytes are still arriving; otherwise K and V alternate per group.
+template <int NG, bool KF>
 __device__ __forceinline__ void issue_chunk(ChunkRegs<NG>& c, const Params& P, const LaneOffsets& lo_,
                                             int bids, int kb_idx, int kh, int c0, int hi, int lr, int lp)
 {
     const u32x4_t z4 = {0u, 0u, 0u, 0u};
     const u32x2_t z2 = {0u, 0u};
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
+    auto issue_k = [&](int g) {
         const int t0 = c0 + 16 * g;
         if (t0 < hi) {
             const int64_t blk = __builtin_amdgcn_readlane(bids, NG * kb_idx + g);
             const int slot0 = t0 & (P.pblk - 1);
             const uint8_t* kb = P.k + blk * P.sk0 + (int64_t)slot0 * P.sk1 + (int64_t)kh * P.sk2;
-            const uint8_t* vb = P.v + blk * P.sv0 + (int64_t)slot0 * P.sv1 + (int64_t)kh * P.sv2;
             if (t0 + 16 <= hi) {
                 c.kr[g][0] = load_nt_16(kb + lo_.k);
                 c.kr[g][1] = load_nt_16(kb + lo_.k + 64);
+            } else {
+                const bool kok = t0 + lr < hi;
+                c.kr[g][0] = kok ? load_nt_16(kb + lo_.k) : z4;
+                c.kr[g][1] = kok ? load_nt_16(kb + lo_.k + 64) : z4;
+            }
+        } else {
+            c.kr[g][0] = z4;
+            c.kr[g][1] = z4;
+        }
+    };
+    auto issue_v = [&](int g) {
+        const int t0 = c0 + 16 * g;
+        if (t0 < hi) {
+            const int64_t blk = __builtin_amdgcn_readlane(bids, NG * kb_idx + g);
+            const int slot0 = t0 & (P.pblk - 1);
+            const uint8_t* vb = P.v + blk * P.sv0 + (int64_t)slot0 * P.sv1 + (int64_t)kh * P.sv2;
+            if (t0 + 16 <= hi) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     c.vr[g >> 1][4 * (g & 1) + i] =
                         __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(vb + lo_.v[i]));
             } else {
-                const bool kok = t0 + lr < hi;
-                c.kr[g][0] = kok ? load_nt_16(kb + lo_.k) : z4;
-                c.kr[g][1] = kok ? load_nt_16(kb + lo_.k + 64) : z4;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const bool vok = t0 + 4 * lp + i < hi;
@@ -163,10 +177,20 @@ __device__ __forceinline__ void issue_chunk(ChunkRegs<NG>& c, const Params& P, c
                 }
             }
         } else {
-            c.kr[g][0] = z4;
-            c.kr[g][1] = z4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) c.vr[g >> 1][4 * (g & 1) + i] = z2;
+        }
+    };
+    if constexpr (KF) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) issue_k(g);
+#pragma unroll
+        for (int g = 0; g < NG; ++g) issue_v(g);
+    } else {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            issue_k(g);
+            issue_v(g);
         }
     }
 }
@@ -238,7 +262,7 @@ __device__ __forceinline__ void consume_chunk(const ChunkRegs<NG>& c, WaveState&
     }
 }
 
-template <int W, int NG, int DEPTH>
+template <int W, int NG, int DEPTH, bool KF>
 __global__ void __launch_bounds__(W * 64)
 decode_kernel(Params P)
 {
@@ -289,7 +313,7 @@ decode_kernel(Params P)
     const LaneOffsets lofs = lane_offsets(P, lr, lp);
     ChunkRegs<NG> ca;
     [[maybe_unused]] ChunkRegs<NG> cb;
-    issue_chunk<NG>(ca, P, lofs, bid_cur, 0, kh, c0, hi, lr, lp);
+    issue_chunk<NG, KF>(ca, P, lofs, bid_cur, 0, kh, c0, hi, lr, lp);
     int k_issue = 1;                       // index (within the wave) of the next chunk to request
 
     WaveState st;
@@ -311,7 +335,7 @@ decode_kernel(Params P)
             c0 += stride;
             if (c0 >= hi) break;
             next_ids();
-            issue_chunk<NG>(ca, P, lofs, bid_cur, k_issue % CPB, kh, c0, hi, lr, lp);
+            issue_chunk<NG, KF>(ca, P, lofs, bid_cur, k_issue % CPB, kh, c0, hi, lr, lp);
             ++k_issue;
         }
     } else {
@@ -319,13 +343,13 @@ decode_kernel(Params P)
         while (c0 < hi) {
             const int c1 = c0 + stride;
             next_ids();
-            issue_chunk<NG>(cb, P, lofs, bid_cur, k_issue % CPB, kh, c1, hi, lr, lp);
+            issue_chunk<NG, KF>(cb, P, lofs, bid_cur, k_issue % CPB, kh, c1, hi, lr, lp);
             ++k_issue;
             consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
             if (c1 >= hi) break;
             const int c2 = c1 + stride;
             next_ids();
-            issue_chunk<NG>(ca, P, lofs, bid_cur, k_issue % CPB, kh, c2, hi, lr, lp);
+            issue_chunk<NG, KF>(ca, P, lofs, bid_cur, k_issue % CPB, kh, c2, hi, lr, lp);
             ++k_issue;
             consume_chunk<NG>(cb, st, qf, qk_scale, c1, hi, lp);
             c0 = c2;
@@ -477,20 +501,24 @@ inline size_t scratch_bytes(int ns, int hq, int hkv, int nsplit)
            (size_t)ns * (size_t)hkv * (size_t)nsplit * (size_t)record_floats(gqa) * sizeof(float);
 }
 
-// Launch variants (waves per workgroup, 16-token groups per chunk, chunks in flight per wave).
+// Launch variants (waves per workgroup, 16-token groups per chunk, chunks in flight per wave,
+// K bytes of a chunk requested before its V bytes).
 struct Variant {
     int waves, ng, depth;
+    bool kfirst;
 };
-constexpr Variant kVariants[] = {{8, 4, 1}, {8, 2, 1}, {4, 4, 1}, {4, 4, 2}};
+constexpr Variant kVariants[] = {{8, 4, 1, false}, {8, 2, 1, false}, {4, 4, 1, false}, {4, 4, 2, false},
+                                 {8, 2, 2, true},  {8, 2, 2, false}, {8, 2, 1, true}};
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
 // Launch tunables (host state; fp8kv_decode_tune changes them for sweeps).
-int g_variant = 0;
+constexpr int kDefaultVariant = 4;
+int g_variant = kDefaultVariant;
 int g_target_wgs = 256;
 
 // Splits per (sequence, kv head): enough workgroups to reach g_target_wgs, but never fewer
-// than one chunk per workgroup and never more than needed to give every wave one chunk... unless
-// that leaves the grid short of the target.
+// than one chunk per workgroup, and never so few that a wave has more than its pipeline depth of
+// chunks (more splits are taken then, even beyond the target).
 inline int plan_splits(int ns, int hkv, int max_seq_len)
 {
     if (max_seq_len <= 0) return 1;
@@ -499,7 +527,8 @@ inline int plan_splits(int ns, int hkv, int max_seq_len)
     const int pairs = ns * hkv;
     const int by_fill = (g_target_wgs + pairs - 1) / pairs;                  // fill the GPU
     const int by_chunks = (max_seq_len + chunk - 1) / chunk;                 // >= 1 chunk per WG
-    const int by_waves = (max_seq_len + v.waves * chunk - 1) / (v.waves * chunk);  // <= 1 chunk per wave
+    const int per_wg = v.waves * chunk * v.depth;                            // one pipeline load per wave
+    const int by_waves = (max_seq_len + per_wg - 1) / per_wg;
     int n = by_fill < by_chunks ? by_fill : by_chunks;
     if (n < by_waves) n = by_waves;
     if (n < 1) n = 1;
@@ -592,16 +621,19 @@ extern "C" int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
     switch (g_variant) {
-        case 1: launch_kernel(decode_kernel<8, 2, 1>, grid, dim3(8 * 64), 0, st, P); break;
-        case 2: launch_kernel(decode_kernel<4, 4, 1>, grid, dim3(4 * 64), 0, st, P); break;
-        case 3: launch_kernel(decode_kernel<4, 4, 2>, grid, dim3(4 * 64), 0, st, P); break;
-        default: launch_kernel(decode_kernel<8, 4, 1>, grid, dim3(8 * 64), 0, st, P); break;
+        case 0: launch_kernel(decode_kernel<8, 4, 1, false>, grid, dim3(8 * 64), 0, st, P); break;
+        case 1: launch_kernel(decode_kernel<8, 2, 1, false>, grid, dim3(8 * 64), 0, st, P); break;
+        case 2: launch_kernel(decode_kernel<4, 4, 1, false>, grid, dim3(4 * 64), 0, st, P); break;
+        case 3: launch_kernel(decode_kernel<4, 4, 2, false>, grid, dim3(4 * 64), 0, st, P); break;
+        case 5: launch_kernel(decode_kernel<8, 2, 2, false>, grid, dim3(8 * 64), 0, st, P); break;
+        case 6: launch_kernel(decode_kernel<8, 2, 1, true>, grid, dim3(8 * 64), 0, st, P); break;
+        default: launch_kernel(decode_kernel<8, 2, 2, true>, grid, dim3(8 * 64), 0, st, P); break;
     }
     return finish_launch();
 }
 
 extern "C" void fp8kv_decode_tune(int variant, int target_wgs)
 {
-    g_variant = (variant >= 0 && variant < kNumVariants) ? variant : 0;
+    g_variant = (variant >= 0 && variant < kNumVariants) ? variant : kDefaultVariant;
     g_target_wgs = target_wgs > 0 ? target_wgs : 256;
 }

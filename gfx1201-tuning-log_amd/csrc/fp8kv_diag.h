@@ -17,10 +17,11 @@ int fp8kv_h4mv_audit(int N, int K, int M);
  * and audits. */
 void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode);
 
-/* Tuning hook for sweeps of the decode attention launch: kernel variant index (0 = default: 8 waves,
- * 4 groups of 16 keys per wave) and the workgroup count its split planner aims for (0 = default
- * 256).  Affects later launches. */
-void fp8kv_decode_tune(int waves, int target_wgs);
+/* Tuning hook for sweeps of the decode attention launch: kernel variant index (0..6; any other
+ * value, e.g. -1, selects the default, variant 4: 8 waves, chunks of 2 groups of 16 keys, 2 chunks
+ * in flight per wave, K bytes requested before V bytes) and the workgroup count its split planner
+ * aims for (0 = default 256).  Affects later launches. */
+void fp8kv_decode_tune(int variant, int target_wgs);
 
 /* Tuning hook for sweeps of the prefill attention launch: index of the (waves, row-sets per wave,
  * LDS ring depth) shape to use for every GQA, or -1 for the per-GQA default. */
