@@ -14,9 +14,11 @@
 // gfx950 design:
 //   * grid (num_splits, HKV, NS); a workgroup of W waves owns a 16-aligned token span of its
 //     (sequence, kv head); wave w takes chunks w, w + W, ... of the span, a chunk being NG
-//     16-token groups.  Q, the scales and the wave's block ids are requested first, then every K
-//     and V byte of the wave's first chunk (and, with DEPTH 2, of the next one while the current
-//     one is computed).
+//     16-token groups.  Q and the scales are requested first; then, per chunk (DEPTH 1) or pair
+//     of chunks (DEPTH 2), the block ids with scalar loads and every K and V byte with loads
+//     issued back to back, the second chunk of a pair arriving while the first is computed.
+//     The wave index is uniform and no load sits under a branch, so the compiler's vmcnt waits
+//     are exact (each use waits for its own bytes only).
 //   * S^T = K . Q^T on v_mfma_f32_16x16x32_bf16: A = 16 tokens x 32 d of K, B = Q^T with the GQA
 //     query heads of the kv head in columns 0..GQA-1 (zero beyond).  Lane (r, p) = (lane % 16,
 //     lane / 16) loads 16 bytes of token r at d = 16 p and at d = 64 + 16 p; the d order is
@@ -98,17 +100,50 @@ struct WaveState {
     f32x4_t o[8];
 };
 
-// Block ids of a wave's chunks, prefetched with one vector load per 64 / NG chunks: lane
-// NG k + g of batch b holds the block of group g of the wave's chunk (64 / NG) b + k (0 past the
-// context).
+// Block ids of one chunk, one per 16-token group, read with scalar loads (their waits count
+// lgkmcnt and never hold back the K and V loads in flight).  A group that starts at or past hi
+// takes the id of the span's last group (`last`: the start of the 16-token group holding token
+// hi - 1), so every address formed from the ids lies in a block the sequence owns.
 template <int NG>
-__device__ __forceinline__ int load_block_ids(const Params& P, const int32_t* btrow, int first,
-                                              int stride, int hi, int batch, int lane)
+struct ChunkIds {
+    int blk[NG];
+};
+
+typedef __attribute__((address_space(4))) const int32_t const_i32_t;   // read-only for the launch
+
+template <int NG>
+__device__ __forceinline__ ChunkIds<NG> load_chunk_ids(const Params& P, const int32_t* btrow, int c0, int last)
 {
-    constexpr int CPB = 64 / NG;
-    const int t0 = first + stride * (CPB * batch + lane / NG) + 16 * (lane % NG);
-    return t0 < hi ? btrow[t0 >> P.pshift] : 0;
+    // The constant address space makes the compiler use scalar loads for these uniform reads,
+    // whatever stores or fences come before them in the kernel.
+    const_i32_t* row = (const_i32_t*)btrow;
+    ChunkIds<NG> ids;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int t0 = c0 + 16 * g;
+        ids.blk[g] = row[(t0 < last ? t0 : last) >> P.pshift];
+    }
+    return ids;
 }
+
+// Both chunks' block ids are in registers here: their scalar loads are issued together and
+// waited for once, instead of one round trip per id.
+// (The ids pass through the asm as in/out operands, so every use of them is ordered after it.)
+template <int NG>
+__device__ __forceinline__ void ids_ready(ChunkIds<NG>& a, ChunkIds<NG>& b)
+{
+    static_assert(NG == 2 || NG == 4, "two or four groups per chunk");
+    if constexpr (NG == 2) {
+        asm volatile("" : "+s"(a.blk[0]), "+s"(a.blk[1]), "+s"(b.blk[0]), "+s"(b.blk[1]));
+    } else {
+        asm volatile("" : "+s"(a.blk[0]), "+s"(a.blk[1]), "+s"(a.blk[2]), "+s"(a.blk[3]),
+                          "+s"(b.blk[0]), "+s"(b.blk[1]), "+s"(b.blk[2]), "+s"(b.blk[3]));
+    }
+}
+
+// Keeps the compiler from moving loads issued before it past it (into the branch that uses
+// them), which would undo the software pipeline.
+__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
 
 // Per-lane byte offsets of the chunk loads within one 16-token group (32-bit: the host rejects
 // slot strides that could overflow them).
@@ -126,60 +161,34 @@ __device__ __forceinline__ LaneOffsets lane_offsets(const Params& P, int lr, int
     return o;
 }
 
-// Request every K and V byte of the chunk starting at token c0 (tokens >= hi are zero-filled and
-// never read).  Wave-uniform branches per 16-token group: full groups load unconditionally, the
-// group holding hi masks per lane.  Group g's block id is lane NG kb_idx + g of `bids`; the
-// group's base address is scalar, the per-lane part a 32-bit offset.  KF requests the K bytes of
-// every group before any V byte, so the S^T MFMAs and the softmax of the chunk can start while
-// its V bytes are still arriving; otherwise K and V alternate per group.
+// Request every K and V byte of the chunk starting at token c0 with the same instruction
+// sequence wherever the chunk lies, so the compiler's wait counts stay exact: the group holding hi
+// reads all 16 of its slots (inside its block; tokens >= hi are masked where used), and a group
+// past hi reads one line of the span's last group with every lane (no new traffic).  Group g's
+// base address is scalar (block id from `ids`), the per-lane part a 32-bit offset.  KF requests
+// the K bytes of every group before any V byte, so the S^T MFMAs and the softmax of a chunk can
+// start while its V bytes are still arriving; otherwise K and V alternate per group.
 template <int NG, bool KF>
 __device__ __forceinline__ void issue_chunk(ChunkRegs<NG>& c, const Params& P, const LaneOffsets& lo_,
-                                            int bids, int kb_idx, int kh, int c0, int hi, int lr, int lp)
+                                            const ChunkIds<NG>& ids, int kh, int c0, int hi, int last)
 {
-    const u32x4_t z4 = {0u, 0u, 0u, 0u};
-    const u32x2_t z2 = {0u, 0u};
-    auto issue_k = [&](int g) {
+    auto slot_of = [&](int g) -> int64_t {
         const int t0 = c0 + 16 * g;
-        if (t0 < hi) {
-            const int64_t blk = __builtin_amdgcn_readlane(bids, NG * kb_idx + g);
-            const int slot0 = t0 & (P.pblk - 1);
-            const uint8_t* kb = P.k + blk * P.sk0 + (int64_t)slot0 * P.sk1 + (int64_t)kh * P.sk2;
-            if (t0 + 16 <= hi) {
-                c.kr[g][0] = load_nt_16(kb + lo_.k);
-                c.kr[g][1] = load_nt_16(kb + lo_.k + 64);
-            } else {
-                const bool kok = t0 + lr < hi;
-                c.kr[g][0] = kok ? load_nt_16(kb + lo_.k) : z4;
-                c.kr[g][1] = kok ? load_nt_16(kb + lo_.k + 64) : z4;
-            }
-        } else {
-            c.kr[g][0] = z4;
-            c.kr[g][1] = z4;
-        }
+        return (int64_t)((t0 < last ? t0 : last) & (P.pblk - 1));
+    };
+    auto issue_k = [&](int g) {
+        const uint32_t m = c0 + 16 * g < hi ? ~0u : 0u;
+        const uint8_t* kb = P.k + (int64_t)ids.blk[g] * P.sk0 + slot_of(g) * P.sk1 + (int64_t)kh * P.sk2;
+        c.kr[g][0] = load_nt_16(kb + (lo_.k & m));
+        c.kr[g][1] = load_nt_16(kb + (lo_.k & m) + 64);
     };
     auto issue_v = [&](int g) {
-        const int t0 = c0 + 16 * g;
-        if (t0 < hi) {
-            const int64_t blk = __builtin_amdgcn_readlane(bids, NG * kb_idx + g);
-            const int slot0 = t0 & (P.pblk - 1);
-            const uint8_t* vb = P.v + blk * P.sv0 + (int64_t)slot0 * P.sv1 + (int64_t)kh * P.sv2;
-            if (t0 + 16 <= hi) {
+        const uint32_t m = c0 + 16 * g < hi ? ~0u : 0u;
+        const uint8_t* vb = P.v + (int64_t)ids.blk[g] * P.sv0 + slot_of(g) * P.sv1 + (int64_t)kh * P.sv2;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    c.vr[g >> 1][4 * (g & 1) + i] =
-                        __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(vb + lo_.v[i]));
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool vok = t0 + 4 * lp + i < hi;
-                    c.vr[g >> 1][4 * (g & 1) + i] =
-                        vok ? __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(vb + lo_.v[i])) : z2;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) c.vr[g >> 1][4 * (g & 1) + i] = z2;
-        }
+        for (int i = 0; i < 4; ++i)
+            c.vr[g >> 1][4 * (g & 1) + i] =
+                __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(vb + (lo_.v[i] & m)));
     };
     if constexpr (KF) {
 #pragma unroll
@@ -193,6 +202,7 @@ __device__ __forceinline__ void issue_chunk(ChunkRegs<NG>& c, const Params& P, c
             issue_v(g);
         }
     }
+    issue_fence();
 }
 
 // S^T = K . Q^T, online softmax update, O^T += V^T . P^T for one chunk.
@@ -255,8 +265,20 @@ __device__ __forceinline__ void consume_chunk(const ChunkRegs<NG>& c, WaveState&
         pb[1] = pack_bf16x2(s[2 * G][2], s[2 * G][3]);
         pb[2] = pack_bf16x2(s[2 * G + 1][0], s[2 * G + 1][1]);
         pb[3] = pack_bf16x2(s[2 * G + 1][2], s[2 * G + 1][3]);
+        // V bytes of tokens >= hi are stale cache slots (possibly NaN codes): zero them so that
+        // P = 0 contributes nothing.
+        u32x2_t vv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vv[j] = c.vr[G][j];
+        if (c0 + 16 * NG > hi) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int tok = c0 + 32 * G + (j < 4 ? 4 * lp + j : 16 + 4 * lp + (j - 4));
+                if (tok >= hi) vv[j] = (u32x2_t){0u, 0u};
+            }
+        }
         u32x4_t va[8];
-        v_fragments(c.vr[G], va);
+        v_fragments(vv, va);
 #pragma unroll
         for (int n = 0; n < 8; ++n) st.o[n] = mfma16x16x32_bf16(as_bf16x8(va[n]), as_bf16x8(pb), st.o[n]);
     }
@@ -267,7 +289,6 @@ __global__ void __launch_bounds__(W * 64)
 decode_kernel(Params P)
 {
     constexpr int CH = 16 * NG;                 // tokens per chunk
-    constexpr int CPB = 64 / NG;                // chunks per block-id batch
     constexpr int T = W * 64;
     constexpr int EPT = (kMaxGqa * kD + T - 1) / T;   // merge elements per thread (upper bound)
     __shared__ float lds_ml[W][kMaxGqa][2];
@@ -278,7 +299,7 @@ decode_kernel(Params P)
     const int sp = blockIdx.x, kh = blockIdx.y, seq = blockIdx.z;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15;
     const int lp = lane >> 4;
     const int gqa = P.gqa;
@@ -304,55 +325,44 @@ decode_kernel(Params P)
     const float qk_scale = P.sm_scale * P.k_scale[0] * kLog2e;
     const float vs = P.v_scale[0];
 
-    // Block ids of the wave's first two batches of chunks, then the first chunk's loads.
-    const int stride = CH * W;
-    const int c_first = lo + CH * wave;
-    int c0 = c_first;
-    int bid_cur = load_block_ids<NG>(P, btrow, c_first, stride, hi, 0, lane);
-    int bid_next = load_block_ids<NG>(P, btrow, c_first, stride, hi, 1, lane);
-    const LaneOffsets lofs = lane_offsets(P, lr, lp);
-    ChunkRegs<NG> ca;
-    [[maybe_unused]] ChunkRegs<NG> cb;
-    issue_chunk<NG, KF>(ca, P, lofs, bid_cur, 0, kh, c0, hi, lr, lp);
-    int k_issue = 1;                       // index (within the wave) of the next chunk to request
-
     WaveState st;
     st.m_run = neg_inf();
     st.l_run = 0.f;
 #pragma unroll
     for (int n = 0; n < 8; ++n) st.o[n] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 
-    // Block-id batches rotate every CPB chunks, one batch ahead of the loads that need them.
-    auto next_ids = [&]() {
-        if (k_issue % CPB == 0) {
-            bid_cur = bid_next;
-            bid_next = load_block_ids<NG>(P, btrow, c_first, stride, hi, k_issue / CPB + 1, lane);
-        }
-    };
-    if constexpr (DEPTH == 1) {
-        while (c0 < hi) {
-            consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
-            c0 += stride;
-            if (c0 >= hi) break;
-            next_ids();
-            issue_chunk<NG, KF>(ca, P, lofs, bid_cur, k_issue % CPB, kh, c0, hi, lr, lp);
-            ++k_issue;
-        }
-    } else {
-        // two-deep software pipeline: the next chunk is requested before the current one is used
-        while (c0 < hi) {
-            const int c1 = c0 + stride;
-            next_ids();
-            issue_chunk<NG, KF>(cb, P, lofs, bid_cur, k_issue % CPB, kh, c1, hi, lr, lp);
-            ++k_issue;
-            consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
-            if (c1 >= hi) break;
-            const int c2 = c1 + stride;
-            next_ids();
-            issue_chunk<NG, KF>(ca, P, lofs, bid_cur, k_issue % CPB, kh, c2, hi, lr, lp);
-            ++k_issue;
-            consume_chunk<NG>(cb, st, qf, qk_scale, c1, hi, lp);
-            c0 = c2;
+    // The wave's chunks start at c_first and step by `stride`.
+    const int stride = CH * W;
+    const int c_first = lo + CH * wave;
+    const int last = (hi - 1) & ~15;
+    if (c_first < hi) {
+        const LaneOffsets lofs = lane_offsets(P, lr, lp);
+        ChunkRegs<NG> ca;
+        [[maybe_unused]] ChunkRegs<NG> cb;
+        int c0 = c_first;
+        if constexpr (DEPTH == 1) {
+            do {
+                const ChunkIds<NG> ia = load_chunk_ids<NG>(P, btrow, c0, last);
+                issue_chunk<NG, KF>(ca, P, lofs, ia, kh, c0, hi, last);
+                consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
+                c0 += stride;
+            } while (c0 < hi);
+        } else {
+            // Chunks in pairs: both block-id sets in one scalar round trip, both chunks' loads
+            // back to back, then chunk A is used while chunk B is still arriving.  Straight-line
+            // code up to the use of B keeps the compiler's wait counts exact.  A chunk B past hi
+            // reads one broadcast line per instruction and is not used.
+            do {
+                ChunkIds<NG> ia = load_chunk_ids<NG>(P, btrow, c0, last);
+                ChunkIds<NG> ib = load_chunk_ids<NG>(P, btrow, c0 + stride, last);
+                ids_ready(ia, ib);
+                issue_chunk<NG, KF>(ca, P, lofs, ia, kh, c0, hi, last);
+                issue_chunk<NG, KF>(cb, P, lofs, ib, kh, c0 + stride, hi, last);
+                consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
+                if (c0 + stride >= hi) break;
+                consume_chunk<NG>(cb, st, qf, qk_scale, c0 + stride, hi, lp);
+                c0 += 2 * stride;
+            } while (c0 < hi);
         }
     }
 
