@@ -526,9 +526,13 @@ constexpr int kDefaultVariant = 4;
 int g_variant = kDefaultVariant;
 int g_target_wgs = 256;
 
-// Splits per (sequence, kv head): enough workgroups to reach g_target_wgs, but never fewer
-// than one chunk per workgroup, and never so few that a wave has more than its pipeline depth of
-// chunks (more splits are taken then, even beyond the target).
+// Splits per (sequence, kv head): enough workgroups to reach g_target_wgs (one per CU: at the
+// kernel's register use only one 8-wave workgroup fits on a CU, so a larger grid runs in two
+// rounds), never fewer than one chunk per workgroup, and at most kMaxPlannedSplits, since the
+// merging workgroup reads the split records kMergeBatch at a time.  A wave loops over as many
+// chunk pairs as its span holds.
+constexpr int kMaxPlannedSplits = 32;
+
 inline int plan_splits(int ns, int hkv, int max_seq_len)
 {
     if (max_seq_len <= 0) return 1;
@@ -537,12 +541,9 @@ inline int plan_splits(int ns, int hkv, int max_seq_len)
     const int pairs = ns * hkv;
     const int by_fill = (g_target_wgs + pairs - 1) / pairs;                  // fill the GPU
     const int by_chunks = (max_seq_len + chunk - 1) / chunk;                 // >= 1 chunk per WG
-    const int per_wg = v.waves * chunk * v.depth;                            // one pipeline load per wave
-    const int by_waves = (max_seq_len + per_wg - 1) / per_wg;
     int n = by_fill < by_chunks ? by_fill : by_chunks;
-    if (n < by_waves) n = by_waves;
+    if (n > kMaxPlannedSplits) n = kMaxPlannedSplits;
     if (n < 1) n = 1;
-    if (n > kMaxSplits) n = kMaxSplits;
     return n;
 }
 
