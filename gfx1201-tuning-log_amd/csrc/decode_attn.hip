@@ -284,6 +284,58 @@ __device__ __forceinline__ void consume_chunk(const ChunkRegs<NG>& c, WaveState&
     }
 }
 
+// Final merge of up to SMAX split records in one round trip: every o value a thread needs (its
+// elements tid + T j of every split) and every split's m and l (to LDS) are requested together
+// with straight-line loads (split indices past nsplit repeat the last split and are not used), so
+// the only wait is the barrier's.  Each element then weighs split s by exp2(m_s - max_s m_s).
+// wm / wl: LDS for [nsplit][gqa] m and l.
+template <int SMAX, int T>
+__device__ __forceinline__ void merge_all(const Params& P, const float* recs, int rf, int E, int gqa,
+                                          float* wm, float* wl, int tid, float vs, int64_t out_row)
+{
+    const int ns = P.nsplit;
+    const int NSG = ns * gqa;
+    for (int e0 = 0; e0 < E; e0 += 2 * T) {
+        float ov[2][SMAX];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            int e = e0 + tid + T * j;
+            e = e < E ? e : E - 1;
+#pragma unroll
+            for (int s = 0; s < SMAX; ++s)
+                ov[j][s] = load_coherent(recs + (int64_t)(s < ns ? s : ns - 1) * rf + e);
+        }
+        if (e0 == 0) {
+            for (int i = tid; i < NSG; i += T) {
+                const int s = i / gqa, h = i - s * gqa;
+                wm[i] = load_coherent(recs + (int64_t)s * rf + E + h);
+                wl[i] = load_coherent(recs + (int64_t)s * rf + E + gqa + h);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int e = e0 + tid + T * j;
+            if (e >= E) continue;
+            const int h = e / kD;
+            float m = neg_inf();
+            for (int s = 0; s < ns; ++s) m = fmaxf(m, wm[s * gqa + h]);
+            const float mu = m == neg_inf() ? 0.f : m;
+            float acc = 0.f, l = 0.f;
+#pragma unroll
+            for (int s = 0; s < SMAX; ++s) {
+                if (s < ns) {
+                    const float f = __builtin_amdgcn_exp2f(wm[s * gqa + h] - mu);
+                    acc += f * ov[j][s];
+                    l += f * wl[s * gqa + h];
+                }
+            }
+            const float r = l > 0.f ? acc * vs / l : 0.f;
+            P.out[out_row + e] = (__bf16)r;
+        }
+    }
+}
+
 template <int W, int NG, int DEPTH, bool KF>
 __global__ void __launch_bounds__(W * 64)
 decode_kernel(Params P)
@@ -443,7 +495,24 @@ decode_kernel(Params P)
     __syncthreads();
     if (!lds_last) return;
 
-    // Final merge, one round trip per kMergeBatch splits: m and l of every split go to LDS once
+    const float* recs_all = P.part + pair * P.nsplit * rf;
+    const int64_t out_row = (int64_t)qtok * P.o_stride + (int64_t)(kh * gqa) * kD;
+    if (P.nsplit <= 32) {
+        float* wm_all = &lds_o[0][0][0];
+        float* wl_all = wm_all + 32 * kMaxGqa;
+        if (P.nsplit <= 8)
+            merge_all<8, T>(P, recs_all, rf, E, gqa, wm_all, wl_all, tid, vs, out_row);
+        else if (P.nsplit <= 16)
+            merge_all<16, T>(P, recs_all, rf, E, gqa, wm_all, wl_all, tid, vs, out_row);
+        else
+            merge_all<32, T>(P, recs_all, rf, E, gqa, wm_all, wl_all, tid, vs, out_row);
+        if (tid == 0)
+            __hip_atomic_store(P.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+
+    // More than 32 splits (only when the caller asks for them): one round trip per kMergeBatch
+    // splits: m and l of every split go to LDS once
     // (one load per split and head), each thread loads the o values of its own elements
     // tid + T j, and both are in flight together before the barrier.
     const float* recs = P.part + pair * P.nsplit * rf;

@@ -113,7 +113,7 @@ def test_zero_context_gives_zeros():
     torch.testing.assert_close(got[1], _oracle(c)[1], rtol=RTOL, atol=ATOL)
 
 
-@pytest.mark.parametrize("splits", [1, 3, 16, 64, 256])
+@pytest.mark.parametrize("splits", [1, 3, 8, 9, 16, 17, 24, 32, 33, 64, 256])
 def test_split_count_invariance(splits):
     c = workloads.decode_case([3000, 1500, 4096], seed=8)
     _check(c, num_splits=splits)
@@ -202,7 +202,7 @@ def test_every_launch_variant(variant):
     c = workloads.decode_case([4096, 1500, 33, 2900], seed=15, layout="engine")
     try:
         lib.fp8kv_decode_tune(variant, 0)
-        for splits in (1, 4, 8, 37):
+        for splits in (1, 4, 8, 13, 32, 37):
             _check(c, num_splits=splits)
     finally:
         lib.fp8kv_decode_tune(-1, 0)
