@@ -204,6 +204,71 @@ def bench_cache_write(T: int, steps: int, warmup: int, HKV=4, D=128, PBLK=16, po
     return r
 
 
+def bench_rmsnorm(M: int, H: int, steps: int, warmup: int, seed: int = 0):
+    """Residual add + RMSNorm (mode 0) of M rows of H, rotated over sets above the MALL for large M."""
+    import torch
+    from fp8kv_amd import ops
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    row_bytes = 8 * H
+    n_sets = max(2, min(16, -(-2 * (256 << 20) // max(1, M * row_bytes)) + 1)) if M * row_bytes > (1 << 20) else 2
+    sets = [(torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16),
+             torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16),
+             torch.empty(M, H, dtype=torch.bfloat16, device=dev)) for _ in range(n_sets)]
+    w = torch.randn(H, device=dev, generator=g).to(torch.bfloat16)
+
+    def launch(i):
+        x, res, out = sets[i]
+        ops.fused_add_rmsnorm(x, res, w, 1e-6, out=out)
+
+    wall, per = time_launches(launch, n_sets, steps, warmup)
+    del sets
+    torch.cuda.empty_cache()
+    r = _summary(wall, per, M * row_bytes + 2 * H)
+    r.update({"rows": M, "hidden": H})
+    return r
+
+
+def bench_silu_mul(M: int, d: int, steps: int, warmup: int, seed: int = 0):
+    import torch
+    from fp8kv_amd import ops
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    gu = torch.randn(M, 2 * d, device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty(M, d, dtype=torch.bfloat16, device=dev)
+    wall, per = time_launches(lambda i: ops.silu_mul(gu, out=out), 1, steps, warmup)
+    r = _summary(wall, per, 6 * M * d)
+    r.update({"rows": M, "d": d})
+    return r
+
+
+def bench_gate_up_silu(M: int, steps: int, warmup: int, N: int = 37888, K: int = 3584):
+    """configs[4] gate/up linear at M rows followed by SiLU-and-mul: the fused epilogue
+    (h4mv_silu_mul on interleaved weights, one launch) against the two launches it replaces."""
+    import torch
+    from fp8kv_amd import ops, workloads
+    dev = torch.device("cuda")
+    n_sets = max(4, -(-2 * (256 << 20) // (N * K // 2)) + 1)
+    ws = []
+    for i in range(n_sets):
+        c = workloads.w4_case(N, K, M, seed=40 + i)
+        ws.append(ops.interleave_gate_up(c["W"].to(dev), c["St"].to(dev)))
+    x = c["X"].to(dev)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(M, N // 2, dtype=torch.bfloat16, device=dev)
+    wall_f, per_f = time_launches(lambda i: ops.h4mv_silu_mul(x, ws[i][0], ws[i][1], out=out), n_sets, steps, warmup)
+    wall_m, per_m = time_launches(lambda i: ops.h4mv(x, ws[i][0], ws[i][1], out=y), n_sets, steps, warmup)
+    wall_s, per_s = time_launches(lambda i: ops.silu_mul(y, out=out), 1, steps, warmup)
+    del ws
+    torch.cuda.empty_cache()
+    nbytes = N * K // 2 + N * K // 32 + 2 * M * K + 2 * M * (N // 2)
+    r = _summary(wall_f, per_f, nbytes)
+    r["us_kernel_two_launches"] = round((statistics.mean(per_m) + statistics.mean(per_s)) * 1e3, 3)
+    r["us_step_two_launches"] = round((wall_m + wall_s) * 1e3, 3)
+    r["rows"] = M
+    return r
+
+
 # configs[4]: the 28-layer decode step at batch 8 (per layer: the four MXFP4 linears at M = 8 and
 # the fp8 decode attention over 8 sequences of 4096 tokens, 24/4 heads).
 STACK_LINEARS = [("qkv", 4096, 3584), ("o", 3584, 3072), ("gate_up", 37888, 3584), ("down", 3584, 18944)]
@@ -434,7 +499,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--legs", default="w4,decode,prefill,cache,stack,copy",
+    ap.add_argument("--legs", default="w4,decode,prefill,cache,epi,stack,copy",
                     help="comma list of legs to run (w4, decode, prefill, cache, stack, copy)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -470,6 +535,11 @@ def main():
     if "cache" in legs_wanted:
         legs["cache_write_2048"] = bench_cache_write(2048, max(5, args.steps // 4), max(2, args.warmup // 4))
         legs["cache_write_8"] = bench_cache_write(8, args.steps, args.warmup)
+    if "epi" in legs_wanted:
+        legs["rmsnorm_8x3584"] = bench_rmsnorm(8, 3584, args.steps, args.warmup)
+        legs["rmsnorm_2048x3584"] = bench_rmsnorm(2048, 3584, max(5, args.steps // 4), max(2, args.warmup // 4))
+        legs["silu_mul_8x18944"] = bench_silu_mul(8, 18944, args.steps, args.warmup)
+        legs["gate_up_silu_cfg4_M8"] = bench_gate_up_silu(8, args.steps, args.warmup)
     if "stack" in legs_wanted:
         legs["stack_cfg4_28_layers_b8"] = bench_stack(max(3, args.steps // 20), max(2, args.warmup // 10))
     if "copy" in legs_wanted:

@@ -71,6 +71,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// bf16 round trip of an f32 (round to nearest even): the value a bf16 store would hold.
+__device__ __forceinline__ float round_to_bf16(float f) { return (float)(__bf16)f; }
+
+// SiLU in f32, x / (1 + e^-x): one definition for the stand-alone activation kernel and the
+// matvec epilogue, so both give the same bits.
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
 __device__ __forceinline__ f32x4_t mfma16x16x32_bf16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

@@ -279,7 +279,11 @@ __device__ __forceinline__ void issue_step(unsigned char* slot, const uint8_t* w
 // so those variants are launched with at most kMaxWavesRT waves.
 constexpr int kMaxWavesRT = 4;
 
-template <int MMAX, bool XG, int DEPTH, int RT, typename OutT>
+// EPI selects the output stage: 0 writes Out[M, N]; 1 and 2 apply SiLU-and-mul to gate/up rows
+// interleaved 8 + 8 per 16-row tile (h4mv_interleave_gate_up) and write Out[M, N / 2]: gate and
+// up are first rounded to bf16 (the values a plain matvec would store), then
+// Out = bf16(silu(g) * u) (EPI 1) or bf16(bf16(silu(g)) * u) (EPI 2).
+template <int MMAX, bool XG, int DEPTH, int RT, typename OutT, int EPI = 0>
 __global__ void __launch_bounds__(RT == 1 ? 1024 : 64 * kMaxWavesRT)
 h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
                    const __bf16* __restrict__ X, OutT* __restrict__ Out,
@@ -417,6 +421,33 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
                 acc[t] += reinterpret_cast<const f32x4_t*>(smem + w * L.total)[t * 64 + lane];
     }
 
+    if constexpr (EPI != 0) {
+        // lane (m, q < 2) holds gate rows 4q .. 4q + 3 of each tile's 8 features, lane (m, q + 2)
+        // = lane + 32 the up rows of the same features
+        f32x4_t up[RT];
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) up[t][i] = __shfl_xor(acc[t][i], 32);
+        if (r >= M || q >= 2) return;
+        const int half = N >> 1;
+        __bf16* orow = reinterpret_cast<__bf16*>(Out) + (size_t)r * (size_t)half;
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const int tile = (n0 >> 4) + t;
+            if (16 * tile >= N) continue;
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float sg = silu_f32(round_to_bf16(acc[t][i]));
+                if constexpr (EPI == 2) sg = round_to_bf16(sg);
+                o[i] = sg * round_to_bf16(up[t][i]);
+            }
+            *reinterpret_cast<u32x2_t*>(orow + 8 * tile + 4 * q) =
+                (u32x2_t){pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        }
+        return;
+    }
     const int m = r;
     if (m >= M) return;
     OutT* orow = Out + (size_t)m * (size_t)N;
@@ -566,14 +597,14 @@ inline bool stream_plan(int N, int K, int M, StreamPlan& p)
     return p.lds <= kLdsPerCU;
 }
 
-template <int MMAX, bool XG, typename OutT>
+template <int MMAX, bool XG, typename OutT, int EPI = 0>
 void launch_stream_x(const StreamPlan& p, const void* W, const void* St, const void* Xb, void* Out,
                      int N, int K, int M, hipStream_t s)
 {
     const dim3 grid((unsigned)((N + kRowsPerWG * p.rt - 1) / (kRowsPerWG * p.rt)));
     const dim3 block(64 * p.nw);
 #define FP8KV_D(D, RT) \
-    launch_kernel(h4mv_stream_kernel<MMAX, XG, D, RT, OutT>, grid, block, p.lds, s, \
+    launch_kernel(h4mv_stream_kernel<MMAX, XG, D, RT, OutT, EPI>, grid, block, p.lds, s, \
                   static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
                   static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M, p.per)
     if (p.rt == 4) {
@@ -590,19 +621,19 @@ void launch_stream_x(const StreamPlan& p, const void* W, const void* St, const v
 #undef FP8KV_D
 }
 
-template <typename OutT>
+template <typename OutT, int EPI = 0>
 void launch_stream_m(const StreamPlan& p, const void* W, const void* St, const void* Xb, void* Out,
                      int N, int K, int M, hipStream_t s)
 {
     if (p.xg) {                             // MMAX only sizes the LDS copies: one variant
-        launch_stream_x<8, true, OutT>(p, W, St, Xb, Out, N, K, M, s);
+        launch_stream_x<8, true, OutT, EPI>(p, W, St, Xb, Out, N, K, M, s);
         return;
     }
     switch (p.mmax) {
-        case 1: launch_stream_x<1, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-        case 2: launch_stream_x<2, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-        case 4: launch_stream_x<4, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
-        default: launch_stream_x<8, false, OutT>(p, W, St, Xb, Out, N, K, M, s); break;
+        case 1: launch_stream_x<1, false, OutT, EPI>(p, W, St, Xb, Out, N, K, M, s); break;
+        case 2: launch_stream_x<2, false, OutT, EPI>(p, W, St, Xb, Out, N, K, M, s); break;
+        case 4: launch_stream_x<4, false, OutT, EPI>(p, W, St, Xb, Out, N, K, M, s); break;
+        default: launch_stream_x<8, false, OutT, EPI>(p, W, St, Xb, Out, N, K, M, s); break;
     }
 }
 
@@ -628,6 +659,24 @@ int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N,
 
 }  // namespace h4mv_detail
 }  // namespace fp8kv
+
+extern "C" int h4mv_silu_mul(const void* W, const void* St, const void* Xb, void* Out, int N, int K,
+                             int M, int mode, void* stream)
+{
+    using namespace fp8kv;
+    using namespace fp8kv::h4mv_detail;
+    if (!W || !St || !Xb || !Out) return FP8KV_ERR_ARG;
+    if (N < 16 || K < 32 || M < 1 || (mode != 0 && mode != 1)) return FP8KV_ERR_ARG;
+    if (M > 8 || (K & 511) != 0 || (N & 15) != 0) return FP8KV_ERR_SHAPE;
+    if (!aligned(W, 16) || !aligned(Xb, 16) || !aligned(Out, 8) || !aligned(St, 4)) return FP8KV_ERR_ALIGN;
+    StreamPlan p;
+    if (!stream_plan(N, K, M, p)) return FP8KV_ERR_SHAPE;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    begin_launch();
+    if (mode == 0) launch_stream_m<__bf16, 1>(p, W, St, Xb, Out, N, K, M, s);
+    else launch_stream_m<__bf16, 2>(p, W, St, Xb, Out, N, K, M, s);
+    return finish_launch();
+}
 
 // ---------------------------------------------------------------------------------------------
 // Host-side address audit of the streaming kernel: enumerates, for the launch the entry points

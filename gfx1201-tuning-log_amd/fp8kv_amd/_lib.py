@@ -43,6 +43,12 @@ SIGNATURES: dict[str, tuple] = {
     # fp8 KV-cache write (csrc/cache_write.hip)
     "fp8kv_cache_write": (_c_i, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp] + [_c_i64] * 6
                           + [_c_vp] * 3 + [_c_i] * 4 + [_c_vp]),
+    # layer epilogues (csrc/epilogues.hip, h4mv_silu_mul in csrc/h4mv.hip)
+    "fp8kv_fused_add_rmsnorm": (_c_i, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_i, _c_i,
+                                       _c_f, _c_i, _c_vp]),
+    "fp8kv_silu_mul": (_c_i, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i, _c_i, _c_i, _c_vp]),
+    "h4mv_interleave_gate_up": (_c_i, [_c_vp] * 4 + [_c_i] * 2 + [_c_vp]),
+    "h4mv_silu_mul": (_c_i, [_c_vp] * 4 + [_c_i] * 4 + [_c_vp]),
     # host-only diagnostics (csrc/fp8kv_diag.h)
     "fp8kv_h4mv_audit": (_c_i, [_c_i] * 3),
     "fp8kv_h4mv_tune": (None, [_c_i] * 4),

@@ -275,3 +275,93 @@ def cache_write(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
         slot_mapping.data_ptr(), ks.data_ptr(), vs.data_ptr(), T, HKV, D, k_cache.shape[1],
         _stream_ptr(key))
     _lib.check("fp8kv_cache_write", st)
+
+
+# ------------------------------------------------------------------------------ layer epilogues
+
+def _bf16_rows(t: torch.Tensor, name: str) -> None:
+    _require(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 2 and t.stride(1) == 1,
+             f"{name} must be a 2-D bf16 device tensor with contiguous rows")
+
+
+def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+                      out: torch.Tensor | None = None, mode: int = 0) -> torch.Tensor:
+    """residual <- x + residual (bf16, in place); returns rmsnorm(x + residual) * weight in bf16.
+
+    mode 0: the compiled vLLM native form the reference engine runs (f32 sum used for the mean
+    and the scaling); mode 1: vLLM's _C.fused_add_rms_norm (bf16-rounded sum).  ``out`` may be
+    ``x`` (vLLM's op writes the result into its input).  fp8kv_fused_add_rmsnorm.
+    """
+    _bf16_rows(x, "x")
+    _bf16_rows(residual, "residual")
+    M, H = x.shape
+    _require(tuple(residual.shape) == (M, H), "residual must match x")
+    _require(weight.is_cuda and weight.dtype == torch.bfloat16 and tuple(weight.shape) == (H,)
+             and weight.is_contiguous(), "weight must be a contiguous bf16 [H] device tensor")
+    if out is None:
+        out = torch.empty_like(x)
+    _bf16_rows(out, "out")
+    _require(tuple(out.shape) == (M, H), "out must match x")
+    st = _lib.load().fp8kv_fused_add_rmsnorm(x.data_ptr(), x.stride(0), residual.data_ptr(),
+                                             residual.stride(0), weight.data_ptr(), out.data_ptr(),
+                                             out.stride(0), M, H, float(eps), int(mode), _stream_ptr(x))
+    _lib.check("fp8kv_fused_add_rmsnorm", st)
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None, mode: int = 0) -> torch.Tensor:
+    """[M, d] = silu(gate_up[:, :d]) * gate_up[:, d:] in bf16 (mode 0: one rounding, as the
+    compiled vLLM native form; mode 1: SiLU rounded first, as vLLM's _C.silu_and_mul)."""
+    _bf16_rows(gate_up, "gate_up")
+    M, d2 = gate_up.shape
+    _require(d2 % 2 == 0, "gate_up width must be even")
+    d = d2 // 2
+    if out is None:
+        out = torch.empty((M, d), dtype=torch.bfloat16, device=gate_up.device)
+    _bf16_rows(out, "out")
+    _require(tuple(out.shape) == (M, d), f"out must be [{M}, {d}]")
+    st = _lib.load().fp8kv_silu_mul(gate_up.data_ptr(), gate_up.stride(0), out.data_ptr(), out.stride(0),
+                                    M, d, int(mode), _stream_ptr(gate_up))
+    _lib.check("fp8kv_silu_mul", st)
+    return out
+
+
+def interleave_gate_up(weight: torch.Tensor, scales_nk: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Load-time row interleave of a merged gate/up weight (rows [gate; up]) for h4mv_silu_mul:
+    each 16-row tile becomes 8 gate rows then the up rows of the same 8 features."""
+    _require(weight.is_cuda and weight.dtype == torch.uint8 and weight.dim() == 2 and weight.is_contiguous(),
+             "weight must be contiguous uint8 [N, K/2] on the device")
+    N, KH = weight.shape
+    K = 2 * KH
+    _require(scales_nk.dtype == torch.uint8 and tuple(scales_nk.shape) == (N, K // 32)
+             and scales_nk.is_contiguous() and scales_nk.device == weight.device,
+             f"scales must be contiguous uint8 [{N}, {K // 32}]")
+    w_out = torch.empty_like(weight)
+    s_out = torch.empty_like(scales_nk)
+    st = _lib.load().h4mv_interleave_gate_up(weight.data_ptr(), scales_nk.data_ptr(), w_out.data_ptr(),
+                                             s_out.data_ptr(), N, K, _stream_ptr(weight))
+    _lib.check("h4mv_interleave_gate_up", st)
+    return w_out, s_out
+
+
+def h4mv_silu_mul(x: torch.Tensor, weight_il: torch.Tensor, scales_il: torch.Tensor,
+                  out: torch.Tensor | None = None, mode: int = 0) -> torch.Tensor:
+    """[M, N/2] = silu_mul(x . dequant(W)^T) for a gate/up weight from interleave_gate_up, in one
+    launch (the same bits as h4mv into [M, N] followed by silu_mul(mode))."""
+    _require(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(),
+             "x must be a contiguous 2-D bf16 device tensor")
+    M, K = x.shape
+    N = weight_il.shape[0]
+    _require(weight_il.dtype == torch.uint8 and tuple(weight_il.shape) == (N, K // 2)
+             and weight_il.is_contiguous(), f"weight must be contiguous uint8 [N, {K // 2}]")
+    _require(scales_il.dtype == torch.uint8 and tuple(scales_il.shape) == (N, K // 32)
+             and scales_il.is_contiguous(), f"scales must be contiguous uint8 [{N}, {K // 32}]")
+    _require(weight_il.device == x.device == scales_il.device, "tensors on different devices")
+    if out is None:
+        out = torch.empty((M, N // 2), dtype=torch.bfloat16, device=x.device)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (M, N // 2) and out.is_contiguous(),
+             f"out must be contiguous bf16 [{M}, {N // 2}]")
+    st = _lib.load().h4mv_silu_mul(weight_il.data_ptr(), scales_il.data_ptr(), x.data_ptr(), out.data_ptr(),
+                                   N, K, M, int(mode), _stream_ptr(x))
+    _lib.check("h4mv_silu_mul", st)
+    return out

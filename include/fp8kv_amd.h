@@ -196,6 +196,53 @@ int fp8kv_cache_write(const void* key, int64_t key_row_stride,
                       int num_tokens, int num_kv_heads, int head_size, int block_size,
                       void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Layer epilogues around the MXFP4 linears (decode and prefill).
+ *
+ * The reference engine runs these as compiler-fused kernels of its vLLM model code (listed in
+ * profiling/prof_engine.txt:13,15,17 and profiling/prof_h4mv.txt:11,13,15: "fused_add_rms_norm"
+ * before the qkv and gate/up linears, "mul silu slice" between gate/up and down).  Two rounding
+ * forms are offered, selected by `mode`:
+ *   0 - the compiled native form those profiles show (f32 intermediates, one final rounding);
+ *   1 - vLLM's custom ops (_C.fused_add_rms_norm, _C.silu_and_mul), which round the residual sum
+ *       and the SiLU output to bf16 before using them.
+ * ------------------------------------------------------------------------------------------- */
+
+/* residual[t, :] <- bf16(x + residual); out[t, :] = bf16(bf16((x + residual) * rsqrt(mean((x +
+ * residual)^2) + eps)) * weight), per token t (mode 1 uses the bf16-rounded sum throughout).
+ * bf16 rows, 16-byte aligned, strides in elements (multiples of 8); hidden_size % 8 == 0 and
+ * <= 16384; out may be x (in place, as vLLM's op writes it).
+ * Replaces: vLLM's fused_add_rms_norm(input, residual, weight, epsilon), the engine's
+ * triton_red_fused_fused_add_rms_norm_* kernels (profiling/prof_engine.txt:13,15). */
+int fp8kv_fused_add_rmsnorm(const void* x, int64_t x_row_stride, void* residual,
+                            int64_t residual_row_stride, const void* weight, void* out,
+                            int64_t out_row_stride, int num_tokens, int hidden_size, float eps,
+                            int mode, void* stream);
+
+/* out[t, j] = bf16(silu(gate_up[t, j]) * gate_up[t, d + j]) for j < d (mode 1: silu rounded to
+ * bf16 first).  bf16, 16-byte aligned, strides in elements (multiples of 8), d % 8 == 0.
+ * Replaces: vLLM's silu_and_mul(out, input), the engine's triton_poi_fused_mul_mxfp4_linear_silu_slice
+ * kernel (profiling/prof_engine.txt:17). */
+int fp8kv_silu_mul(const void* gate_up, int64_t in_row_stride, void* out, int64_t out_row_stride,
+                   int num_tokens, int d, int mode, void* stream);
+
+/* Load-time row interleave of a merged gate/up MXFP4 weight for h4mv_silu_mul: row 16 T + i of
+ * W_out / St_out is gate row 8 T + i (i < 8) or up row N/2 + 8 T + i - 8 (i >= 8) of W [N, K/2] /
+ * St [N, K/32] (the layout h4mv_launch reads).  N % 16 == 0, K % 32 == 0; run once per weight.
+ * No counterpart in the reference (its gate/up linear writes both halves and a separate kernel
+ * applies SiLU-and-mul). */
+int h4mv_interleave_gate_up(const void* W, const void* St, void* W_out, void* St_out, int N, int K,
+                            void* stream);
+
+/* Out[M, N/2] = silu_mul(X . dequant(W, St)^T) for a gate/up weight interleaved by
+ * h4mv_interleave_gate_up: the same bits as h4mv_launch into a bf16 [M, N] buffer (un-interleaved
+ * order) followed by fp8kv_silu_mul(mode), in one launch that never writes the gate and up
+ * values.  M <= 8, K % 512 == 0, N % 16 == 0, Out 8-byte aligned.
+ * Replaces: the gate/up mxfp4_linear (h4mv/fp8kv_hipw4.py:62-94 with h4mv_launch) followed by the
+ * engine's SiLU-and-mul kernel (profiling/prof_engine.txt:17). */
+int h4mv_silu_mul(const void* W, const void* St, const void* Xb, void* Out, int N, int K, int M,
+                  int mode, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -139,3 +139,61 @@ def test_cache_write_zero_tokens_is_a_no_op(lib):
 ])
 def test_repack_scales_rejects_before_launch(lib, args, code):
     assert lib.h4mv_repack_scales(*args) == code
+
+
+# Layer epilogues: every call below is rejected (or is a no-op) before any HIP call.
+RN_OK = [A, 4096, A, 4096, A, A, 4096, 8, 4096, 1e-6, 0, None]
+
+
+@pytest.mark.parametrize("idx,val,code", [
+    (0, None, 1),              # no x
+    (8, 4100, 2),              # hidden size not a multiple of 8
+    (8, 16392, 2),             # hidden size above 16384
+    (10, 2, 1),                # unknown mode
+    (9, -1.0, 1),              # negative eps
+    (1, 100, 1),               # row stride shorter than a row
+    (1, 4100, 3),              # row stride not a multiple of 8
+    (4, A + 8, 3),             # weight not 16-byte aligned
+])
+def test_rmsnorm_rejects_before_launch(lib, idx, val, code):
+    args = list(RN_OK)
+    args[idx] = val
+    assert lib.fp8kv_fused_add_rmsnorm(*args) == code
+
+
+def test_rmsnorm_zero_tokens_is_a_no_op(lib):
+    args = list(RN_OK)
+    args[7] = 0
+    assert lib.fp8kv_fused_add_rmsnorm(*args) == 0
+
+
+@pytest.mark.parametrize("args,code", [
+    ((None, 64, A, 32, 4, 32, 0, None), 1),       # null input
+    ((A, 64, A, 32, 4, 36, 0, None), 2),         # d % 8 != 0
+    ((A, 48, A, 32, 4, 32, 0, None), 1),         # input row shorter than 2 d
+    ((A, 64, A, 32, 4, 32, 3, None), 1),         # unknown mode
+    ((A + 2, 64, A, 32, 4, 32, 0, None), 3),     # misaligned input
+])
+def test_silu_mul_rejects_before_launch(lib, args, code):
+    assert lib.fp8kv_silu_mul(*args) == code
+
+
+@pytest.mark.parametrize("args,code", [
+    ((A, A, A, A, 8, 1024, 1, 0, None), 1),      # N < 16
+    ((A, A, A, A, 64, 1024, 9, 0, None), 2),     # M > 8
+    ((A, A, A, A, 64, 1000, 1, 0, None), 2),     # K % 512 != 0
+    ((A, A, A, A, 72, 1024, 1, 0, None), 2),     # N % 16 != 0
+    ((A, A, A, A + 4, 64, 1024, 1, 0, None), 3), # out not 8-byte aligned
+    ((A, A, A, A, 64, 1024, 1, 5, None), 1),     # unknown mode
+])
+def test_h4mv_silu_mul_rejects_before_launch(lib, args, code):
+    assert lib.h4mv_silu_mul(*args) == code
+
+
+@pytest.mark.parametrize("args,code", [
+    ((A, A, A, A, 72, 1024, None), 2),           # N % 16 != 0
+    ((A, A, A, None, 64, 1024, None), 1),        # no scale output
+    ((A + 8, A, A, A, 64, 1024, None), 3),       # misaligned codes
+])
+def test_interleave_rejects_before_launch(lib, args, code):
+    assert lib.h4mv_interleave_gate_up(*args) == code
