@@ -269,6 +269,41 @@ def bench_gate_up_silu(M: int, steps: int, warmup: int, N: int = 37888, K: int =
     return r
 
 
+MFMA_FP8_PEAK_TFLOPS = 5000.0      # dense fp8 (and fp8 x fp4) MFMA peak of MI355X
+
+
+def bench_w4a8_gemm(M: int, steps: int, warmup: int):
+    """The configs[4] linears at M tokens (a prefill chunk) through the MXFP8 quantiser and the
+    MXFP4 x MXFP8 block-scaled GEMM; weights rotated above the MALL."""
+    import torch
+    from fp8kv_amd import ops, workloads
+    dev = torch.device("cuda")
+    out = {}
+    x = torch.randn(M, 18944, device=dev).to(torch.bfloat16)
+    for name, N, K in STACK_LINEARS:
+        wbytes = N * K // 2
+        n_sets = max(2, min(8, -(-2 * (256 << 20) // wbytes) + 1))
+        ws = []
+        for i in range(n_sets):
+            c = workloads.w4_case(N, K, 1, seed=60 + i)
+            ws.append((c["W"].to(dev), c["St"].to(dev)))
+        xq, sx = ops.quant_mxfp8(x[:, :K].contiguous())
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        wall, per = time_launches(lambda i: ops.h4a8_gemm(xq, sx, ws[i][0], ws[i][1], out=y), n_sets,
+                                  steps, warmup)
+        xc = x[:, :K].contiguous()
+        wq, perq = time_launches(lambda i: ops.quant_mxfp8(xc, out=(xq, sx)), 1, steps, warmup)
+        flops = 2.0 * M * N * K
+        k_us = statistics.mean(per) * 1e3
+        out[name] = {"N": N, "K": K, "us_kernel": round(k_us, 3), "us_step": round(wall * 1e3, 3),
+                     "TFLOPs_kernel": round(flops / (k_us * 1e-6) / 1e12, 2),
+                     "frac_kernel": round(flops / (k_us * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFLOPS, 4),
+                     "us_quant": round(statistics.mean(perq) * 1e3, 3)}
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 # configs[4]: the 28-layer decode step at batch 8 (per layer: the four MXFP4 linears at M = 8 and
 # the fp8 decode attention over 8 sequences of 4096 tokens, 24/4 heads).
 STACK_LINEARS = [("qkv", 4096, 3584), ("o", 3584, 3072), ("gate_up", 37888, 3584), ("down", 3584, 18944)]
@@ -499,8 +534,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--legs", default="w4,decode,prefill,cache,epi,stack,copy",
-                    help="comma list of legs to run (w4, decode, prefill, cache, stack, copy)")
+    ap.add_argument("--legs", default="w4,decode,prefill,cache,epi,gemm,stack,copy",
+                    help="comma list of legs to run (w4, decode, prefill, cache, epi, gemm, stack, copy)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one GPU; "
@@ -540,6 +575,8 @@ def main():
         legs["rmsnorm_2048x3584"] = bench_rmsnorm(2048, 3584, max(5, args.steps // 4), max(2, args.warmup // 4))
         legs["silu_mul_8x18944"] = bench_silu_mul(8, 18944, args.steps, args.warmup)
         legs["gate_up_silu_cfg4_M8"] = bench_gate_up_silu(8, args.steps, args.warmup)
+    if "gemm" in legs_wanted:
+        legs["w4a8_gemm_cfg4_linears_M2048"] = bench_w4a8_gemm(2048, max(5, args.steps // 4), max(2, args.warmup // 4))
     if "stack" in legs_wanted:
         legs["stack_cfg4_28_layers_b8"] = bench_stack(max(3, args.steps // 20), max(2, args.warmup // 10))
     if "copy" in legs_wanted:

@@ -49,6 +49,9 @@ SIGNATURES: dict[str, tuple] = {
     "fp8kv_silu_mul": (_c_i, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i, _c_i, _c_i, _c_vp]),
     "h4mv_interleave_gate_up": (_c_i, [_c_vp] * 4 + [_c_i] * 2 + [_c_vp]),
     "h4mv_silu_mul": (_c_i, [_c_vp] * 4 + [_c_i] * 4 + [_c_vp]),
+    # MXFP4 x MXFP8 GEMM (csrc/w4a8_gemm.hip)
+    "h4a8_quant_act": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp, _c_i, _c_i, _c_vp]),
+    "h4a8_gemm": (_c_i, [_c_vp] * 5 + [_c_i] * 3 + [_c_vp]),
     # host-only diagnostics (csrc/fp8kv_diag.h)
     "fp8kv_h4mv_audit": (_c_i, [_c_i] * 3),
     "fp8kv_h4mv_tune": (None, [_c_i] * 4),

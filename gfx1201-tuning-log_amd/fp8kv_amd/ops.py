@@ -365,3 +365,50 @@ def h4mv_silu_mul(x: torch.Tensor, weight_il: torch.Tensor, scales_il: torch.Ten
                                    N, K, M, int(mode), _stream_ptr(x))
     _lib.check("h4mv_silu_mul", st)
     return out
+
+
+# ------------------------------------------------------------------------------ MXFP4 x MXFP8 GEMM
+
+def quant_mxfp8(x: torch.Tensor, out: tuple[torch.Tensor, torch.Tensor] | None = None):
+    """bf16 [M, K] -> (e4m3fn codes uint8 [M, K], e8m0 scale bytes uint8 [M, K/32]) per 32-wide
+    block of K (OCP MX, shared exponent floor(log2 max|x|) - 8).  h4a8_quant_act."""
+    _bf16_rows(x, "x")
+    M, K = x.shape
+    if out is None:
+        out = (torch.empty((M, K), dtype=torch.uint8, device=x.device),
+               torch.empty((M, K // 32), dtype=torch.uint8, device=x.device))
+    xq, sx = out
+    _require(xq.dtype == torch.uint8 and tuple(xq.shape) == (M, K) and xq.is_contiguous(), "codes must be uint8 [M, K]")
+    _require(sx.dtype == torch.uint8 and tuple(sx.shape) == (M, K // 32) and sx.is_contiguous(),
+             "scales must be uint8 [M, K/32]")
+    st = _lib.load().h4a8_quant_act(x.data_ptr(), x.stride(0), xq.data_ptr(), sx.data_ptr(), M, K, _stream_ptr(x))
+    _lib.check("h4a8_quant_act", st)
+    return xq, sx
+
+
+def h4a8_gemm(xq: torch.Tensor, sx: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 [M, N] = dequant(xq, sx) . dequant(weight, scales_nk)^T on the block-scaled MFMA."""
+    M, K = xq.shape
+    N = weight.shape[0]
+    _require(xq.is_cuda and xq.dtype == torch.uint8 and xq.is_contiguous(), "xq must be contiguous uint8 [M, K]")
+    _require(sx.dtype == torch.uint8 and tuple(sx.shape) == (M, K // 32) and sx.is_contiguous(), "sx must be uint8 [M, K/32]")
+    _require(weight.dtype == torch.uint8 and tuple(weight.shape) == (N, K // 2) and weight.is_contiguous(),
+             "weight must be contiguous uint8 [N, K/2]")
+    _require(scales_nk.dtype == torch.uint8 and tuple(scales_nk.shape) == (N, K // 32) and scales_nk.is_contiguous(),
+             "scales must be contiguous uint8 [N, K/32]")
+    _require(xq.device == sx.device == weight.device == scales_nk.device, "tensors on different devices")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=xq.device)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (M, N) and out.is_contiguous(),
+             "out must be contiguous bf16 [M, N]")
+    st = _lib.load().h4a8_gemm(weight.data_ptr(), scales_nk.data_ptr(), xq.data_ptr(), sx.data_ptr(),
+                               out.data_ptr(), N, K, M, _stream_ptr(xq))
+    _lib.check("h4a8_gemm", st)
+    return out
+
+
+def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor) -> torch.Tensor:
+    """x [M, K] bf16 -> [M, N] bf16 through the MXFP8 quantiser and the block-scaled GEMM."""
+    xq, sx = quant_mxfp8(x)
+    return h4a8_gemm(xq, sx, weight, scales_nk)

@@ -243,6 +243,33 @@ int h4mv_interleave_gate_up(const void* W, const void* St, void* W_out, void* St
 int h4mv_silu_mul(const void* W, const void* St, const void* Xb, void* Out, int N, int K, int M,
                   int mode, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * MXFP4 x MXFP8 GEMM for M >= 16 (prefill-sized linears) on gfx950's block-scaled MFMA.
+ *
+ * The reference engine's prefill linears run its vLLM fork's W4A8 GEMM on per-token fp8
+ * activations (radiance_mxfp4_fp8_gemm; profiling/prof_engine.txt:3-4, profiling/prof_prefill.txt:8,
+ * docs/06-w4gemm-hip-roadmap.md:140; the activations come from vLLM's
+ * dynamic_per_token_scaled_fp8_quant, profiling/prof_engine.txt:8).  That library is closed, so
+ * these entry points define the operator on gfx950's native MXFP8 block format instead.
+ * ------------------------------------------------------------------------------------------- */
+
+/* Xq[m, k] = e4m3fn(X[m, k] / 2^(Sx[m, k/32] - 127)) per 32-wide block of k, with the e8m0
+ * byte Sx = floor(log2(max |block|)) - 8 + 127 clamped to [0, 254] (0 for an all-zero block,
+ * 255 = NaN for a block holding NaN or +-inf): OCP MX v1.0 MXFP8, round to nearest even,
+ * saturated to +-448.  X bf16 [M, K] (row stride in elements, multiple of 8, 16-byte aligned),
+ * Xq uint8 [M, K] (16-byte aligned), Sx uint8 [M, K/32]; K % 32 == 0.
+ * Replaces: vLLM's dynamic_per_token_scaled_fp8_quant ahead of the W4A8 GEMM
+ * (profiling/prof_engine.txt:8). */
+int h4a8_quant_act(const void* X, int64_t x_row_stride, void* Xq, void* Sx, int M, int K, void* stream);
+
+/* Out[m, n] = bf16( sum_k dq(Xq, Sx)[m, k] * dq(W, St)[n, k] ), f32 accumulation; W / St in
+ * the layout h4mv_launch reads (uint8 [N, K/2], low nibble = even k; uint8 [N, K/32]).
+ * K % 128 == 0, N % 4 == 0, Out bf16 [M, N] 8-byte aligned; any M >= 1 (the matvec is faster
+ * for M <= 8).
+ * Replaces: radiance_mxfp4_fp8_gemm (the fork's W4A8 prefill GEMM, profiling/prof_prefill.txt:8). */
+int h4a8_gemm(const void* W, const void* St, const void* Xq, const void* Sx, void* Out, int N, int K,
+              int M, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -197,3 +197,28 @@ def test_h4mv_silu_mul_rejects_before_launch(lib, args, code):
 ])
 def test_interleave_rejects_before_launch(lib, args, code):
     assert lib.h4mv_interleave_gate_up(*args) == code
+
+
+@pytest.mark.parametrize("args,code", [
+    ((A, 64, A, A, 4, 48, None), 2),              # K % 32 != 0
+    ((A, 16, A, A, 4, 64, None), 1),              # row stride shorter than K
+    ((A + 8, 64, A, A, 4, 64, None), 3),          # X not 16-byte aligned
+    ((None, 64, A, A, 4, 64, None), 1),           # no X
+])
+def test_quant_act_rejects_before_launch(lib, args, code):
+    assert lib.h4a8_quant_act(*args) == code
+
+
+@pytest.mark.parametrize("args,code", [
+    ((A, A, A, A, A, 64, 192, 16, None), 2),      # K % 128 != 0
+    ((A, A, A, A, A, 66, 256, 16, None), 2),      # N % 4 != 0
+    ((A, A, A, A, A + 2, 64, 256, 16, None), 3),  # out misaligned
+    ((A, A, None, A, A, 64, 256, 16, None), 1),   # no activations
+])
+def test_h4a8_gemm_rejects_before_launch(lib, args, code):
+    assert lib.h4a8_gemm(*args) == code
+
+
+def test_h4a8_zero_rows_are_a_no_op(lib):
+    assert lib.h4a8_gemm(A, A, A, A, A, 64, 256, 0, None) == 0
+    assert lib.h4a8_quant_act(A, 64, A, A, 0, 64, None) == 0

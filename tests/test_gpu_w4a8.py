@@ -1,0 +1,84 @@
+"""GPU parity of the MXFP8 quantiser (h4a8_quant_act) and the MXFP4 x MXFP8 GEMM (h4a8_gemm).
+
+Bars: quantiser codes and scale bytes bit-exact against the oracle; GEMM output (on the same
+quantised operands) within half a bf16 ulp of the fp64 oracle plus 1e-4 * max|ref| (fp32
+accumulation inside the MFMA, the matvec's bf16 bar); end to end (bf16 x through the quantiser
+and the GEMM) against the unquantised W4A16 product, the error MXFP8 activations cost, < 5e-2
+relative to the largest output.
+"""
+import numpy as np
+import pytest
+import torch
+
+from fp8kv_amd import ops, workloads
+from oracle import matvec, w4a8
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _x(M, K, seed, spread=0.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    if spread:
+        x = x * torch.exp(torch.empty(M, K // 32, 1).uniform_(-spread, spread, generator=g)).expand(M, K // 32, 32).reshape(M, K)
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,K,spread", [(1, 32, 0), (16, 512, 0), (300, 3584, 20.0), (7, 18944, 5.0)])
+def test_quant_bit_exact(M, K, spread):
+    x = _x(M, K, M + K, spread)
+    xq, sx = ops.quant_mxfp8(x.to(DEV))
+    torch.cuda.synchronize()
+    rc, rs = w4a8.quant_mxfp8(x.float().numpy())
+    assert np.array_equal(sx.cpu().numpy(), rs)
+    assert np.array_equal(xq.cpu().numpy(), rc)
+
+
+def test_quant_special_blocks():
+    x = torch.zeros(2, 128)
+    x[0, 40] = float("inf")
+    x[0, 70] = 2.0 ** -130
+    x[1, 0:32] = torch.linspace(-1000, 1000, 32)
+    x[1, 96] = float("nan")
+    x = x.to(torch.bfloat16)
+    xq, sx = ops.quant_mxfp8(x.to(DEV))
+    rc, rs = w4a8.quant_mxfp8(x.float().numpy())
+    assert np.array_equal(sx.cpu().numpy(), rs)
+    finite = np.repeat(rs != 255, 32, axis=1)
+    assert np.array_equal(xq.cpu().numpy()[finite], rc[finite])
+
+
+def _gemm_case(N, K, M, seed):
+    c = workloads.w4_case(N, K, M, seed=seed)
+    rc, rs = w4a8.quant_mxfp8(c["X"].float().numpy())
+    return c, rc, rs
+
+
+@pytest.mark.parametrize("N,K,M", [(256, 512, 16), (200, 1024, 37), (4096, 3584, 300), (512, 18944, 64),
+                                   (128, 128, 1), (1024, 3072, 129)])
+def test_gemm_parity(N, K, M):
+    c, rc, rs = _gemm_case(N, K, M, seed=N + M)
+    out = ops.h4a8_gemm(torch.from_numpy(rc).to(DEV), torch.from_numpy(rs).to(DEV), c["W"].to(DEV), c["St"].to(DEV))
+    torch.cuda.synchronize()
+    ref = w4a8.gemm(c["W"].numpy(), c["St"].numpy(), rc, rs)
+    got = out.float().cpu().numpy()
+    assert matvec.bf16_excess_error(got, ref) < 1e-4
+
+
+def test_end_to_end_against_w4a16_product():
+    N, K, M = 1024, 3584, 64
+    c = workloads.w4_case(N, K, M, seed=21)
+    got = ops.mxfp4_linear(c["X"].to(DEV), c["W"].to(DEV), c["St"].to(DEV)).float().cpu().numpy()
+    ref = matvec.w4mv(c["W"].numpy(), c["St"].numpy(), c["X"].float().numpy())
+    assert matvec.rel_to_max_error(got, ref) < 5e-2
+
+
+def test_nan_scale_block_gives_nan_rows():
+    N, K, M = 128, 256, 16
+    c = workloads.w4_case(N, K, M, seed=22)
+    x = c["X"].clone()
+    x[3, 100] = float("inf")
+    got = ops.mxfp4_linear(x.to(DEV), c["W"].to(DEV), c["St"].to(DEV)).float().cpu()
+    assert torch.isnan(got[3]).all()
+    assert torch.isfinite(torch.cat([got[:3], got[4:]])).all()
