@@ -27,6 +27,10 @@ void fp8kv_decode_tune(int variant, int target_wgs);
  * LDS ring depth) shape to use for every GQA, or -1 for the per-GQA default. */
 void fp8kv_prefill_tune(int shape);
 
+/* Tuning hook for the MXFP4 x MXFP8 GEMM: 0 = the LDS-pipelined kernel (default), 1 = the
+ * direct-to-register kernel.  Affects later launches. */
+void fp8kv_gemm_tune(int variant);
+
 /* Measurement hook: the next kernel launched by this host thread through any entry point records
  * start_event / stop_event (hipEvent_t, either may be NULL) at its own start and end, via
  * hipExtLaunchKernel.  hipEventElapsedTime between them is then the kernel's execution time.

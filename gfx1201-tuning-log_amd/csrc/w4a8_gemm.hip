@@ -30,12 +30,16 @@
 //     weight-row blocks with all token blocks of each, keeping a weight tile in one L2.
 #include "fp8kv_common.h"
 #include "fp8kv_status.h"
+#include "fp8kv_diag.h"
 
 namespace fp8kv {
 namespace w4a8_detail {
 
 constexpr int kBN = 128, kBM = 128, kBK = 128;
 constexpr int kXcds = 8;
+
+// 0: the LDS-pipelined kernel (default); 1: the direct-to-register kernel (tuning hook only).
+int g_gemm_variant = 0;
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 
@@ -177,6 +181,180 @@ gemm_kernel(Params P)
     }
 }
 
+// ---- LDS-pipelined variant -------------------------------------------------------------------
+// Each 128-k step of the workgroup's tile (weight codes BN x 64 B, activations BM x 128 B stored
+// as two [BM][64 B] halves, and both scale sets, 4 B per row) is copied global -> LDS with direct
+// DMA (global_load_lds; every wave issues the same number of copies per step, so vmcnt counts
+// are exact), S steps in flight in an LDS ring.  After one barrier per step, each wave reads the
+// next step's fragments into registers (ds_read_b128: every read covers one contiguous KB) while
+// its MFMAs work on the current step.
+template <int DPW>
+__device__ __forceinline__ void wait_stages_ahead(int ahead)
+{
+    // ahead = stages issued after the one needed, at most 3
+    if (ahead >= 3) wait_vmcnt<3 * DPW>();
+    else if (ahead == 2) wait_vmcnt<2 * DPW>();
+    else if (ahead == 1) wait_vmcnt<DPW>();
+    else wait_vmcnt<0>();
+}
+
+__device__ __forceinline__ void lds_barrier_all() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int WN, int WM, int S>
+struct LdsGeom {
+    static constexpr int NW = WN * WM;
+    static constexpr int BN = 64 * WN, BM = 64 * WM;
+    static constexpr int W_BYTES = BN * 64;
+    static constexpr int X_BYTES = BM * 128;
+    static constexpr int SW_BYTES = BN * 4, SX_BYTES = BM * 4;
+    static constexpr int STAGE = W_BYTES + X_BYTES + SW_BYTES + SX_BYTES;
+    static constexpr int NW_W = W_BYTES / 1024, NW_X = X_BYTES / 1024;
+    static constexpr int NW_S = (SW_BYTES + SX_BYTES) / 256;
+    static constexpr int NDMA = NW_W + NW_X + NW_S;
+    static constexpr int DPW = NDMA / NW;
+    static constexpr int LDS = S * STAGE;
+    static_assert(NDMA % NW == 0, "copies must split evenly over the waves");
+    static_assert(3 * DPW < 64, "vmcnt range");
+};
+
+template <int WN, int WM, int S>
+__global__ void __launch_bounds__(64 * WN * WM)
+gemm_lds_kernel(Params P)
+{
+    using G = LdsGeom<WN, WM, S>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int L = blockIdx.x;
+    const int total = P.nblk * P.mblk;
+    const int per = (total + kXcds - 1) / kXcds;
+    const int t = (L % kXcds) * per + L / kXcds;
+    if (t >= total) return;
+    const int nb = t / P.mblk, mb = t - nb * P.mblk;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, j = lane >> 4;
+    const int wn = wave % WN, wm = wave / WN;
+    const int N0 = nb * G::BN, M0 = mb * G::BM;
+    const int kh = P.K >> 1, ks = P.K >> 5;
+    const int nsteps = P.K / kBK;
+
+    // This wave's DMA copies: per copy, the lane's source at step 0, the per-step source stride
+    // and the LDS offset within a stage (copy d = wave * DPW + c of the stage's NDMA copies).
+    const uint8_t* src[G::DPW];
+    int sstride[G::DPW], ldsoff[G::DPW];
+    bool dword[G::DPW];
+#pragma unroll
+    for (int c = 0; c < G::DPW; ++c) {
+        const int d = wave * G::DPW + c;
+        if (d < G::NW_W) {                                   // weight codes: rows 16 d .. 16 d + 15
+            int n = N0 + 16 * d + (lane >> 2);
+            n = n < P.N ? n : P.N - 1;
+            src[c] = P.W + (int64_t)n * kh + 16 * (lane & 3);
+            sstride[c] = 64;
+            ldsoff[c] = 1024 * d;
+            dword[c] = false;
+        } else if (d < G::NW_W + G::NW_X) {                  // activations: half e / (BM/16)
+            const int e = d - G::NW_W;
+            const int half = e / (G::BM / 16), rb = e % (G::BM / 16);
+            int m = M0 + 16 * rb + (lane >> 2);
+            m = m < P.M ? m : P.M - 1;
+            src[c] = P.Xq + (int64_t)m * P.K + 64 * half + 16 * (lane & 3);
+            sstride[c] = 128;
+            ldsoff[c] = G::W_BYTES + 1024 * e;
+            dword[c] = false;
+        } else {                                             // scales: 64 rows per copy
+            const int e = d - G::NW_W - G::NW_X;
+            if (e < G::BN / 64) {
+                int n = N0 + 64 * e + lane;
+                n = n < P.N ? n : P.N - 1;
+                src[c] = P.St + (int64_t)n * ks;
+                ldsoff[c] = G::W_BYTES + G::X_BYTES + 256 * e;
+            } else {
+                const int e2 = e - G::BN / 64;
+                int m = M0 + 64 * e2 + lane;
+                m = m < P.M ? m : P.M - 1;
+                src[c] = P.Sx + (int64_t)m * ks;
+                ldsoff[c] = G::W_BYTES + G::X_BYTES + G::SW_BYTES + 256 * e2;
+            }
+            sstride[c] = 4;
+            dword[c] = true;
+        }
+    }
+    auto issue = [&](int step) {
+        unsigned char* stage = smem + (step % S) * G::STAGE;
+#pragma unroll
+        for (int c = 0; c < G::DPW; ++c) {
+            const uint8_t* p = src[c] + (int64_t)step * sstride[c];
+            if (dword[c]) dma4_to_lds(p, stage + ldsoff[c]);
+            else dma16_to_lds(p, stage + ldsoff[c]);
+        }
+    };
+    // fragment offsets within a stage
+    int aoff[4], boff[4], saoff[4], sboff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        aoff[i] = (wn * 64 + 16 * i + r) * 64 + 16 * j;
+        boff[i] = G::W_BYTES + (wm * 64 + 16 * i + r) * 64 + 16 * j;
+        saoff[i] = G::W_BYTES + G::X_BYTES + (wn * 64 + 16 * i + r) * 4;
+        sboff[i] = G::W_BYTES + G::X_BYTES + G::SW_BYTES + (wm * 64 + 16 * i + r) * 4;
+    }
+    auto read = [&](Frags& f, int step) {
+        const unsigned char* stage = smem + (step % S) * G::STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f.a[i] = *reinterpret_cast<const u32x4_t*>(stage + aoff[i]);
+            f.b[i][0] = *reinterpret_cast<const u32x4_t*>(stage + boff[i]);
+            f.b[i][1] = *reinterpret_cast<const u32x4_t*>(stage + boff[i] + G::BM * 64);
+            f.sa[i] = *reinterpret_cast<const uint32_t*>(stage + saoff[i]);
+            f.sb[i] = *reinterpret_cast<const uint32_t*>(stage + sboff[i]);
+        }
+    };
+
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+
+    // Ring protocol for step q: every wave waits until its own copies of step q have landed (at
+    // most min(S - 2, steps left) later steps still in flight), the barrier makes everyone's
+    // copies visible and retires step q - 1's buffer (each wave read it, lgkmcnt(0), before the
+    // barrier), step q + S - 1 is copied into that buffer, and step q's fragments are read.
+    auto sync_read = [&](Frags& f, int q) {
+        const int left = nsteps - 1 - q;
+        wait_stages_ahead<G::DPW>(left < S - 2 ? left : S - 2);
+        lds_barrier_all();
+        if (q + S - 1 < nsteps) issue(q + S - 1);
+        read(f, q);
+    };
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+        if (s < nsteps) issue(s);
+    Frags fa, fb;
+    sync_read(fa, 0);
+    for (int s = 0; s < nsteps; s += 2) {
+        if (s + 1 < nsteps) sync_read(fb, s + 1);
+        compute(fa, acc, j);                         // MFMAs on step s while step s + 1 is read
+        if (s + 1 >= nsteps) break;
+        if (s + 2 < nsteps) sync_read(fa, s + 2);
+        compute(fb, acc, j);
+    }
+
+    const int n0 = N0 + wn * 64, m0 = M0 + wm * 64;
+#pragma unroll
+    for (int im = 0; im < 4; ++im) {
+        const int m = m0 + 16 * im + r;
+        if (m >= P.M) continue;
+        __bf16* orow = P.Out + (int64_t)m * P.N;
+#pragma unroll
+        for (int in = 0; in < 4; ++in) {
+            const int n = n0 + 16 * in + 4 * j;
+            if (n >= P.N) continue;
+            const f32x4_t v = acc[in][im];
+            *reinterpret_cast<u32x2_t*>(orow + n) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        }
+    }
+}
+
 // ---- activation quantiser: bf16 [M, K] -> e4m3fn [M, K] + e8m0 [M, K/32] ---------------------
 // One thread per 32-element block: four 16-byte loads, the block maximum, two 16-byte stores.
 __global__ void __launch_bounds__(256)
@@ -285,7 +463,18 @@ extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const vo
     const int64_t total = (int64_t)P.nblk * P.mblk;
     if (total > 0x7FFFFFFF - kXcds) return FP8KV_ERR_SHAPE;
     const int64_t grid = ((total + kXcds - 1) / kXcds) * kXcds;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
-    launch_kernel(gemm_kernel, dim3((unsigned)grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), P);
+    if (g_gemm_variant == 1) {
+        launch_kernel(gemm_kernel, dim3((unsigned)grid), dim3(256), 0, st, P);
+    } else {
+        using G = LdsGeom<2, 2, 4>;
+        launch_kernel(gemm_lds_kernel<2, 2, 4>, dim3((unsigned)grid), dim3(64 * G::NW), G::LDS, st, P);
+    }
     return finish_launch();
+}
+
+extern "C" void fp8kv_gemm_tune(int variant)
+{
+    fp8kv::w4a8_detail::g_gemm_variant = variant == 1 ? 1 : 0;
 }
