@@ -272,14 +272,14 @@ def bench_gate_up_silu(M: int, steps: int, warmup: int, N: int = 37888, K: int =
 MFMA_FP8_PEAK_TFLOPS = 5000.0      # dense fp8 (and fp8 x fp4) MFMA peak of MI355X
 
 
-def bench_w4a8_gemm(M: int, steps: int, warmup: int, variant: int = 0):
+def bench_w4a8_gemm(M: int, steps: int, warmup: int, variant: int = -1, order: int = 0):
     """The configs[4] linears at M tokens (a prefill chunk) through the MXFP8 quantiser and the
     MXFP4 x MXFP8 block-scaled GEMM; weights rotated above the MALL."""
     import torch
     from fp8kv_amd import ops, workloads
     dev = torch.device("cuda")
     from fp8kv_amd import _lib
-    _lib.load().fp8kv_gemm_tune(variant)
+    _lib.load().fp8kv_gemm_tune(variant, order)
     out = {}
     x = torch.randn(M, 18944, device=dev).to(torch.bfloat16)
     for name, N, K in STACK_LINEARS:
@@ -303,7 +303,7 @@ def bench_w4a8_gemm(M: int, steps: int, warmup: int, variant: int = 0):
                      "us_quant": round(statistics.mean(perq) * 1e3, 3)}
         del ws
         torch.cuda.empty_cache()
-    _lib.load().fp8kv_gemm_tune(0)
+    _lib.load().fp8kv_gemm_tune(-1, 0)
     return out
 
 

@@ -27,9 +27,11 @@ void fp8kv_decode_tune(int variant, int target_wgs);
  * LDS ring depth) shape to use for every GQA, or -1 for the per-GQA default. */
 void fp8kv_prefill_tune(int shape);
 
-/* Tuning hook for the MXFP4 x MXFP8 GEMM: 0 = the LDS-pipelined kernel (default), 1 = the
- * direct-to-register kernel.  Affects later launches. */
-void fp8kv_gemm_tune(int variant);
+/* Tuning hook for the MXFP4 x MXFP8 GEMM: kernel variant (0..5, any other value selects the
+ * default, 5: LDS ring of 2 steps, fragments single-buffered, two waves per SIMD) and tile order
+ * (0 = XCDs split the token blocks, the default; 1 = XCDs split the weight blocks only).
+ * Affects later launches. */
+void fp8kv_gemm_tune(int variant, int order);
 
 /* Measurement hook: the next kernel launched by this host thread through any entry point records
  * start_event / stop_event (hipEvent_t, either may be NULL) at its own start and end, via

@@ -38,17 +38,29 @@ namespace w4a8_detail {
 constexpr int kBN = 128, kBM = 128, kBK = 128;
 constexpr int kXcds = 8;
 
-// 0: the LDS-pipelined kernel (default); 1: the direct-to-register kernel (tuning hook only).
-int g_gemm_variant = 0;
+// 0: the LDS kernel, fragments double-buffered, 4-step ring, one workgroup per CU; 1: the
+// direct-to-register kernel; 2 / 3: as 0 with a 3 / 5-step ring; 4: single-buffered fragments,
+// registers capped for two waves per SIMD, 3-step ring; 5 (default): as 4 with a 2-step ring
+// (51 KB of LDS, so up to three workgroups share a CU).  Measured on the configs[4] linears at
+// M = 2048: 5 ~1.40 PFLOP/s, 4 ~1.33, 0 ~1.01, 1 ~0.40.
+constexpr int kDefaultVariant = 5;
+int g_gemm_variant = kDefaultVariant;
+// 0: XCDs split the token blocks (default); 1: XCDs split the weight blocks only.
+int g_gemm_order = 0;
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 
 struct Frags {
     u32x4_t a[4];        // weight n-tile i: 16 bytes (32 e2m1 codes)
-    u32x4_t b[4][2];     // token m-tile i: 16 bytes at k 16j and at 64 + 16j
+    v8i b[4];            // token m-tile i: 16 bytes at k 16j (low half) and at 64 + 16j (high half)
     uint32_t sa[4];      // scale dword of (row, k step) per n-tile: 4 blocks, this lane's is byte j
     uint32_t sb[4];
 };
+
+__device__ __forceinline__ v8i concat8(u32x4_t lo, u32x4_t hi)
+{
+    return (v8i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
 
 struct Params {
     const uint8_t* W;
@@ -58,7 +70,26 @@ struct Params {
     __bf16* Out;
     int N, K, M;
     int nblk, mblk;
+    int gm, gn;          // tile order: the 8 XCDs split the token blocks gm ways and the weight blocks gn ways
 };
+
+// Tile of workgroup L, or false when L has none.  Workgroup L runs on XCD L % 8 (round-robin
+// dispatch); XCD x = (xm, xn) takes token blocks xm, xm + gm, ... and the xn-th range of weight
+// blocks, weight-block major, so each XCD's L2 holds its share of the activations and the
+// weight tiles it streams are shared by the workgroups running it at the same time.
+__device__ __forceinline__ bool tile_of(const Params& P, int L, int& nb, int& mb)
+{
+    const int x = L % kXcds, slot = L / kXcds;
+    const int xm = x % P.gm, xn = x / P.gm;
+    const int my_m = (P.mblk - xm + P.gm - 1) / P.gm;
+    const int nper = (P.nblk + P.gn - 1) / P.gn;
+    const int n_lo = xn * nper;
+    const int n_hi = n_lo + nper < P.nblk ? n_lo + nper : P.nblk;
+    if (my_m <= 0 || n_lo >= n_hi || slot >= my_m * (n_hi - n_lo)) return false;
+    nb = n_lo + slot / my_m;
+    mb = xm + P.gm * (slot % my_m);
+    return true;
+}
 
 __device__ __forceinline__ uint32_t load_u32(const void* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
@@ -71,8 +102,7 @@ __device__ __forceinline__ void load_frags(Frags& f, const Params& P, const uint
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         f.a[i] = load_nt_16(wrow[i] + ((kk + 32 * j) >> 1));
-        f.b[i][0] = load_16(xrow[i] + kk + 16 * j);
-        f.b[i][1] = load_16(xrow[i] + kk + 64 + 16 * j);
+        f.b[i] = concat8(load_16(xrow[i] + kk + 16 * j), load_16(xrow[i] + kk + 64 + 16 * j));
         f.sa[i] = load_u32(srow[i] + (kk >> 5));
         f.sb[i] = load_u32(sxrow[i] + (kk >> 5));
     }
@@ -82,20 +112,21 @@ template <int I, int J>
 __device__ __forceinline__ f32x4_t mfma_tile(const Frags& f, uint32_t sa, uint32_t sb, f32x4_t acc)
 {
     const v8i a = {(int)f.a[I][0], (int)f.a[I][1], (int)f.a[I][2], (int)f.a[I][3], 0, 0, 0, 0};
-    const v8i b = {(int)f.b[J][0][0], (int)f.b[J][0][1], (int)f.b[J][0][2], (int)f.b[J][0][3],
-                   (int)f.b[J][1][0], (int)f.b[J][1][1], (int)f.b[J][1][2], (int)f.b[J][1][3]};
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc, 4, 0, I, (int)sa, J, (int)sb);
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, f.b[J], acc, 4, 0, I, (int)sa, J, (int)sb);
 }
 
 __device__ __forceinline__ void compute(const Frags& f, f32x4_t (&acc)[4][4], int j)
 {
     // this lane's scale byte (k block j) of each tile, packed: tile i in byte i (op_sel picks it)
-    uint32_t sa = 0, sb = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        sa |= ((f.sa[i] >> (8 * j)) & 0xFFu) << (8 * i);
-        sb |= ((f.sb[i] >> (8 * j)) & 0xFFu) << (8 * i);
-    }
+    // v_perm_b32(hi, lo, sel) picks bytes of {hi, lo}; selector bytes j and j + 4 take byte j
+    // of lo and of hi
+    const uint32_t sel = (uint32_t)j | ((uint32_t)(j + 4) << 8);
+    const uint32_t a01 = __builtin_amdgcn_perm(f.sa[1], f.sa[0], sel);
+    const uint32_t a23 = __builtin_amdgcn_perm(f.sa[3], f.sa[2], sel);
+    const uint32_t b01 = __builtin_amdgcn_perm(f.sb[1], f.sb[0], sel);
+    const uint32_t b23 = __builtin_amdgcn_perm(f.sb[3], f.sb[2], sel);
+    const uint32_t sa = (a01 & 0xFFFFu) | (a23 << 16);
+    const uint32_t sb = (b01 & 0xFFFFu) | (b23 << 16);
     acc[0][0] = mfma_tile<0, 0>(f, sa, sb, acc[0][0]);
     acc[0][1] = mfma_tile<0, 1>(f, sa, sb, acc[0][1]);
     acc[0][2] = mfma_tile<0, 2>(f, sa, sb, acc[0][2]);
@@ -117,14 +148,8 @@ __device__ __forceinline__ void compute(const Frags& f, f32x4_t (&acc)[4][4], in
 __global__ void __launch_bounds__(256)
 gemm_kernel(Params P)
 {
-    // XCD-aware tile order: workgroup id L runs on XCD L % 8; XCD x takes tiles
-    // [x * per, (x + 1) * per) of the n-major order (all token blocks of a weight block together).
-    const int L = blockIdx.x;
-    const int total = P.nblk * P.mblk;
-    const int per = (total + kXcds - 1) / kXcds;
-    const int t = (L % kXcds) * per + L / kXcds;
-    if (t >= total) return;
-    const int nb = t / P.mblk, mb = t - nb * P.mblk;
+    int nb, mb;
+    if (!tile_of(P, blockIdx.x, nb, mb)) return;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -217,18 +242,16 @@ struct LdsGeom {
     static_assert(3 * DPW < 64, "vmcnt range");
 };
 
-template <int WN, int WM, int S>
-__global__ void __launch_bounds__(64 * WN * WM)
-gemm_lds_kernel(Params P)
+// DB: fragments double-buffered in registers (one workgroup per CU) or single-buffered with two
+// workgroups per CU (registers capped at 256 per lane, so two waves share each SIMD and one
+// wave's MFMAs cover the other's waits).
+template <int WN, int WM, int S, bool DB>
+__device__ __forceinline__ void gemm_lds_body(const Params& P)
 {
     using G = LdsGeom<WN, WM, S>;
     extern __shared__ __align__(16) unsigned char smem[];
-    const int L = blockIdx.x;
-    const int total = P.nblk * P.mblk;
-    const int per = (total + kXcds - 1) / kXcds;
-    const int t = (L % kXcds) * per + L / kXcds;
-    if (t >= total) return;
-    const int nb = t / P.mblk, mb = t - nb * P.mblk;
+    int nb, mb;
+    if (!tile_of(P, blockIdx.x, nb, mb)) return;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, j = lane >> 4;
@@ -237,75 +260,84 @@ gemm_lds_kernel(Params P)
     const int kh = P.K >> 1, ks = P.K >> 5;
     const int nsteps = P.K / kBK;
 
-    // This wave's DMA copies: per copy, the lane's source at step 0, the per-step source stride
-    // and the LDS offset within a stage (copy d = wave * DPW + c of the stage's NDMA copies).
-    const uint8_t* src[G::DPW];
-    int sstride[G::DPW], ldsoff[G::DPW];
-    bool dword[G::DPW];
+    // This wave's DMA copies: copy c of wave w is copy d = c * NW + w of the stage, so the kind of
+    // every copy (weight codes, activations, scales) is known at compile time (each kind's copy
+    // count is a multiple of the wave count).  Sources are a uniform tile base (advanced per step)
+    // plus a 32-bit lane offset, the form the copy instruction takes with a scalar base.
+    static_assert(G::NW_W % G::NW == 0 && G::NW_X % G::NW == 0 && G::NW_S % G::NW == 0,
+                  "copy kinds must split evenly over the waves");
+    const uint8_t* const wtile = P.W + (int64_t)N0 * kh;
+    const uint8_t* const xtile = P.Xq + (int64_t)M0 * P.K;
+    const uint8_t* const swtile = P.St + (int64_t)N0 * ks;
+    const uint8_t* const sxtile = P.Sx + (int64_t)M0 * ks;
+    uint32_t loff[G::DPW];
+    int ldsoff[G::DPW];
 #pragma unroll
     for (int c = 0; c < G::DPW; ++c) {
-        const int d = wave * G::DPW + c;
-        if (d < G::NW_W) {                                   // weight codes: rows 16 d .. 16 d + 15
-            int n = N0 + 16 * d + (lane >> 2);
-            n = n < P.N ? n : P.N - 1;
-            src[c] = P.W + (int64_t)n * kh + 16 * (lane & 3);
-            sstride[c] = 64;
+        const int d = c * G::NW + wave;
+        if (c < G::NW_W / G::NW) {                           // weight codes: rows 16 d .. 16 d + 15
+            int n = 16 * d + (lane >> 2);
+            n = N0 + n < P.N ? n : P.N - 1 - N0;
+            loff[c] = (uint32_t)n * (uint32_t)kh + 16u * (uint32_t)(lane & 3);
             ldsoff[c] = 1024 * d;
-            dword[c] = false;
-        } else if (d < G::NW_W + G::NW_X) {                  // activations: half e / (BM/16)
+        } else if (c < (G::NW_W + G::NW_X) / G::NW) {        // activations: half e / (BM/16)
             const int e = d - G::NW_W;
             const int half = e / (G::BM / 16), rb = e % (G::BM / 16);
-            int m = M0 + 16 * rb + (lane >> 2);
-            m = m < P.M ? m : P.M - 1;
-            src[c] = P.Xq + (int64_t)m * P.K + 64 * half + 16 * (lane & 3);
-            sstride[c] = 128;
+            int m = 16 * rb + (lane >> 2);
+            m = M0 + m < P.M ? m : P.M - 1 - M0;
+            loff[c] = (uint32_t)m * (uint32_t)P.K + 64u * half + 16u * (uint32_t)(lane & 3);
             ldsoff[c] = G::W_BYTES + 1024 * e;
-            dword[c] = false;
         } else {                                             // scales: 64 rows per copy
             const int e = d - G::NW_W - G::NW_X;
             if (e < G::BN / 64) {
-                int n = N0 + 64 * e + lane;
-                n = n < P.N ? n : P.N - 1;
-                src[c] = P.St + (int64_t)n * ks;
+                int n = 64 * e + lane;
+                n = N0 + n < P.N ? n : P.N - 1 - N0;
+                loff[c] = (uint32_t)n * (uint32_t)ks;
                 ldsoff[c] = G::W_BYTES + G::X_BYTES + 256 * e;
             } else {
                 const int e2 = e - G::BN / 64;
-                int m = M0 + 64 * e2 + lane;
-                m = m < P.M ? m : P.M - 1;
-                src[c] = P.Sx + (int64_t)m * ks;
+                int m = 64 * e2 + lane;
+                m = M0 + m < P.M ? m : P.M - 1 - M0;
+                loff[c] = (uint32_t)m * (uint32_t)ks;
                 ldsoff[c] = G::W_BYTES + G::X_BYTES + G::SW_BYTES + 256 * e2;
             }
-            sstride[c] = 4;
-            dword[c] = true;
         }
     }
     auto issue = [&](int step) {
         unsigned char* stage = smem + (step % S) * G::STAGE;
+        const uint8_t* wb = wtile + (int64_t)step * 64;
+        const uint8_t* xb = xtile + (int64_t)step * 128;
 #pragma unroll
         for (int c = 0; c < G::DPW; ++c) {
-            const uint8_t* p = src[c] + (int64_t)step * sstride[c];
-            if (dword[c]) dma4_to_lds(p, stage + ldsoff[c]);
-            else dma16_to_lds(p, stage + ldsoff[c]);
+            if (c < G::NW_W / G::NW) {
+                dma16_to_lds(wb + loff[c], stage + ldsoff[c]);
+            } else if (c < (G::NW_W + G::NW_X) / G::NW) {
+                dma16_to_lds(xb + loff[c], stage + ldsoff[c]);
+            } else {
+                const int e = c * G::NW + wave - G::NW_W - G::NW_X;     // uniform
+                const uint8_t* sbase = (e < G::BN / 64 ? swtile : sxtile) + (int64_t)step * 4;
+                dma4_to_lds(sbase + loff[c], stage + ldsoff[c]);
+            }
         }
     };
-    // fragment offsets within a stage
-    int aoff[4], boff[4], saoff[4], sboff[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        aoff[i] = (wn * 64 + 16 * i + r) * 64 + 16 * j;
-        boff[i] = G::W_BYTES + (wm * 64 + 16 * i + r) * 64 + 16 * j;
-        saoff[i] = G::W_BYTES + G::X_BYTES + (wn * 64 + 16 * i + r) * 4;
-        sboff[i] = G::W_BYTES + G::X_BYTES + G::SW_BYTES + (wm * 64 + 16 * i + r) * 4;
-    }
+    // fragment reads: one lane base per kind, tiles at constant offsets from it
+    const int abase = (wn * 64 + r) * 64 + 16 * j;
+    const int bbase = G::W_BYTES + (wm * 64 + r) * 64 + 16 * j;
+    const int sabase = G::W_BYTES + G::X_BYTES + (wn * 64 + r) * 4;
+    const int sbbase = G::W_BYTES + G::X_BYTES + G::SW_BYTES + (wm * 64 + r) * 4;
     auto read = [&](Frags& f, int step) {
         const unsigned char* stage = smem + (step % S) * G::STAGE;
+        const unsigned char* pa = stage + abase;
+        const unsigned char* pb = stage + bbase;
+        const unsigned char* psa = stage + sabase;
+        const unsigned char* psb = stage + sbbase;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            f.a[i] = *reinterpret_cast<const u32x4_t*>(stage + aoff[i]);
-            f.b[i][0] = *reinterpret_cast<const u32x4_t*>(stage + boff[i]);
-            f.b[i][1] = *reinterpret_cast<const u32x4_t*>(stage + boff[i] + G::BM * 64);
-            f.sa[i] = *reinterpret_cast<const uint32_t*>(stage + saoff[i]);
-            f.sb[i] = *reinterpret_cast<const uint32_t*>(stage + sboff[i]);
+            f.a[i] = *reinterpret_cast<const u32x4_t*>(pa + 1024 * i);
+            f.b[i] = concat8(*reinterpret_cast<const u32x4_t*>(pb + 1024 * i),
+                             *reinterpret_cast<const u32x4_t*>(pb + 1024 * i + G::BM * 64));
+            f.sa[i] = *reinterpret_cast<const uint32_t*>(psa + 64 * i);
+            f.sb[i] = *reinterpret_cast<const uint32_t*>(psb + 64 * i);
         }
     };
 
@@ -329,14 +361,24 @@ gemm_lds_kernel(Params P)
 #pragma unroll
     for (int s = 0; s < S - 1; ++s)
         if (s < nsteps) issue(s);
-    Frags fa, fb;
-    sync_read(fa, 0);
-    for (int s = 0; s < nsteps; s += 2) {
-        if (s + 1 < nsteps) sync_read(fb, s + 1);
-        compute(fa, acc, j);                         // MFMAs on step s while step s + 1 is read
-        if (s + 1 >= nsteps) break;
-        if (s + 2 < nsteps) sync_read(fa, s + 2);
-        compute(fb, acc, j);
+    if constexpr (DB) {
+        Frags fa, fb;
+        sync_read(fa, 0);
+        // pairs of steps without an exit in between (the accumulators stay in place), then the
+        // odd last step
+        for (int s = 0; s + 1 < nsteps; s += 2) {
+            sync_read(fb, s + 1);
+            compute(fa, acc, j);                     // MFMAs on step s while step s + 1 is read
+            if (s + 2 < nsteps) sync_read(fa, s + 2);
+            compute(fb, acc, j);
+        }
+        if (nsteps & 1) compute(fa, acc, j);
+    } else {
+        Frags f;
+        for (int s = 0; s < nsteps; ++s) {
+            sync_read(f, s);
+            compute(f, acc, j);
+        }
     }
 
     const int n0 = N0 + wn * 64, m0 = M0 + wm * 64;
@@ -353,6 +395,20 @@ gemm_lds_kernel(Params P)
             *reinterpret_cast<u32x2_t*>(orow + n) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
     }
+}
+
+template <int WN, int WM, int S>
+__global__ void __launch_bounds__(64 * WN * WM)
+gemm_lds_kernel(Params P)
+{
+    gemm_lds_body<WN, WM, S, true>(P);
+}
+
+template <int WN, int WM, int S>
+__global__ void __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_lds2_kernel(Params P)
+{
+    gemm_lds_body<WN, WM, S, false>(P);
 }
 
 // ---- activation quantiser: bf16 [M, K] -> e4m3fn [M, K] + e8m0 [M, K/32] ---------------------
@@ -458,23 +514,47 @@ extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const vo
     P.N = N;
     P.K = K;
     P.M = M;
-    P.nblk = (N + kBN - 1) / kBN;
-    P.mblk = (M + kBM - 1) / kBM;
-    const int64_t total = (int64_t)P.nblk * P.mblk;
-    if (total > 0x7FFFFFFF - kXcds) return FP8KV_ERR_SHAPE;
-    const int64_t grid = ((total + kXcds - 1) / kXcds) * kXcds;
+    const int variant = g_gemm_variant;
+    const int BN = variant == 1 ? kBN : 128, BM = variant == 1 ? kBM : 128;
+    P.nblk = (N + BN - 1) / BN;
+    P.mblk = (M + BM - 1) / BM;
+    if ((int64_t)P.nblk * P.mblk > 0x7FFFFFFF - kXcds) return FP8KV_ERR_SHAPE;
+    // token blocks split over up to 8 XCDs (the largest power of two dividing their count, so
+    // every XCD gets the same number), the weight blocks over the rest
+    int gm = 1;
+    while (gm < kXcds && P.mblk % (2 * gm) == 0) gm *= 2;
+    if (g_gemm_order == 1) gm = 1;                         // weight-block split only
+    P.gm = gm;
+    P.gn = kXcds / gm;
+    const int64_t per_xcd = (int64_t)((P.mblk + gm - 1) / gm) * ((P.nblk + P.gn - 1) / P.gn);
+    const int64_t grid = per_xcd * kXcds;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
-    if (g_gemm_variant == 1) {
-        launch_kernel(gemm_kernel, dim3((unsigned)grid), dim3(256), 0, st, P);
-    } else {
-        using G = LdsGeom<2, 2, 4>;
-        launch_kernel(gemm_lds_kernel<2, 2, 4>, dim3((unsigned)grid), dim3(64 * G::NW), G::LDS, st, P);
+    switch (variant) {
+        case 1:
+            launch_kernel(gemm_kernel, dim3((unsigned)grid), dim3(256), 0, st, P);
+            break;
+        case 2:
+            launch_kernel(gemm_lds_kernel<2, 2, 3>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 3>::LDS, st, P);
+            break;
+        case 3:
+            launch_kernel(gemm_lds_kernel<2, 2, 5>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 5>::LDS, st, P);
+            break;
+        case 4:
+            launch_kernel(gemm_lds2_kernel<2, 2, 3>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 3>::LDS, st, P);
+            break;
+        default:
+            launch_kernel(gemm_lds2_kernel<2, 2, 2>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 2>::LDS, st, P);
+            break;
+        case 0:
+            launch_kernel(gemm_lds_kernel<2, 2, 4>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 4>::LDS, st, P);
+            break;
     }
     return finish_launch();
 }
 
-extern "C" void fp8kv_gemm_tune(int variant)
+extern "C" void fp8kv_gemm_tune(int variant, int order)
 {
-    fp8kv::w4a8_detail::g_gemm_variant = variant == 1 ? 1 : 0;
+    fp8kv::w4a8_detail::g_gemm_variant = (variant >= 0 && variant <= 5) ? variant : fp8kv::w4a8_detail::kDefaultVariant;
+    fp8kv::w4a8_detail::g_gemm_order = order == 1 ? 1 : 0;
 }

@@ -25,10 +25,17 @@ SOURCES = ["h4mv.hip", "h4mv_repack.hip", "decode_attn.hip", "prefill_attn.hip",
 # Packed-fp32 VALU forms are disabled for every HIP file built here (the compiler would otherwise
 # emit v_pk_{add,mul,fma}_f32 from ordinary float code).
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
+
+# Per-file code-generation options.  The block-scaled MFMA accumulates in place only in its VGPR
+# form; left to choose, the compiler keeps the GEMM accumulators in VGPRs and copies them into
+# AGPRs around every MFMA.
+FILE_FLAGS = {
+    "w4a8_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def hipcc() -> str:
@@ -38,23 +45,35 @@ def hipcc() -> str:
     raise FileNotFoundError("hipcc not found (set HIPCC)")
 
 
-def build(out: str = LIB_PATH, verbose: bool = False) -> str:
-    """Compile every source in SOURCES into one shared library; atomic replace of ``out``."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    fd, tmp = tempfile.mkstemp(prefix=".fp8kv_amd_", suffix=".so", dir=os.path.dirname(out))
-    os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), file=sys.stderr)
-    try:
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-6000:]}")
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-6000:]}")
+
+
+def build(out: str = LIB_PATH, verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile every source in SOURCES (one object each, in parallel) and link them into one
+    shared library; atomic replace of ``out``."""
+    from concurrent.futures import ThreadPoolExecutor
+    cc = hipcc()
+    with tempfile.TemporaryDirectory(prefix=".fp8kv_amd_build_", dir=os.path.dirname(out)) as tmpdir:
+        objs = []
+        cmds = []
+        for src in SOURCES:
+            obj = os.path.join(tmpdir, os.path.splitext(src)[0] + ".o")
+            objs.append(obj)
+            cmds.append([cc, *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+                         os.path.join(CSRC, src), "-o", obj])
+        workers = jobs or min(len(cmds), max(1, min(8, os.cpu_count() or 1)))
+        with ThreadPoolExecutor(max_workers=workers) as ex:
+            for f in [ex.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        tmp = os.path.join(tmpdir, LIB_NAME)
+        _run([cc, *HIPCC_FLAGS, "-shared", *objs, "-o", tmp], verbose)
         os.chmod(tmp, 0o755)
         os.replace(tmp, out)
-    finally:
-        if os.path.exists(tmp):
-            os.unlink(tmp)
     return out
 
 

@@ -55,18 +55,18 @@ def _gemm_case(N, K, M, seed):
     return c, rc, rs
 
 
-@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("variant,order", [(-1, 0), (0, 0), (0, 1), (1, 0), (2, 0), (3, 1), (4, 0), (5, 1)])
 @pytest.mark.parametrize("N,K,M", [(256, 512, 16), (200, 1024, 37), (4096, 3584, 300), (512, 18944, 64),
                                    (128, 128, 1), (1024, 3072, 129), (384, 256, 200), (128, 384, 64)])
-def test_gemm_parity(N, K, M, variant):
+def test_gemm_parity(N, K, M, variant, order):
     lib = _lib.load()
     c, rc, rs = _gemm_case(N, K, M, seed=N + M)
     try:
-        lib.fp8kv_gemm_tune(variant)
+        lib.fp8kv_gemm_tune(variant, order)
         out = ops.h4a8_gemm(torch.from_numpy(rc).to(DEV), torch.from_numpy(rs).to(DEV), c["W"].to(DEV), c["St"].to(DEV))
         torch.cuda.synchronize()
     finally:
-        lib.fp8kv_gemm_tune(0)
+        lib.fp8kv_gemm_tune(-1, 0)
     ref = w4a8.gemm(c["W"].numpy(), c["St"].numpy(), rc, rs)
     got = out.float().cpu().numpy()
     assert matvec.bf16_excess_error(got, ref) < 1e-4
