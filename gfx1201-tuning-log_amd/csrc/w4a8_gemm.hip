@@ -31,6 +31,7 @@
 #include "fp8kv_common.h"
 #include "fp8kv_status.h"
 #include "fp8kv_diag.h"
+#include <utility>
 
 namespace fp8kv {
 namespace w4a8_detail {
@@ -40,11 +41,22 @@ constexpr int kXcds = 8;
 
 // 0: the LDS kernel, fragments double-buffered, 4-step ring, one workgroup per CU; 1: the
 // direct-to-register kernel; 2 / 3: as 0 with a 3 / 5-step ring; 4: single-buffered fragments,
-// registers capped for two waves per SIMD, 3-step ring; 5 (default): as 4 with a 2-step ring
-// (51 KB of LDS, so up to three workgroups share a CU).  Measured on the configs[4] linears at
-// M = 2048: 5 ~1.40 PFLOP/s, 4 ~1.33, 0 ~1.01, 1 ~0.40.
-constexpr int kDefaultVariant = 5;
+// registers capped for two waves per SIMD, 3-step ring; 5: as 4 with a 2-step ring (51 KB of
+// LDS, so up to three workgroups share a CU); 6 / 7: as 5 with 8 x 4 / 4 x 8 MFMA tiles per wave.
+// Measured on the configs[4] linears at M = 2048: 6 ~1.22-1.69 PFLOP/s, 5 ~1.27-1.41, 7 ~1.05-1.27,
+// 4 ~1.33, 0 ~1.01, 1 ~0.40.
+// Default (-1): variant 6 (the 8 x 4 wave tile, 256 x 128 per workgroup) when its grid has at
+// least 256 tiles or K >= 8192, else variant 5 (measured at the configs[4] linears, M = 2048:
+// gate/up 1.41 -> 1.66 PFLOP/s and down 1.41 -> 1.47 with variant 6, o 1.27 -> 1.22).
+constexpr int kDefaultVariant = -1;
 int g_gemm_variant = kDefaultVariant;
+
+inline int pick_variant(int N, int K, int M)
+{
+    if (g_gemm_variant >= 0) return g_gemm_variant;
+    const int64_t tiles6 = (int64_t)((N + 255) / 256) * ((M + 127) / 128);
+    return (tiles6 >= 256 || K >= 8192) ? 6 : 5;
+}
 // 0: XCDs split the token blocks (default); 1: XCDs split the weight blocks only.
 int g_gemm_order = 0;
 
@@ -411,6 +423,203 @@ gemm_lds2_kernel(Params P)
     gemm_lds_body<WN, WM, S, false>(P);
 }
 
+// ---- larger wave tiles -------------------------------------------------------------------------
+// Each wave computes TN x TM MFMA tiles (16 x 16 each): TN weight tiles share one activation
+// fragment and TM activation tiles one weight fragment, so a 128-k step costs 16 (TN + 2 TM)
+// bytes of LDS reads per lane for TN * TM MFMAs.  Scale bytes: four tiles per VGPR (op_sel).
+template <int WN, int WM, int TN, int TM, int S>
+struct BigGeom {
+    static constexpr int NW = WN * WM;
+    static constexpr int BN = 16 * TN * WN, BM = 16 * TM * WM;
+    static constexpr int W_BYTES = BN * 64;
+    static constexpr int X_BYTES = BM * 128;
+    static constexpr int SW_BYTES = BN * 4, SX_BYTES = BM * 4;
+    static constexpr int STAGE = W_BYTES + X_BYTES + SW_BYTES + SX_BYTES;
+    static constexpr int NW_W = W_BYTES / 1024, NW_X = X_BYTES / 1024;
+    static constexpr int NW_SW = SW_BYTES / 256, NW_SX = SX_BYTES / 256;
+    // scale copies padded to a multiple of the wave count (the extra copies repeat the last one)
+    static constexpr int NW_S = ((NW_SW + NW_SX + NW - 1) / NW) * NW;
+    static constexpr int NDMA = NW_W + NW_X + NW_S;
+    static constexpr int DPW = NDMA / NW;
+    static constexpr int LDS = S * STAGE;
+    static_assert(NW_W % NW == 0 && NW_X % NW == 0, "copy kinds must split evenly over the waves");
+    static_assert(TN % 4 == 0 && TM % 4 == 0, "tiles come in groups of four (one scale VGPR)");
+    static_assert((S - 1) * DPW < 64, "vmcnt range");
+};
+
+template <int TN, int TM>
+struct BigFrags {
+    u32x4_t a[TN];
+    v8i b[TM];
+    uint32_t sa[TN];
+    uint32_t sb[TM];
+};
+
+template <int TN, int TM, int... Is>
+__device__ __forceinline__ void big_mfmas(const BigFrags<TN, TM>& f, const uint32_t (&sa)[TN / 4],
+                                          const uint32_t (&sb)[TM / 4], f32x4_t (&acc)[TN][TM],
+                                          std::integer_sequence<int, Is...>)
+{
+    ((acc[Is / TM][Is % TM] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+          (v8i){(int)f.a[Is / TM][0], (int)f.a[Is / TM][1], (int)f.a[Is / TM][2], (int)f.a[Is / TM][3], 0, 0, 0, 0},
+          f.b[Is % TM], acc[Is / TM][Is % TM], 4, 0, (Is / TM) % 4, (int)sa[(Is / TM) / 4], (Is % TM) % 4,
+          (int)sb[(Is % TM) / 4])), ...);
+}
+
+template <int TN, int TM>
+__device__ __forceinline__ void big_compute(const BigFrags<TN, TM>& f, f32x4_t (&acc)[TN][TM], int j)
+{
+    const uint32_t sel = (uint32_t)j | ((uint32_t)(j + 4) << 8);
+    uint32_t sa[TN / 4], sb[TM / 4];
+#pragma unroll
+    for (int g = 0; g < TN / 4; ++g) {
+        const uint32_t lo = __builtin_amdgcn_perm(f.sa[4 * g + 1], f.sa[4 * g], sel);
+        const uint32_t hi = __builtin_amdgcn_perm(f.sa[4 * g + 3], f.sa[4 * g + 2], sel);
+        sa[g] = (lo & 0xFFFFu) | (hi << 16);
+    }
+#pragma unroll
+    for (int g = 0; g < TM / 4; ++g) {
+        const uint32_t lo = __builtin_amdgcn_perm(f.sb[4 * g + 1], f.sb[4 * g], sel);
+        const uint32_t hi = __builtin_amdgcn_perm(f.sb[4 * g + 3], f.sb[4 * g + 2], sel);
+        sb[g] = (lo & 0xFFFFu) | (hi << 16);
+    }
+    big_mfmas<TN, TM>(f, sa, sb, acc, std::make_integer_sequence<int, TN * TM>{});
+}
+
+template <int WN, int WM, int TN, int TM, int S>
+__global__ void __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_big_kernel(Params P)
+{
+    using G = BigGeom<WN, WM, TN, TM, S>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int nb, mb;
+    if (!tile_of(P, blockIdx.x, nb, mb)) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, j = lane >> 4;
+    const int wn = wave % WN, wm = wave / WN;
+    const int N0 = nb * G::BN, M0 = mb * G::BM;
+    const int kh = P.K >> 1, ks = P.K >> 5;
+    const int nsteps = P.K / kBK;
+
+    const uint8_t* const wtile = P.W + (int64_t)N0 * kh;
+    const uint8_t* const xtile = P.Xq + (int64_t)M0 * P.K;
+    const uint8_t* const swtile = P.St + (int64_t)N0 * ks;
+    const uint8_t* const sxtile = P.Sx + (int64_t)M0 * ks;
+    uint32_t loff[G::DPW];
+    int ldsoff[G::DPW];
+    bool from_w[G::DPW];
+#pragma unroll
+    for (int c = 0; c < G::DPW; ++c) {
+        const int d = c * G::NW + wave;
+        from_w[c] = false;
+        if (c < G::NW_W / G::NW) {
+            int n = 16 * d + (lane >> 2);
+            n = N0 + n < P.N ? n : P.N - 1 - N0;
+            loff[c] = (uint32_t)n * (uint32_t)kh + 16u * (uint32_t)(lane & 3);
+            ldsoff[c] = 1024 * d;
+        } else if (c < (G::NW_W + G::NW_X) / G::NW) {
+            const int e = d - G::NW_W;
+            const int half = e / (G::BM / 16), rb = e % (G::BM / 16);
+            int m = 16 * rb + (lane >> 2);
+            m = M0 + m < P.M ? m : P.M - 1 - M0;
+            loff[c] = (uint32_t)m * (uint32_t)P.K + 64u * half + 16u * (uint32_t)(lane & 3);
+            ldsoff[c] = G::W_BYTES + 1024 * e;
+        } else {
+            int e = d - G::NW_W - G::NW_X;
+            if (e >= G::NW_SW + G::NW_SX) e = G::NW_SW + G::NW_SX - 1;      // padding copy: repeat
+            if (e < G::NW_SW) {
+                int n = 64 * e + lane;
+                n = N0 + n < P.N ? n : P.N - 1 - N0;
+                loff[c] = (uint32_t)n * (uint32_t)ks;
+                ldsoff[c] = G::W_BYTES + G::X_BYTES + 256 * e;
+                from_w[c] = true;
+            } else {
+                const int e2 = e - G::NW_SW;
+                int m = 64 * e2 + lane;
+                m = M0 + m < P.M ? m : P.M - 1 - M0;
+                loff[c] = (uint32_t)m * (uint32_t)ks;
+                ldsoff[c] = G::W_BYTES + G::X_BYTES + G::SW_BYTES + 256 * e2;
+            }
+        }
+    }
+    auto issue = [&](int step) {
+        unsigned char* stage = smem + (step % S) * G::STAGE;
+        const uint8_t* wb = wtile + (int64_t)step * 64;
+        const uint8_t* xb = xtile + (int64_t)step * 128;
+#pragma unroll
+        for (int c = 0; c < G::DPW; ++c) {
+            if (c < G::NW_W / G::NW) {
+                dma16_to_lds(wb + loff[c], stage + ldsoff[c]);
+            } else if (c < (G::NW_W + G::NW_X) / G::NW) {
+                dma16_to_lds(xb + loff[c], stage + ldsoff[c]);
+            } else {
+                const uint8_t* sbase = (from_w[c] ? swtile : sxtile) + (int64_t)step * 4;
+                dma4_to_lds(sbase + loff[c], stage + ldsoff[c]);
+            }
+        }
+    };
+    const int abase = (wn * 16 * TN + r) * 64 + 16 * j;
+    const int bbase = G::W_BYTES + (wm * 16 * TM + r) * 64 + 16 * j;
+    const int sabase = G::W_BYTES + G::X_BYTES + (wn * 16 * TN + r) * 4;
+    const int sbbase = G::W_BYTES + G::X_BYTES + G::SW_BYTES + (wm * 16 * TM + r) * 4;
+    auto read = [&](BigFrags<TN, TM>& f, int step) {
+        const unsigned char* stage = smem + (step % S) * G::STAGE;
+#pragma unroll
+        for (int i = 0; i < TN; ++i) {
+            f.a[i] = *reinterpret_cast<const u32x4_t*>(stage + abase + 1024 * i);
+            f.sa[i] = *reinterpret_cast<const uint32_t*>(stage + sabase + 64 * i);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            f.b[i] = concat8(*reinterpret_cast<const u32x4_t*>(stage + bbase + 1024 * i),
+                             *reinterpret_cast<const u32x4_t*>(stage + bbase + 1024 * i + G::BM * 64));
+            f.sb[i] = *reinterpret_cast<const uint32_t*>(stage + sbbase + 64 * i);
+        }
+    };
+
+    f32x4_t acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+
+    // ring protocol as in gemm_lds_body (wait for step q, barrier, refill the retired buffer, read)
+    auto sync_read = [&](BigFrags<TN, TM>& f, int q) {
+        const int left = nsteps - 1 - q;
+        const int ahead = left < S - 2 ? left : S - 2;
+        if (ahead >= 2) wait_vmcnt<2 * G::DPW>();
+        else if (ahead == 1) wait_vmcnt<G::DPW>();
+        else wait_vmcnt<0>();
+        lds_barrier_all();
+        if (q + S - 1 < nsteps) issue(q + S - 1);
+        read(f, q);
+    };
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+        if (s < nsteps) issue(s);
+    BigFrags<TN, TM> f;
+    for (int s = 0; s < nsteps; ++s) {
+        sync_read(f, s);
+        big_compute<TN, TM>(f, acc, j);
+    }
+
+    const int n0 = N0 + wn * 16 * TN, m0 = M0 + wm * 16 * TM;
+#pragma unroll
+    for (int im = 0; im < TM; ++im) {
+        const int m = m0 + 16 * im + r;
+        if (m >= P.M) continue;
+        __bf16* orow = P.Out + (int64_t)m * P.N;
+#pragma unroll
+        for (int in = 0; in < TN; ++in) {
+            const int n = n0 + 16 * in + 4 * j;
+            if (n >= P.N) continue;
+            const f32x4_t v = acc[in][im];
+            *reinterpret_cast<u32x2_t*>(orow + n) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        }
+    }
+}
+
 // ---- activation quantiser: bf16 [M, K] -> e4m3fn [M, K] + e8m0 [M, K/32] ---------------------
 // One thread per 32-element block: four 16-byte loads, the block maximum, two 16-byte stores.
 __global__ void __launch_bounds__(256)
@@ -514,8 +723,9 @@ extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const vo
     P.N = N;
     P.K = K;
     P.M = M;
-    const int variant = g_gemm_variant;
-    const int BN = variant == 1 ? kBN : 128, BM = variant == 1 ? kBM : 128;
+    const int variant = pick_variant(N, K, M);
+    const int BN = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::BN : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::BN : 128;
+    const int BM = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::BM : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::BM : 128;
     P.nblk = (N + BN - 1) / BN;
     P.mblk = (M + BM - 1) / BM;
     if ((int64_t)P.nblk * P.mblk > 0x7FFFFFFF - kXcds) return FP8KV_ERR_SHAPE;
@@ -543,7 +753,15 @@ extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const vo
         case 4:
             launch_kernel(gemm_lds2_kernel<2, 2, 3>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 3>::LDS, st, P);
             break;
-        default:
+        case 6:
+            launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2>, dim3((unsigned)grid), dim3(256),
+                          BigGeom<2, 2, 8, 4, 2>::LDS, st, P);
+            break;
+        case 7:
+            launch_kernel(gemm_big_kernel<2, 2, 4, 8, 2>, dim3((unsigned)grid), dim3(256),
+                          BigGeom<2, 2, 4, 8, 2>::LDS, st, P);
+            break;
+        default:                                          // 5
             launch_kernel(gemm_lds2_kernel<2, 2, 2>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 2>::LDS, st, P);
             break;
         case 0:
@@ -555,6 +773,6 @@ extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const vo
 
 extern "C" void fp8kv_gemm_tune(int variant, int order)
 {
-    fp8kv::w4a8_detail::g_gemm_variant = (variant >= 0 && variant <= 5) ? variant : fp8kv::w4a8_detail::kDefaultVariant;
+    fp8kv::w4a8_detail::g_gemm_variant = (variant >= 0 && variant <= 7) ? variant : -1;
     fp8kv::w4a8_detail::g_gemm_order = order == 1 ? 1 : 0;
 }
