@@ -27,7 +27,7 @@ void fp8kv_decode_tune(int variant, int target_wgs);
  * LDS ring depth) shape to use for every GQA, or -1 for the per-GQA default. */
 void fp8kv_prefill_tune(int shape);
 
-/* Tuning hook for the MXFP4 x MXFP8 GEMM: kernel variant (0..7; any other value selects the
+/* Tuning hook for the MXFP4 x MXFP8 GEMM: kernel variant (0..8; any other value selects the
  * default, which picks variant 6 or 5 from the shape) and tile order
  * (0 = XCDs split the token blocks, the default; 1 = XCDs split the weight blocks only).
  * Affects later launches. */

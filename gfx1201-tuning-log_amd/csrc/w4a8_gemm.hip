@@ -42,9 +42,10 @@ constexpr int kXcds = 8;
 // 0: the LDS kernel, fragments double-buffered, 4-step ring, one workgroup per CU; 1: the
 // direct-to-register kernel; 2 / 3: as 0 with a 3 / 5-step ring; 4: single-buffered fragments,
 // registers capped for two waves per SIMD, 3-step ring; 5: as 4 with a 2-step ring (51 KB of
-// LDS, so up to three workgroups share a CU); 6 / 7: as 5 with 8 x 4 / 4 x 8 MFMA tiles per wave.
-// Measured on the configs[4] linears at M = 2048: 6 ~1.22-1.69 PFLOP/s, 5 ~1.27-1.41, 7 ~1.05-1.27,
-// 4 ~1.33, 0 ~1.01, 1 ~0.40.
+// LDS, so up to three workgroups share a CU); 6 / 7: as 5 with 8 x 4 / 4 x 8 MFMA tiles per wave;
+// 8: 8 waves of 8 x 4 tiles (256 x 256 per workgroup, 3-step ring, 150 KB of LDS).  Measured on
+// the configs[4] linears at M = 2048: 6 ~1.22-1.69 PFLOP/s, 5 ~1.27-1.41, 8 ~0.88-1.67 (only
+// gate/up fills the GPU), 7 ~1.05-1.27, 4 ~1.33, 0 ~1.01, 1 ~0.40.
 // Default (-1): variant 6 (the 8 x 4 wave tile, 256 x 128 per workgroup) when its grid has at
 // least 256 tiles or K >= 8192, else variant 5 (measured at the configs[4] linears, M = 2048:
 // gate/up 1.41 -> 1.66 PFLOP/s and down 1.41 -> 1.47 with variant 6, o 1.27 -> 1.22).
@@ -724,8 +725,10 @@ extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const vo
     P.K = K;
     P.M = M;
     const int variant = pick_variant(N, K, M);
-    const int BN = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::BN : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::BN : 128;
-    const int BM = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::BM : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::BM : 128;
+    const int BN = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::BN : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::BN
+                 : variant == 8 ? BigGeom<2, 4, 8, 4, 3>::BN : 128;
+    const int BM = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::BM : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::BM
+                 : variant == 8 ? BigGeom<2, 4, 8, 4, 3>::BM : 128;
     P.nblk = (N + BN - 1) / BN;
     P.mblk = (M + BM - 1) / BM;
     if ((int64_t)P.nblk * P.mblk > 0x7FFFFFFF - kXcds) return FP8KV_ERR_SHAPE;
@@ -761,6 +764,10 @@ extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const vo
             launch_kernel(gemm_big_kernel<2, 2, 4, 8, 2>, dim3((unsigned)grid), dim3(256),
                           BigGeom<2, 2, 4, 8, 2>::LDS, st, P);
             break;
+        case 8:
+            launch_kernel(gemm_big_kernel<2, 4, 8, 4, 3>, dim3((unsigned)grid), dim3(512),
+                          BigGeom<2, 4, 8, 4, 3>::LDS, st, P);
+            break;
         default:                                          // 5
             launch_kernel(gemm_lds2_kernel<2, 2, 2>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 2>::LDS, st, P);
             break;
@@ -773,6 +780,6 @@ extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const vo
 
 extern "C" void fp8kv_gemm_tune(int variant, int order)
 {
-    fp8kv::w4a8_detail::g_gemm_variant = (variant >= 0 && variant <= 7) ? variant : -1;
+    fp8kv::w4a8_detail::g_gemm_variant = (variant >= 0 && variant <= 8) ? variant : -1;
     fp8kv::w4a8_detail::g_gemm_order = order == 1 ? 1 : 0;
 }

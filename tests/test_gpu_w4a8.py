@@ -55,7 +55,7 @@ def _gemm_case(N, K, M, seed):
     return c, rc, rs
 
 
-@pytest.mark.parametrize("variant,order", [(-1, 0), (0, 0), (0, 1), (1, 0), (2, 0), (3, 1), (4, 0), (5, 1), (6, 0), (6, 1), (7, 0)])
+@pytest.mark.parametrize("variant,order", [(-1, 0), (0, 0), (0, 1), (1, 0), (2, 0), (3, 1), (4, 0), (5, 1), (6, 0), (6, 1), (7, 0), (8, 0)])
 @pytest.mark.parametrize("N,K,M", [(256, 512, 16), (200, 1024, 37), (4096, 3584, 300), (512, 18944, 64),
                                    (128, 128, 1), (1024, 3072, 129), (384, 256, 200), (128, 384, 64)])
 def test_gemm_parity(N, K, M, variant, order):
