@@ -15,6 +15,13 @@ during graph capture: :32-43) and calls
 81-83), returning a fresh bf16 [M, N] tensor (bias is applied outside, :9-10).  Anything else,
 or any exception, runs the stolen body (:91-94).
 
+With FP8KV_HIPW4_GEMM=1 as well, larger batches (M > FP8KV_HIPW4_MAX_M, the prefill-sized
+linears the reference leaves to its fork's W4A8 GEMM) take the library's own GEMM path when its
+gate holds (contiguous 2-D bf16 x, K % 128 == 0, N % 4 == 0, K / 32 scale rows, 16-byte aligned
+weight): x is quantised to MXFP8 (h4a8_quant_act) and multiplied on the block-scaled MFMA
+(h4a8_gemm).  This path is opt-in: its activations are MXFP8 (per-32 block scales), not the
+fork's per-token fp8, so its results differ from the fork's within fp8 rounding.
+
 The library path is FP8KV_AMD_LIB if set, else the in-tree build (the reference hard-codes
 /opt/fp8kv/libh4mv.so).
 """
@@ -31,7 +38,7 @@ if _PKG not in sys.path:
     sys.path.insert(0, _PKG)
 
 TAG = "[hipw4]"
-STATS = {"fast": 0, "slow": 0, "logged": False, "calls": 0}
+STATS = {"fast": 0, "gemm": 0, "slow": 0, "logged": False, "calls": 0}
 _STATE = {"installed": False, "body": None, "patched": None}
 
 
@@ -49,6 +56,36 @@ def load_launcher(path: str | None = None):
     lib.h4mv_launch.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
     lib.h4mv_launch.restype = None
     return lib.h4mv_launch
+
+
+def load_gemm(path: str | None = None):
+    """Callable gemm(x, weight, st, out, stream) running h4a8_quant_act then h4a8_gemm through
+    ctypes (status checked; quantised activations in fresh torch buffers)."""
+    import torch
+    if path is None:
+        from fp8kv_amd import _lib
+        path = _lib.lib_path()
+    lib = ctypes.CDLL(path)
+    vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.h4a8_quant_act.argtypes = [vp, i64, vp, vp, ci, ci, vp]
+    lib.h4a8_quant_act.restype = ci
+    lib.h4a8_gemm.argtypes = [vp] * 5 + [ci] * 3 + [vp]
+    lib.h4a8_gemm.restype = ci
+
+    def gemm(x, weight, st, out, stream):
+        M, K = x.shape
+        N = weight.shape[0]
+        xq = torch.empty((M, K), dtype=torch.uint8, device=x.device)
+        sx = torch.empty((M, K // 32), dtype=torch.uint8, device=x.device)
+        rc = lib.h4a8_quant_act(x.data_ptr(), K, xq.data_ptr(), sx.data_ptr(), M, K, stream)
+        if rc != 0:
+            raise RuntimeError(f"h4a8_quant_act status {rc}")
+        rc = lib.h4a8_gemm(weight.data_ptr(), st.data_ptr(), xq.data_ptr(), sx.data_ptr(), out.data_ptr(),
+                           N, K, M, stream)
+        if rc != 0:
+            raise RuntimeError(f"h4a8_gemm status {rc}")
+
+    return gemm
 
 
 def _device_repack(s):
@@ -93,8 +130,20 @@ def fast_path_ok(x, weight, weight_scale, maxm: int, torch) -> bool:
             and weight.data_ptr() % 16 == 0)
 
 
-def make_patched(body, launch, repack, maxm: int, torch, stream_ptr):
-    """The replacement op body: fast path through ``launch`` (h4mv_launch), else ``body``."""
+def gemm_path_ok(x, weight, weight_scale, maxm: int, torch) -> bool:
+    """Gate of the opt-in GEMM path for batches above the matvec's M limit."""
+    if not (torch.is_tensor(x) and x.dim() == 2 and x.is_contiguous() and x.shape[0] > maxm
+            and x.dtype == torch.bfloat16):
+        return False
+    N = weight.shape[0]
+    K = weight.shape[1] * 2
+    return (K % 128 == 0 and N % 4 == 0 and N >= 8 and weight_scale.shape[0] == K // 32
+            and weight.is_contiguous() and weight.data_ptr() % 16 == 0)
+
+
+def make_patched(body, launch, repack, maxm: int, torch, stream_ptr, gemm=None):
+    """The replacement op body: fast path through ``launch`` (h4mv_launch), the opt-in GEMM path
+    through ``gemm`` for larger batches, else ``body``."""
 
     def _patched(x, weight, weight_scale, wref):
         try:
@@ -115,6 +164,14 @@ def make_patched(body, launch, repack, maxm: int, torch, stream_ptr):
                         _log(f"ENGAGED N={N} K={K} M={M} (x={tuple(x.shape)} w={tuple(weight.shape)} "
                              f"s={tuple(weight_scale.shape)})")
                     return out
+            elif gemm is not None and gemm_path_ok(x, weight, weight_scale, maxm, torch):
+                st = repack(weight_scale)
+                if st is not None:
+                    M, N = x.shape[0], weight.shape[0]
+                    out = torch.empty((M, N), device=x.device, dtype=torch.bfloat16)
+                    gemm(x, weight, st, out, ctypes.c_void_p(stream_ptr()))
+                    STATS["gemm"] += 1
+                    return out
         except Exception as e:
             _log(f"fast path failed ({e!r}), falling back")
         STATS["slow"] += 1
@@ -133,7 +190,7 @@ def register(patched, torch):
     torch.library.impl("radiance::mxfp4_linear", "CUDA")(patched)
 
 
-def _poll(launch, maxm, tries: int = 1500, delay: float = 0.2):
+def _poll(launch, maxm, tries: int = 1500, delay: float = 0.2, gemm=None):
     import torch
     body = None
     for _ in range(tries):
@@ -151,7 +208,7 @@ def _poll(launch, maxm, tries: int = 1500, delay: float = 0.2):
         return
     repack = ScaleRepack(torch.cuda.is_current_stream_capturing)
     patched = make_patched(body, launch, repack, maxm, torch,
-                           lambda: torch.cuda.current_stream().cuda_stream)
+                           lambda: torch.cuda.current_stream().cuda_stream, gemm=gemm)
     register(patched, torch)
     _STATE.update(body=body, patched=patched)
     _log("op impl overridden")
@@ -166,7 +223,13 @@ def _install() -> bool:
         _log(f"lib load fail: {e}")
         return False
     maxm = int(os.environ.get("FP8KV_HIPW4_MAX_M", "4"))
-    threading.Thread(target=_poll, args=(launch, maxm), daemon=True).start()
+    gemm = None
+    if os.environ.get("FP8KV_HIPW4_GEMM", "0") == "1":
+        try:
+            gemm = load_gemm()
+        except Exception as e:
+            _log(f"gemm path unavailable: {e}")
+    threading.Thread(target=_poll, args=(launch, maxm), kwargs={"gemm": gemm}, daemon=True).start()
     _STATE["installed"] = True
     _log("installed")
     return True

@@ -88,3 +88,19 @@ def test_nan_scale_block_gives_nan_rows():
     got = ops.mxfp4_linear(x.to(DEV), c["W"].to(DEV), c["St"].to(DEV)).float().cpu()
     assert torch.isnan(got[3]).all()
     assert torch.isfinite(torch.cat([got[:3], got[4:]])).all()
+
+
+def test_linear_hook_gemm_path_matches_ops():
+    """The opt-in large-batch path of the MXFP4 linear hook (ctypes into h4a8_quant_act and
+    h4a8_gemm, scales repacked on the device) gives the same bits as ops.mxfp4_linear."""
+    import fp8kv_hipw4 as h
+    N, K, M = 512, 1024, 40
+    c = workloads.w4_case(N, K, M, seed=23)
+    x, w, s_kn = c["X"].to(DEV), c["W"].to(DEV), c["S_kn"].to(DEV)
+    repack = h.ScaleRepack(lambda: False)
+    patched = h.make_patched(lambda *a: None, h.load_launcher(), repack, 8, torch,
+                             lambda: torch.cuda.current_stream().cuda_stream, gemm=h.load_gemm())
+    got = patched(x, w, s_kn, None)
+    want = ops.mxfp4_linear(x, w, c["St"].to(DEV))
+    torch.cuda.synchronize()
+    assert got is not None and torch.equal(got, want)

@@ -500,3 +500,43 @@ def test_sitecustomize_chain_without_vllm(monkeypatch):
     assert not sys.modules["fp8kv_override"]._STATE["installed"]
     assert not sys.modules["fp8kv_prefill"]._STATE["installed"]
     assert not sys.modules["fp8kv_hipw4"]._STATE["installed"]
+
+
+def test_hipw4_gemm_path_for_large_batches(monkeypatch):
+    """With the opt-in GEMM callable, M above the matvec limit goes to it (scales repacked once);
+    without it the stolen body runs as in the reference."""
+    h = _hipw4(monkeypatch)
+    launch = FakeLaunch()
+    repack = h.ScaleRepack(lambda: False, transpose=lambda t: t.t().contiguous())
+    calls = []
+
+    def gemm(x, w, st, out, stream):
+        calls.append((x.data_ptr(), w.data_ptr(), st.data_ptr(), out.data_ptr(), tuple(out.shape), stream.value))
+
+    patched = h.make_patched(lambda *a: "body", launch, repack, 4, torch, lambda: 77, gemm=gemm)
+    x, w, s = _lin(M=40, N=64, K=256)
+    out = patched(x, w, s, None)
+    assert out.shape == (40, 64) and launch.calls == [] and len(calls) == 1
+    xp, wp, sp, op, shape, stream = calls[0]
+    assert (xp, wp, op, shape, stream) == (x.data_ptr(), w.data_ptr(), out.data_ptr(), (40, 64), 77)
+    assert sp == repack.cache[(s.data_ptr(), tuple(s.shape))].data_ptr()
+    x2, _, _ = _lin(M=2, N=64, K=256)
+    patched(x2, w, s, None)
+    assert len(launch.calls) == 1 and len(calls) == 1            # small M still takes the matvec
+    plain = h.make_patched(lambda *a: "body", launch, repack, 4, torch, lambda: 0)
+    assert plain(x, w, s, None) == "body"
+
+
+@pytest.mark.parametrize("case", ["k_not_128", "n_odd", "small_m", "fp32"])
+def test_hipw4_gemm_gate_rejections(monkeypatch, case):
+    h = _hipw4(monkeypatch)
+    x, w, s = _lin(M=40, N=64, K=256)
+    if case == "k_not_128":
+        x, w, s = torch.zeros(40, 96, dtype=torch.bfloat16), torch.zeros(64, 48, dtype=torch.uint8), s[:3]
+    elif case == "n_odd":
+        w = torch.zeros(66, 128, dtype=torch.uint8)
+    elif case == "small_m":
+        x = x[:4]
+    elif case == "fp32":
+        x = x.float()
+    assert not h.gemm_path_ok(x, w, s, 4, torch)
