@@ -6,8 +6,9 @@
 extern "C" {
 #endif
 
-/* Enumerate every global and LDS address the MXFP4 matvec's streaming kernel would touch for
- * (N, K, M) and check it against the operand sizes and the LDS allocation.
+/* Enumerate every global and LDS address the MXFP4 matvec's LDS kernel (K-slice or streaming,
+ * whichever the planner picks) would touch for (N, K, M) and check it against the operand sizes
+ * and the LDS allocation.
  * 0 = all in bounds, 1 = the shape uses the register-path kernel instead, >= 2 = violation id. */
 int fp8kv_h4mv_audit(int N, int K, int M);
 
@@ -16,6 +17,14 @@ int fp8kv_h4mv_audit(int N, int K, int M);
  * (1: copies through LDS, 2: direct loads); 0 = the built-in defaults.  Affects later launches
  * and audits. */
 void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode);
+
+/* Tuning hook for the matvec's K-slice kernel: mode 0 = used from M = 3 on when every CU gets at
+ * least two 16-row tiles (the default), 1 = whenever the shape allows it (N % 16 == 0, K % 512 == 0,
+ * K <= 4096, M <= 8), 2 = never; depth = LDS ring slots per wave (3; any other value: 2, the default);
+ * order = tile order (1: each workgroup a contiguous range, 2: interleaved; 0: default);
+ * workgroups = workgroup count the planner aims for (0: default).  Affects later launches and
+ * audits. */
+void fp8kv_h4mv_kslice_tune(int mode, int depth, int order, int workgroups);
 
 /* Tuning hook for sweeps of the decode attention launch: kernel variant index (0..6; any other
  * value, e.g. -1, selects the default, variant 4: 8 waves, chunks of 2 groups of 16 keys, 2 chunks

@@ -27,6 +27,7 @@
 #include "fp8kv_status.h"
 #include "fp8kv_diag.h"
 #include <algorithm>
+#include <vector>
 
 namespace fp8kv {
 
@@ -279,10 +280,53 @@ __device__ __forceinline__ void issue_step(unsigned char* slot, const uint8_t* w
 // so those variants are launched with at most kMaxWavesRT waves.
 constexpr int kMaxWavesRT = 4;
 
-// EPI selects the output stage: 0 writes Out[M, N]; 1 and 2 apply SiLU-and-mul to gate/up rows
-// interleaved 8 + 8 per 16-row tile (h4mv_interleave_gate_up) and write Out[M, N / 2]: gate and
-// up are first rounded to bf16 (the values a plain matvec would store), then
-// Out = bf16(silu(g) * u) (EPI 1) or bf16(bf16(silu(g)) * u) (EPI 2).
+// Output stage of one 16-row tile (index `tile`) whose partial products are complete: lane
+// (m, q) holds rows 16 tile + 4 q + i of column m in acc[i].  EPI 0 writes Out[M, N]; EPI 1 and 2
+// apply SiLU-and-mul to the gate/up rows interleaved 8 + 8 per tile (h4mv_interleave_gate_up) and
+// write Out[M, N / 2]: gate and up are first rounded to bf16 (the values a plain matvec would
+// store), then Out = bf16(silu(g) * u) (EPI 1) or bf16(bf16(silu(g)) * u) (EPI 2).  Every lane
+// of the wave must call it (EPI 1/2 pair lanes l and l ^ 32).
+template <typename OutT, int EPI>
+__device__ __forceinline__ void store_tile(const f32x4_t& acc, OutT* __restrict__ Out, int tile,
+                                           int N, int M, int r, int q)
+{
+    if constexpr (EPI != 0) {
+        // lane (m, q < 2) holds gate rows 4q .. 4q + 3 of the tile's 8 features, lane (m, q + 2)
+        // = lane + 32 the up rows of the same features
+        f32x4_t up;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(acc[i], 32);
+        if (r >= M || q >= 2 || 16 * tile >= N) return;
+        __bf16* orow = reinterpret_cast<__bf16*>(Out) + (size_t)r * (size_t)(N >> 1);
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sg = silu_f32(round_to_bf16(acc[i]));
+            if constexpr (EPI == 2) sg = round_to_bf16(sg);
+            o[i] = sg * round_to_bf16(up[i]);
+        }
+        *reinterpret_cast<u32x2_t*>(orow + 8 * tile + 4 * q) =
+            (u32x2_t){pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+    } else {
+        const int n = 16 * tile + 4 * q;
+        if (r >= M || n >= N) return;
+        OutT* orow = Out + (size_t)r * (size_t)N;
+        if (((N & 3) == 0) && aligned(Out, 4 * sizeof(OutT)) && n + 3 < N) {
+            if constexpr (sizeof(OutT) == 2) {
+                *reinterpret_cast<u32x2_t*>(orow + n) =
+                    (u32x2_t){pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+            } else {
+                *reinterpret_cast<f32x4_t*>(orow + n) = acc;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (n + i < N) orow[n + i] = (OutT)acc[i];
+        }
+    }
+}
+
+// EPI selects the output stage (store_tile).
 template <int MMAX, bool XG, int DEPTH, int RT, typename OutT, int EPI = 0>
 __global__ void __launch_bounds__(RT == 1 ? 1024 : 64 * kMaxWavesRT)
 h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
@@ -421,53 +465,185 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
                 acc[t] += reinterpret_cast<const f32x4_t*>(smem + w * L.total)[t * 64 + lane];
     }
 
-    if constexpr (EPI != 0) {
-        // lane (m, q < 2) holds gate rows 4q .. 4q + 3 of each tile's 8 features, lane (m, q + 2)
-        // = lane + 32 the up rows of the same features
-        f32x4_t up[RT];
 #pragma unroll
-        for (int t = 0; t < RT; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) up[t][i] = __shfl_xor(acc[t][i], 32);
-        if (r >= M || q >= 2) return;
-        const int half = N >> 1;
-        __bf16* orow = reinterpret_cast<__bf16*>(Out) + (size_t)r * (size_t)half;
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            const int tile = (n0 >> 4) + t;
-            if (16 * tile >= N) continue;
-            float o[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float sg = silu_f32(round_to_bf16(acc[t][i]));
-                if constexpr (EPI == 2) sg = round_to_bf16(sg);
-                o[i] = sg * round_to_bf16(up[t][i]);
-            }
-            *reinterpret_cast<u32x2_t*>(orow + 8 * tile + 4 * q) =
-                (u32x2_t){pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-        }
-        return;
+    for (int t = 0; t < RT; ++t) store_tile<OutT, EPI>(acc[t], Out, (n0 >> 4) + t, N, M, r, q);
+}
+
+// ---------------------------------------------------------------------------------------------
+// K-slice kernel: many 16-row tiles per workgroup, activations held in registers.
+//
+// At M >= 2 the streaming kernel moves M KB of activations into LDS with every 4 KB of codes (per
+// 16-row tile and K step), so its L2 -> LDS traffic is up to three times the HBM stream.  When
+// there are several tiles per CU (N / 16 >= 2 x kKsWorkgroups) and K / 512 <= kKsMaxWaves, the
+// roles are swapped:
+//   * a workgroup owns nt <= TMAX tiles (every G-th tile, G = workgroups: at any moment the
+//     workgroups read neighbouring tiles) and has one wave per K step (512 k);
+//   * wave w loads the activation fragments of step w into registers once (lane (m, q): the same
+//     fragments the streaming kernel reads from LDS), then streams the codes of step w of tile
+//     after tile through its own DEPTH-slot LDS ring, each slot one tile: 4 KB of codes (the
+//     streaming kernel's four copy instructions and bank-conflict-free placement) and the tile's
+//     16 rows x 16 scale bytes of the step (one 4-byte-per-lane copy, row r at 16 r);
+//   * each tile accumulates in its own register tile (the tile loop is unrolled to TMAX) and is
+//     stored to an LDS area after the rings one tile later, while the stream goes on; the waves
+//     meet once, at the end, and wave w adds the partials of tiles w, w + nw, ... in wave order
+//     (a fixed order: the result does not depend on timing) and writes them through store_tile.
+// Activation traffic is then one step of X per wave and launch instead of per tile.  Measured
+// (cfg1 and configs[4] gate/up, M = 1 .. 8): the marginal stream rate is the same at every M and
+// higher than the streaming kernel's, but the fixed cost per launch is about 1 us higher, so the
+// planner takes it from M = 3 on (gate/up M = 8: 20.9 -> 15.7 us, cfg1 M = 8: 14.8 -> 13.6 us;
+// M = 2 and 1 stay faster on the streaming kernel).
+// ---------------------------------------------------------------------------------------------
+constexpr int kKsMaxWaves = 8;                 // K <= 4096; 2 waves per SIMD, 256 VGPRs each
+constexpr int kKsWorkgroups = 256;             // one workgroup per CU of an MI355X
+constexpr int kKsSlotBytes = kStepCodeBytes + 256;
+constexpr int kKsTmax = 16;                    // tiles per workgroup (register tiles)
+constexpr int kKsMinM = 3;                     // default: K-slice kernel from this M on
+
+// Scale copy of a tile-step: lane l fetches bytes 4 (l % 4) .. +3 of row l / 4's 16 scale bytes
+// of the step; offset from the tile's first scale byte of the step.
+__host__ __device__ inline uint32_t ks_s_lane_off(int K, int lane)
+{
+    return (uint32_t)(lane >> 2) * (uint32_t)(K >> 5) + 4u * (uint32_t)(lane & 3);
+}
+// Tiles of workgroup b when T tiles are dealt to G workgroups: tile t0 + i * tstride for
+// i < nt.  Interleaved (tstride = G): at any moment the workgroups read neighbouring tiles, one
+// contiguous stretch of W; contiguous (tstride = 1): each workgroup a stretch of its own.
+__host__ __device__ inline void ks_tiles_of(int b, int T, int G, bool interleaved, int& t0, int& nt,
+                                            int& tstride)
+{
+    const int base = T / G, rem = T % G;
+    nt = base + (b < rem ? 1 : 0);
+    if (interleaved) {
+        t0 = b;
+        tstride = G;
+    } else {
+        t0 = b * base + (b < rem ? b : rem);
+        tstride = 1;
     }
-    const int m = r;
-    if (m >= M) return;
-    OutT* orow = Out + (size_t)m * (size_t)N;
-    const bool vec_ok = ((N & 3) == 0) && aligned(Out, 4 * sizeof(OutT));
+}
+
+// s_waitcnt vmcnt(5 ahead) (five copies per tile) for 0 <= ahead <= A.
+template <int A>
+__device__ __forceinline__ void ks_wait(int ahead)
+{
+    if constexpr (A == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (ahead >= A) wait_vmcnt<5 * A>();
+        else ks_wait<A - 1>(ahead);
+    }
+}
+
+template <int DEPTH, int TMAX, typename OutT, int EPI>
+__global__ void __launch_bounds__(64 * kKsMaxWaves)
+h4mv_kslice_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
+                   const __bf16* __restrict__ X, OutT* __restrict__ Out, int N, int K, int M,
+                   int interleaved)
+{
+    static_assert(DEPTH * 5 < 64, "vmcnt holds at most 63");
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;                 // == K / 512
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    int t0, nt, tstride;
+    ks_tiles_of(blockIdx.x, N >> 4, gridDim.x, interleaved != 0, t0, nt, tstride);
+    const int G = K >> 5;
+    const int gs = wave * kStepGroups;                  // first scale group of this wave's step
+
+    unsigned char* ring = smem + (size_t)wave * DEPTH * kKsSlotBytes;
+    uint32_t woff[4];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        const int n = n0 + 16 * t + 4 * q;
-        if (n >= N) continue;
-        if (vec_ok && n + 3 < N) {
-            if constexpr (sizeof(OutT) == 2) {
-                u32x2_t v = {pack_bf16x2(acc[t][0], acc[t][1]), pack_bf16x2(acc[t][2], acc[t][3])};
-                *reinterpret_cast<u32x2_t*>(orow + n) = v;
-            } else {
-                *reinterpret_cast<f32x4_t*>(orow + n) = acc[t];
-            }
+    for (int i = 0; i < 4; ++i) woff[i] = stream_w_lane_off(0, kRowsPerWG, K, lane, i);
+    const uint32_t soff = ks_s_lane_off(K, lane);
+    const uint8_t* wstep = W + (size_t)t0 * kRowsPerWG * (size_t)(K >> 1) + (size_t)gs * 16;
+    const uint8_t* sstep = St + (size_t)t0 * kRowsPerWG * (size_t)G + gs;
+    const size_t wtile = (size_t)tstride * kRowsPerWG * (size_t)(K >> 1);
+    const size_t stile = (size_t)tstride * kRowsPerWG * (size_t)G;
+    auto issue = [&](int i, unsigned char* slot) {
+        const uint8_t* w = wstep + (size_t)i * wtile;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            __builtin_amdgcn_global_load_lds((const void*)(w + woff[c]), (lds_void_t*)(slot + c * 1024),
+                                             16, 0, kDmaAux);
+        __builtin_amdgcn_global_load_lds((const void*)(sstep + (size_t)i * stile + soff),
+                                         (lds_void_t*)(slot + kStepCodeBytes), 4, 0, 0);
+    };
+    // Tile 0's copies go out first, then the activation loads, then the rest of the ring, filled
+    // unconditionally (a workgroup with nt < DEPTH fetches its last tile again into slots it
+    // never reads): exactly 5 (DEPTH - 1) copies are then younger than the activation loads on
+    // every path, so the wait below covers them (and tile 0) without draining the ring, and the
+    // compiler needs no wait of its own before the MFMAs.
+    u32x4_t xv[4][4];
+    auto load_xv = [&]() {
+        if (r < M) {
+            const unsigned char* xrow = reinterpret_cast<const unsigned char*>(X) +
+                                        (size_t)r * (size_t)K * 2 + (size_t)gs * 64;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xv[u][j] = load_16(xrow + stream_x_frag_off(q, u, j));
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (n + i < N) orow[n + i] = (OutT)acc[t][i];
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) asm volatile("" : "=v"(xv[u][j]));
         }
+        asm volatile("" ::: "memory");
+    };
+    issue(0, ring);
+    load_xv();
+#pragma unroll
+    for (int i = 1; i < DEPTH; ++i) issue(min(i, nt - 1), ring + i * kKsSlotBytes);
+    wait_vmcnt<5 * (DEPTH - 1)>();
+
+    int rdoff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rdoff[u] = stream_w_read_off(r, q, u);
+
+    f32x4_t acc[TMAX];
+    // partial tiles [nt][nwaves][64] after the rings
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(smem + (size_t)nwaves * DEPTH * kKsSlotBytes);
+#pragma unroll
+    for (int i = 0; i < TMAX; ++i) {
+        if (i < nt) {
+            unsigned char* sl = ring + (i % DEPTH) * kKsSlotBytes;
+            // tiles i + 1 .. min(nt, i + DEPTH) - 1 may stay in flight
+            ks_wait<DEPTH - 1>(min(nt - 1 - i, DEPTH - 1));
+            const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(sl + kStepCodeBytes + 16 * r);
+            u32x4_t wv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) wv[u] = *reinterpret_cast<const u32x4_t*>(sl + rdoff[u]);
+            __builtin_amdgcn_s_waitcnt(0xC07F);             // lgkmcnt(0): the slot is free again
+            if (i + DEPTH < nt) issue(i + DEPTH, sl);
+            f32x4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float sc = e8m0_to_f32((sv[u] >> (8 * q)) & 0xFFu);   // group q + 4u of row r
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bf16x8_t a = fp4x8_to_bf16x8(wv[u][j], sc);
+                    if (u & 1) c1 = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), c1);
+                    else       c0 = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), c0);
+                }
+            }
+            acc[i] = c0 + c1;
+            // the previous tile's partial is complete by now: publish it while streaming
+            if (i > 0) red[((i - 1) * nwaves + wave) * 64 + lane] = acc[i - 1];
+        }
+    }
+
+    // ---- add the waves' partial tiles and store ------------------------------------------------
+#pragma unroll
+    for (int i = 0; i < TMAX; ++i)
+        if (i == nt - 1) red[(i * nwaves + wave) * 64 + lane] = acc[i];
+    __syncthreads();
+    for (int i = wave; i < nt; i += nwaves) {
+        f32x4_t a = red[(i * nwaves) * 64 + lane];
+        for (int w = 1; w < nwaves; ++w) a += red[(i * nwaves + w) * 64 + lane];
+        store_tile<OutT, EPI>(a, Out, t0 + i * tstride, N, M, r, q);
     }
 }
 
@@ -637,6 +813,57 @@ void launch_stream_m(const StreamPlan& p, const void* W, const void* St, const v
     }
 }
 
+// K-slice planner (tunables: fp8kv_h4mv_kslice_tune).  mode 0: used from M = kKsMinM on when
+// every CU gets at least two tiles; 1: whenever the shape allows it; 2: never.
+int g_kslice_mode = 0;
+int g_kslice_depth = 0;
+int g_kslice_order = 0;         // 0: default, 1: contiguous, 2: interleaved
+int g_kslice_wgs = 0;           // workgroups the planner aims for (0: kKsWorkgroups)
+
+struct KsPlan {
+    int nw, depth, grid, nt_max, interleaved;
+    size_t lds;
+};
+
+inline bool kslice_plan(int N, int K, int M, KsPlan& p)
+{
+    if (g_kslice_mode == 2) return false;
+    if ((K & 511) != 0 || (N & 15) != 0 || M > 8) return false;
+    const int steps = K >> 9;
+    if (steps > kKsMaxWaves) return false;
+    const int T = N >> 4;
+    if (g_kslice_mode == 0 && (T < 2 * kKsWorkgroups || M < kKsMinM)) return false;
+    p.nw = steps;
+    p.depth = g_kslice_depth == 3 ? 3 : 2;
+    p.interleaved = g_kslice_order == 1 ? 0 : 1;
+    // tiles per workgroup: at most kKsTmax, and rings plus partial tiles within the LDS
+    const size_t ring_bytes = (size_t)p.nw * p.depth * kKsSlotBytes;
+    const int cap = std::min(kKsTmax, (int)((kLdsPerCU - ring_bytes) / ((size_t)p.nw * 1024)));
+    if (cap < 1) return false;
+    int G = std::min(T, g_kslice_wgs > 0 ? g_kslice_wgs : kKsWorkgroups);
+    if ((T + G - 1) / G > cap) G = (T + cap - 1) / cap;
+    p.grid = G;
+    p.nt_max = (T + G - 1) / G;
+    const size_t ring = (size_t)p.nw * p.depth * kKsSlotBytes;
+    const size_t red = (size_t)p.nt_max * p.nw * 1024;
+    p.lds = ring + red;
+    return p.lds <= kLdsPerCU;
+}
+
+template <typename OutT, int EPI = 0>
+void launch_kslice(const KsPlan& p, const void* W, const void* St, const void* Xb, void* Out,
+                   int N, int K, int M, hipStream_t s)
+{
+    const dim3 grid((unsigned)p.grid), block(64 * p.nw);
+#define FP8KV_KS(D) \
+    launch_kernel(h4mv_kslice_kernel<D, kKsTmax, OutT, EPI>, grid, block, (uint32_t)p.lds, s, \
+                  static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
+                  static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M, p.interleaved)
+    if (p.depth == 3) FP8KV_KS(3);
+    else FP8KV_KS(2);
+#undef FP8KV_KS
+}
+
 template <typename OutT>
 int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N, int K, int M,
                 void* stream)
@@ -647,8 +874,11 @@ int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N,
     if (!aligned(W, 16) || !aligned(Xb, 16) || !aligned(Out, sizeof(OutT))) return FP8KV_ERR_ALIGN;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
+    KsPlan kp;
     StreamPlan p;
-    if (aligned(St, 4) && stream_plan(N, K, M, p)) {
+    if (aligned(St, 4) && kslice_plan(N, K, M, kp)) {
+        launch_kslice<OutT>(kp, W, St, Xb, Out, N, K, M, s);
+    } else if (aligned(St, 4) && stream_plan(N, K, M, p)) {
         launch_stream_m<OutT>(p, W, St, Xb, Out, N, K, M, s);
     } else {
         const Plan rp = make_plan(K, M, 4);
@@ -669,9 +899,16 @@ extern "C" int h4mv_silu_mul(const void* W, const void* St, const void* Xb, void
     if (N < 16 || K < 32 || M < 1 || (mode != 0 && mode != 1)) return FP8KV_ERR_ARG;
     if (M > 8 || (K & 511) != 0 || (N & 15) != 0) return FP8KV_ERR_SHAPE;
     if (!aligned(W, 16) || !aligned(Xb, 16) || !aligned(Out, 8) || !aligned(St, 4)) return FP8KV_ERR_ALIGN;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    KsPlan kp;
+    if (kslice_plan(N, K, M, kp)) {
+        begin_launch();
+        if (mode == 0) launch_kslice<__bf16, 1>(kp, W, St, Xb, Out, N, K, M, s);
+        else launch_kslice<__bf16, 2>(kp, W, St, Xb, Out, N, K, M, s);
+        return finish_launch();
+    }
     StreamPlan p;
     if (!stream_plan(N, K, M, p)) return FP8KV_ERR_SHAPE;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
     if (mode == 0) launch_stream_m<__bf16, 1>(p, W, St, Xb, Out, N, K, M, s);
     else launch_stream_m<__bf16, 2>(p, W, St, Xb, Out, N, K, M, s);
@@ -754,15 +991,82 @@ int audit_stream(int N, int K, int M, const StreamPlan& p)
     return 0;
 }
 
+// Audit of the K-slice kernel (same return convention as audit_stream): tile coverage, every
+// code / scale / activation byte read, every LDS byte written or read.
+int audit_kslice(int N, int K, int M, const KsPlan& p)
+{
+    const int T = N >> 4, G = p.grid, nw = p.nw, depth = p.depth;
+    if ((N & 15) || (K & 511) || nw != (K >> 9) || nw > kKsMaxWaves || G < 1 || G > T) return 2;
+    if (depth < 2 || depth > 3 || p.lds > kLdsPerCU) return 3;
+    if ((size_t)nw * depth * kKsSlotBytes + (size_t)p.nt_max * nw * 1024 > p.lds) return 3;
+    const size_t wbytes = (size_t)N * (size_t)(K >> 1), sbytes = (size_t)N * (size_t)(K >> 5);
+    const size_t xbytes = (size_t)M * (size_t)K * 2;
+    const size_t slot = kKsSlotBytes;
+    std::vector<unsigned char> seen((size_t)T, 0);
+    for (int b = 0; b < G; ++b) {
+        int t0, nt, tstride;
+        ks_tiles_of(b, T, G, p.interleaved != 0, t0, nt, tstride);
+        if (nt < 1 || nt > kKsTmax || nt > p.nt_max) return 4;
+        for (int i = 0; i < nt; ++i) {                    // every tile exactly once
+            const long t = (long)t0 + (long)i * tstride;
+            if (t < 0 || t >= T || seen[(size_t)t]) return 4;
+            seen[(size_t)t] = 1;
+        }
+        for (int w = 0; w < nw; ++w) {
+            const int gs = w * kStepGroups;
+            const size_t ring = (size_t)w * depth * slot;
+            if (ring + depth * slot > p.lds) return 5;
+            for (int lane = 0; lane < 64; ++lane) {
+                const int r = lane & 15, q = lane >> 4;
+                if (r < M)
+                    for (int u = 0; u < 4; ++u)
+                        for (int j = 0; j < 4; ++j)
+                            if ((size_t)r * K * 2 + (size_t)gs * 64 + stream_x_frag_off(q, u, j) + 16 > xbytes) return 6;
+                for (int i = 0; i < nt; ++i) {
+                    const size_t sl = ring + (size_t)(i % depth) * slot;
+                    const size_t tile = (size_t)t0 + (size_t)i * tstride;
+                    const size_t wt = tile * kRowsPerWG * (K >> 1) + (size_t)gs * 16;
+                    for (int c = 0; c < 4; ++c) {
+                        if (wt + stream_w_lane_off(0, kRowsPerWG, K, lane, c) + 16 > wbytes) return 7;
+                        if (c * 1024 + 16 * lane + 16 > kStepCodeBytes) return 8;
+                    }
+                    const size_t st = tile * kRowsPerWG * (K >> 5) + gs;
+                    if (st + ks_s_lane_off(K, lane) + 4 > sbytes) return 9;
+                    if (kStepCodeBytes + 4 * lane + 4 > (int)slot) return 10;
+                    if (kStepCodeBytes + 16 * r + 16 > (int)slot) return 11;
+                    for (int u = 0; u < 4; ++u)
+                        if (stream_w_read_off(r, q, u) + 16 > kStepCodeBytes) return 12;
+                    if (sl + slot > p.lds) return 13;
+                    const size_t rings = (size_t)nw * depth * slot;
+                    if (rings + (((size_t)i * nw + w) * 64 + lane) * 16 + 16 > p.lds) return 14;
+                }
+            }
+        }
+    }
+    for (int t = 0; t < T; ++t)
+        if (!seen[(size_t)t]) return 4;
+    return 0;
+}
+
 }}  // namespace fp8kv::h4mv_detail
 
 extern "C" int fp8kv_h4mv_audit(int N, int K, int M)
 {
     using namespace fp8kv::h4mv_detail;
     if (N < 1 || K < 32 || M < 1 || M > 16 || (K & 31)) return 2;
+    KsPlan kp;
+    if (kslice_plan(N, K, M, kp)) return audit_kslice(N, K, M, kp);
     StreamPlan p;
     if (!stream_plan(N, K, M, p)) return 1;
     return audit_stream(N, K, M, p);
+}
+
+extern "C" void fp8kv_h4mv_kslice_tune(int mode, int depth, int order, int workgroups)
+{
+    fp8kv::h4mv_detail::g_kslice_mode = (mode == 1 || mode == 2) ? mode : 0;
+    fp8kv::h4mv_detail::g_kslice_depth = depth;
+    fp8kv::h4mv_detail::g_kslice_order = (order == 1 || order == 2) ? order : 0;
+    fp8kv::h4mv_detail::g_kslice_wgs = workgroups > 0 ? workgroups : 0;
 }
 
 extern "C" void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode)

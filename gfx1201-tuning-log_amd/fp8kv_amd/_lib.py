@@ -55,6 +55,7 @@ SIGNATURES: dict[str, tuple] = {
     # host-only diagnostics (csrc/fp8kv_diag.h)
     "fp8kv_h4mv_audit": (_c_i, [_c_i] * 3),
     "fp8kv_h4mv_tune": (None, [_c_i] * 4),
+    "fp8kv_h4mv_kslice_tune": (None, [_c_i] * 4),
     "fp8kv_decode_tune": (None, [_c_i] * 2),
     "fp8kv_prefill_tune": (None, [_c_i]),
     "fp8kv_gemm_tune": (None, [_c_i, _c_i]),

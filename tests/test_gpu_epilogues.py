@@ -99,6 +99,27 @@ def test_fused_silu_epilogue_equals_two_step(mode, N, K, M):
     assert torch.equal(fused, two)
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("depth", [2, 3])
+def test_fused_silu_epilogue_kslice(mode, depth):
+    """The fused epilogue on the K-slice kernel forced through its tuning hook (one and several
+    tiles per workgroup) equals the two-step path on the same kernel."""
+    from fp8kv_amd import _lib
+    lib = _lib.load()
+    try:
+        lib.fp8kv_h4mv_kslice_tune(1, depth, 0, 0)
+        for N, K, M in ((512, 1024, 3), (8224, 2048, 8), (28672, 4096, 5)):
+            c = workloads.w4_case(N, K, M, seed=N + M + depth)
+            W, St, X = c["W"].to(DEV), c["St"].to(DEV), c["X"].to(DEV)
+            wi, si = ops.interleave_gate_up(W, St)
+            fused = ops.h4mv_silu_mul(X, wi, si, mode=mode)
+            two = ops.silu_mul(ops.h4mv(X, W, St), mode=mode)
+            torch.cuda.synchronize()
+            assert torch.equal(fused, two), (N, K, M)
+    finally:
+        lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+
+
 def test_fused_silu_epilogue_vs_oracle():
     N, K, M = 1024, 2048, 4
     c = workloads.w4_case(N, K, M, seed=11)

@@ -250,3 +250,35 @@ def test_row_tile_variants(rt, N, K, x_mode):
             _check(workloads.w4_case(N=N, K=K, M=M, seed=N + K + M + rt))
     finally:
         lib.fp8kv_h4mv_tune(0, 0, 0, 0)
+
+
+@pytest.mark.parametrize("order", [1, 2])
+@pytest.mark.parametrize("depth", [2, 3])
+@pytest.mark.parametrize("N,K", [(16, 512), (4096, 3584), (4112, 1024), (8208, 2048), (28672, 4096),
+                                 (65536, 512), (66048, 512)])
+def test_kslice_variants(depth, N, K, order):
+    """The K-slice kernel forced through its tuning hook at every ring depth and both tile
+    orders: one tile per workgroup (fewer tiles than ring slots), uneven tile counts (T = 257,
+    513), seven tiles (cfg1), the sixteen-tile maximum and more workgroups than CUs (T = 4128),
+    at M = 1, 3, 8 with bf16 and fp32 outputs."""
+    lib = _lib.load()
+    try:
+        lib.fp8kv_h4mv_kslice_tune(1, depth, order, 0)
+        for M in (1, 3, 8):
+            _check(workloads.w4_case(N=N, K=K, M=M, seed=N + K + M + depth))
+    finally:
+        lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+
+
+def test_kslice_and_streaming_kernels_agree():
+    """Both LDS kernels on the same cfg1 inputs (K-slice by default, streaming forced): within
+    the fp32 rounding of their different accumulation orders."""
+    case = workloads.w4_case(N=28672, K=4096, M=8, seed=7)
+    lib = _lib.load()
+    a = _run(case, out_dtype=torch.float32)
+    try:
+        lib.fp8kv_h4mv_kslice_tune(2, 0, 0, 0)
+        b = _run(case, out_dtype=torch.float32)
+    finally:
+        lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+    assert np.abs(a - b).max() <= 1e-5 * np.abs(a).max()

@@ -49,3 +49,24 @@ def test_h4mv_stream_in_bounds_every_row_tile_count(lib, rt, x_mode):
             assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
     finally:
         lib.fp8kv_h4mv_tune(0, 0, 0, 0)
+
+
+@pytest.mark.parametrize("wgs", [0, 512])
+@pytest.mark.parametrize("order", [1, 2])
+@pytest.mark.parametrize("depth", [2, 3])
+def test_h4mv_kslice_in_bounds(lib, depth, order, wgs):
+    """The K-slice kernel forced on every shape it accepts, both tile orders and two workgroup
+    targets: model shapes, tile counts per workgroup from 1 to 16, more workgroups than CUs,
+    random shapes; every tile is covered exactly once."""
+    rng = random.Random(depth)
+    try:
+        lib.fp8kv_h4mv_kslice_tune(1, depth, order, wgs)
+        shapes = [(N, K) for N, K in CFG4_SHAPES if K <= 4096]
+        shapes += [(16, 512), (4112, 1024), (8208, 2048), (65536, 512), (66048, 512)]
+        for _ in range(60):
+            shapes.append((16 * rng.randrange(1, 5000), 512 * rng.randrange(1, 9)))
+        for N, K in shapes:
+            for M in (1, 3, 8):
+                assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
+    finally:
+        lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
