@@ -468,18 +468,81 @@ __device__ __forceinline__ float max_xor16_32_raw(float v)
     return max_raw(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+// D += A . B^T over 128 k on the block-scaled MFMA with e4m3 A and B (both block scales 1.0):
+// lane (r, p) supplies row r's k 16p .. 16p+15 in bytes 0..15 and 64+16p .. +15 in bytes 16..31
+// of each operand; the products are exact and accumulate in fp32.
+__device__ __forceinline__ f32x4_t mfma_fp8_16x16x128(const v8i& a, const v8i& b, f32x4_t c)
+{
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// One query row's 32 bf16 values held by this lane (the 128-value row is spread over the four
+// lanes n, n + 16, n + 32, n + 48) -> e4m3 hi and lo parts with q * 2^e = hi + lo, where 2^e is
+// the row's scale: the largest |q| of the row times 2^e lies in [128, 256).  Returns 2^-e.
+// hi is q * 2^e rounded to 4 significant bits; the remainder lo is a multiple of the bf16 value's
+// last place below 2^-4 of it, exact in e4m3 whenever |q| >= 2^-9 of the row's largest |q| (the
+// subnormal range covers smaller values to 2^-10 of their place).  The products of the two MFMAs
+// with exact e4m3 K then sum to the bf16 path's S up to fp32 accumulation order.  sign_mask
+// (0x80808080 or 0) negates the row in e4m3 (exact).
+__device__ __forceinline__ float q_fp8_split(const u32x4_t (&qf)[4], uint32_t sign_mask, v8i& hi, v8i& lo)
+{
+    float amax = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            amax = fmaxf(amax, fabsf(__uint_as_float(qf[c][d] << 16)));
+            amax = fmaxf(amax, fabsf(__uint_as_float(qf[c][d] & 0xFFFF0000u)));
+        }
+    amax = max_xor16_32(amax);
+    // biased exponent of the scale 2^e = 2^(7 - floor(log2 amax)), kept where 2^-e is normal too
+    int be = 261 - (int)((__float_as_uint(amax) >> 23) & 0xFFu);
+    be = be < 1 ? 1 : (be > 253 ? 253 : be);
+    const float scale = __uint_as_float((uint32_t)be << 23);
+    const float inv = __uint_as_float((uint32_t)(254 - be) << 23);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {               // dword pair (2h, 2h + 1) of chunk c -> 4 values
+            float x[4];
+            x[0] = __uint_as_float(qf[c][2 * h] << 16) * scale;
+            x[1] = __uint_as_float(qf[c][2 * h] & 0xFFFF0000u) * scale;
+            x[2] = __uint_as_float(qf[c][2 * h + 1] << 16) * scale;
+            x[3] = __uint_as_float(qf[c][2 * h + 1] & 0xFFFF0000u) * scale;
+            uint32_t hw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+            hw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], (int)hw, true);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hw, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hw, true);
+            uint32_t lw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0] - h01[0], x[1] - h01[1], 0, false);
+            lw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2] - h23[0], x[3] - h23[1], (int)lw, true);
+            // chunk c holds d 16p + 8 (c & 1) + 4 h .. of the low half (c < 2) or the high half
+            const int slot = 4 * (c >> 1) + 2 * (c & 1) + h;
+            hw ^= sign_mask;
+            lw ^= sign_mask;
+            // opaque to the compiler, which would otherwise re-derive the parts inside the key loop
+            asm volatile("" : "+v"(hw), "+v"(lw));
+            hi[slot] = (int)hw;
+            lo[slot] = (int)lw;
+        }
+    return inv;
+}
+
 // Online softmax of the RS row-sets of one 32-key tile.  sc holds raw scores S^T (lane (q, p):
-// keys 16 kg + 4 p + e of query row q), -inf where masked; qk = |sm_scale * k_scale| * log2(e),
-// at least 1e-30 (a negative scale is folded into Q's sign), so the row max of the raw scores
-// times qk is the max of the scaled ones and each probability is exp2(fma(s, qk, -m)).  m_run
+// keys 16 kg + 4 p + e of query row q), -inf where masked; qkr[j] = this lane's query row's
+// factor from raw score to log2 units (|sm_scale * k_scale| * log2(e) over the row's Q scale,
+// positive: a negative scale is folded into Q's sign), so the row max of the raw scores times
+// it is the max of the scaled ones and each probability is exp2(fma(s, qk, -m)).  m_run
 // starts at kMaxFloor.  Returns the bf16 probabilities P^T as MFMA B fragments in pb.
 template <int RS>
 __device__ __forceinline__ void softmax_tile(const f32x4_t (&sc)[RS][2], float (&m_run)[RS],
-                                             float (&l_run)[RS], f32x4_t (&o)[RS][8], float qk,
-                                             u32x4_t (&pb)[RS])
+                                             float (&l_run)[RS], f32x4_t (&o)[RS][8],
+                                             const float (&qkr)[RS], u32x4_t (&pb)[RS])
 {
 #pragma unroll
     for (int j = 0; j < RS; ++j) {
+        const float qk = qkr[j];
         float m8 = max3_raw(sc[j][0][0], sc[j][0][1], sc[j][0][2]);
         m8 = max3_raw(m8, sc[j][0][3], sc[j][1][0]);
         m8 = max3_raw(m8, sc[j][1][1], sc[j][1][2]);
@@ -565,7 +628,7 @@ prefill_split_kernel(Params P)
     const int32_t* btrow = P.bt + (int64_t)seq * P.bt_stride;
     const float qk_signed = P.sm_scale * P.k_scale[0] * kLog2e;
     const float qk = fmaxf(fabsf(qk_signed), 1e-30f);         // > 0: -inf * qk stays -inf
-    const uint32_t qflip = qk_signed < 0.f ? 0x80008000u : 0u;   // negate Q (exact in bf16)
+    const uint32_t qflip = qk_signed < 0.f ? 0x80808080u : 0u;   // negate Q (exact in e4m3)
     const float vs = P.v_scale[0];
 
     // This wave's copy instruction of every tile: K rows (waves 0-3) or V rows (waves 4-7)
@@ -586,7 +649,11 @@ prefill_split_kernel(Params P)
         const int ntiles = (k_hi + kBN - 1) / kBN;
         const int nwin = (ntiles + NT - 1) / NT;
 
-        u32x4_t qf[RS][4];
+        // Q as the fp8 B operand of S^T = K.Q^T (lane (n, p): d 16p .. 16p+15 and 64+16p .. +15
+        // of query row n), split exactly into e4m3 hi + lo parts (q_fp8_split), with the row's
+        // scale folded into this lane's softmax factor qkr.
+        v8i qhi[RS], qlo[RS];
+        float qkr[RS];
         const int tok = 16 * blk + lr;
         const bool tok_ok = tok < qlen;
 #pragma unroll
@@ -594,21 +661,13 @@ prefill_split_kernel(Params P)
             const u32x4_t zero = {0u, 0u, 0u, 0u};
             const __bf16* qrow = P.q + (int64_t)(q_begin + (tok_ok ? tok : 0)) * P.q_stride +
                                  (int64_t)(kh * P.gqa + grp * RS + j) * kD;
-            qf[j][0] = tok_ok ? load_16(qrow + 16 * lp) : zero;
-            qf[j][1] = tok_ok ? load_16(qrow + 16 * lp + 8) : zero;
-            qf[j][2] = tok_ok ? load_16(qrow + 64 + 16 * lp) : zero;
-            qf[j][3] = tok_ok ? load_16(qrow + 64 + 16 * lp + 8) : zero;
+            u32x4_t qf[4];
+            qf[0] = tok_ok ? load_16(qrow + 16 * lp) : zero;
+            qf[1] = tok_ok ? load_16(qrow + 16 * lp + 8) : zero;
+            qf[2] = tok_ok ? load_16(qrow + 64 + 16 * lp) : zero;
+            qf[3] = tok_ok ? load_16(qrow + 64 + 16 * lp + 8) : zero;
+            qkr[j] = qk * q_fp8_split(qf, qflip, qhi[j], qlo[j]);
         }
-        wait_vmcnt<0>();
-        // The flip is opaque to the compiler, which would otherwise re-derive the flipped
-        // fragments inside the key loop instead of keeping them.
-#pragma unroll
-        for (int j = 0; j < RS; ++j)
-#pragma unroll
-            for (int st = 0; st < 4; ++st)
-#pragma unroll
-                for (int d = 0; d < 4; ++d)
-                    asm volatile("v_xor_b32 %0, %1, %0" : "+v"(qf[j][st][d]) : "s"(qflip));
 
         // Block ids for this wave's copy instruction of each tile of window wi (its 8 rows lie
         // in one 16-key group, hence one cache block; index clamped to the last key): lane u
@@ -672,17 +731,17 @@ prefill_split_kernel(Params P)
                 const int k0 = t * kBN;
                 const unsigned char* buf = ring + (i % RW) * kWinBytes + tw * kTileBytes;
 
-                u32x4_t kf[2][4];
+                // K as the fp8 A operand, straight from the ring: lane (r, p) = key 16 kg + r,
+                // d 16p .. 16p+15 (chunk p) and 64+16p .. +15 (chunk 4 + p).
+                v8i kf[2];
 #pragma unroll
                 for (int kg = 0; kg < 2; ++kg) {
                     const int row = 16 * kg + lr;
                     const unsigned char* kb = buf + (row >> 3) * 1024;
-#pragma unroll
-                    for (int st = 0; st < 4; ++st) {
-                        const u32x2_t raw = *reinterpret_cast<const u32x2_t*>(
-                            kb + 16 * k_slot(row & 7, (st >> 1) * 4 + lp) + 8 * (st & 1));
-                        kf[kg][st] = __builtin_bit_cast(u32x4_t, fp8x8_to_bf16x8(raw[0], raw[1]));
-                    }
+                    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(kb + 16 * k_slot(row & 7, lp));
+                    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(kb + 16 * k_slot(row & 7, 4 + lp));
+                    kf[kg] = (v8i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                                   (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
                 }
                 // V^T raw rows (lane (c, p) transposes d = 8c .. 8c+7) and their widening go ahead
                 // of S^T = K.Q^T, so the VALU work can run between the MFMAs.
@@ -700,17 +759,15 @@ prefill_split_kernel(Params P)
                 for (int j = 0; j < RS; ++j)
 #pragma unroll
                     for (int kg = 0; kg < 2; ++kg) {
-                        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                        for (int st = 0; st < 4; ++st)
-                            acc = mfma16x16x32_bf16(as_bf16x8(kf[kg][st]), as_bf16x8(qf[j][st]), acc);
-                        sc[j][kg] = acc;
+                        const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+                        f32x4_t acc = mfma_fp8_16x16x128(kf[kg], qhi[j], zero);
+                        sc[j][kg] = mfma_fp8_16x16x128(kf[kg], qlo[j], acc);
                     }
-                // Interleave: one MFMA, then up to three VALU (the V widening, 48 instructions).
+                // Interleave: one MFMA, then up to four VALU (the V widening, 48 instructions).
 #pragma unroll
-                for (int g = 0; g < 8 * RS; ++g) {
+                for (int g = 0; g < 4 * RS; ++g) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
                 }
                 if (k0 + kBN - 1 > qpos0) {                        // tile reaches past the first row
                     const int qpos = qpos0 + lr;
@@ -723,7 +780,7 @@ prefill_split_kernel(Params P)
                                 if (k0 + 16 * kg + 4 * lp + e > qpos) sc[j][kg][e] = neg_inf();
                 }
                 u32x4_t pb[RS];
-                softmax_tile<RS>(sc, m_run, l_run, o, qk, pb);
+                softmax_tile<RS>(sc, m_run, l_run, o, qkr, pb);
 #pragma unroll
                 for (int j = 0; j < RS; ++j)
 #pragma unroll
