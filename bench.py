@@ -38,7 +38,7 @@ ROTATE_BYTES = 1 << 30         # >= 4x the 256 MB MALL
 # HBM bytes per launch of each leg's kernel, from two rocprofv3 --pmc runs of this script
 # (FETCH_SIZE, then WRITE_SIZE, scaled by what they read for a 256 MiB copy; commands and tables in
 # profiles/*.md).  They are properties of the kernels as built when profiled, not measured here.
-MEASURED_TRAFFIC = {"w4_gemv_M1": 62575635, "decode_b8_4k": 35963204, "prefill_cfg3": 35150368}
+MEASURED_TRAFFIC = {"w4_gemv_M1": 62582098, "decode_b8_4k": 35966787, "prefill_cfg3": 38111782}
 METRIC = "µs/layer + achieved HBM GB/s (%roofline): decode attn b8@4k, W4 GEMV M=1"
 
 
@@ -90,10 +90,23 @@ def time_launches(launch, n_sets: int, steps: int, warmup: int, arm: bool = True
     return t0.elapsed_time(t1) / steps, per
 
 
+def _pct(xs, q):
+    """q-quantile (0..1) of xs by linear interpolation."""
+    xs = sorted(xs)
+    if not xs:
+        return float("nan")
+    pos = q * (len(xs) - 1)
+    lo = int(pos)
+    hi = min(lo + 1, len(xs) - 1)
+    return xs[lo] + (xs[hi] - xs[lo]) * (pos - lo)
+
+
 def _summary(wall_ms, per, nbytes):
     k_us = statistics.mean(per) * 1e3
     return {"us_step": round(wall_ms * 1e3, 3), "us_kernel": round(k_us, 3),
             "us_kernel_median": round(statistics.median(per) * 1e3, 3),
+            "us_kernel_p10": round(_pct(per, 0.1) * 1e3, 3),
+            "us_kernel_p90": round(_pct(per, 0.9) * 1e3, 3),
             "bytes": nbytes, "GBps_step": round(nbytes / (wall_ms * 1e-3) / 1e9, 1),
             "GBps_kernel": round(nbytes / (k_us * 1e-6) / 1e9, 1),
             "frac_kernel": round(nbytes / (k_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -520,6 +533,95 @@ def cpu_baseline_w4(N: int, K: int, budget_s: float = 15.0):
             "cpu_model": _cpu_model()}
 
 
+def _cpu_time(fn, budget_s: float, min_runs: int = 3, max_runs: int = 20):
+    """Median wall time of fn after 2 warm-ups, within about budget_s."""
+    for _ in range(2):
+        fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_legs(budget_s: float = 4.0):
+    """Further CPU baselines (reported beside cpu_baseline, not targets), each a bounded sample on
+    the host's cores with torch fp32: the cfg1 GEMV on pre-dequantised weights, decode attention of
+    one b8@4k sequence (block-table gather, fp8 dequant, per-head softmax.V) scaled to the
+    algorithmic bytes of that sequence, and 64 query tokens of the cfg3 prefill at the end of its
+    causal range (q0 + 1984 .. q0 + 2047) scaled to their FLOPs."""
+    import torch
+    from fp8kv_amd import workloads
+    from oracle.formats import E2M1, E8M0, E4M3FN
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    out = {"cores": threads, "torch_threads": torch.get_num_threads(), "cpu_model": _cpu_model()}
+    g = torch.Generator().manual_seed(11)
+
+    # matvec on pre-dequantised fp32 weights (cfg1, M = 1)
+    N, K = 28672, 4096
+    case = workloads.w4_case(N=N, K=K, M=1, seed=5)
+    lut = torch.tensor(E2M1, dtype=torch.float32)
+    w = torch.empty(N, K, dtype=torch.float32)
+    w[:, 0::2] = lut[(case["W"] & 15).long()]
+    w[:, 1::2] = lut[(case["W"] >> 4).long()]
+    w = (w.view(N, K // 32, 32) * torch.tensor(E8M0, dtype=torch.float32)[case["St"].long()][:, :, None]).view(N, K)
+    x = case["X"].float()
+    med, n = _cpu_time(lambda: x @ w.t(), budget_s)
+    out["w4_gemv_M1_predequantised"] = {"value": round(w4_bytes(N, K, 1) / med / 1e9, 3), "unit": "GB/s",
+                                        "ms": round(med * 1e3, 3), "runs": n}
+    del w
+
+    # decode attention, one sequence of the b8@4k workload
+    HQ, HKV, D, PBLK, ctx, nb = 24, 4, 128, 16, 4096, 5060
+    pool = torch.randint(0, 256, (nb, PBLK, HKV, 2 * D), dtype=torch.uint8, generator=g)
+    pool[(pool & 0x7F) == 0x7F] = 0x3C
+    bt = torch.randperm(nb, generator=g)[:ctx // PBLK]
+    q = torch.randn(HQ, D, generator=g).to(torch.bfloat16).float()
+    e4 = torch.tensor(E4M3FN, dtype=torch.float32)
+    ks = vs = 0.01
+
+    def decode_once():
+        kv = pool.index_select(0, bt).view(ctx, HKV, 2 * D)
+        k = e4[kv[:, :, :D].long()] * ks
+        v = e4[kv[:, :, D:].long()] * vs
+        qh = q.view(HKV, HQ // HKV, D)
+        s = torch.einsum("hgd,thd->hgt", qh, k) / math.sqrt(D)
+        return torch.einsum("hgt,thd->hgd", torch.softmax(s, -1), v)
+
+    med, n = _cpu_time(decode_once, budget_s)
+    dbytes = decode_bytes([ctx], HQ, HKV, D, PBLK)
+    out["decode_one_seq_4k"] = {"value": round(dbytes / med / 1e9, 3), "unit": "GB/s",
+                                "ms": round(med * 1e3, 3), "runs": n,
+                                "sample": "one sequence of b8@4k (8x that for the whole batch)"}
+
+    # prefill: the last 64 query tokens of cfg3 (q0 = 2048, qlen = 2048)
+    q0, qlen, T = 2048, 2048, 64
+    pos = torch.arange(q0 + qlen - T, q0 + qlen)
+    ctxp = q0 + qlen
+    kvp = torch.randint(0, 256, (ctxp, HKV, 2 * D), dtype=torch.uint8, generator=g)
+    kvp[(kvp & 0x7F) == 0x7F] = 0x3C
+    qp = torch.randn(T, HQ, D, generator=g).to(torch.bfloat16).float()
+
+    def prefill_once():
+        k = e4[kvp[:, :, :D].long()] * ks
+        v = e4[kvp[:, :, D:].long()] * vs
+        qh = qp.view(T, HKV, HQ // HKV, D)
+        s = torch.einsum("thgd,khd->hgtk", qh, k) / math.sqrt(D)
+        mask = torch.arange(ctxp)[None, :] > pos[:, None]
+        s = s.masked_fill(mask, float("-inf"))
+        return torch.einsum("hgtk,khd->thgd", torch.softmax(s, -1), v)
+
+    med, n = _cpu_time(prefill_once, budget_s)
+    fl = 4 * D * HQ * int((pos + 1).sum())
+    out["prefill_cfg3_64_tokens"] = {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s",
+                                     "ms": round(med * 1e3, 3), "runs": n,
+                                     "sample": "query tokens 1984..2047 of cfg3 (causal over 4032..4095 keys)"}
+    return out
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -585,6 +687,7 @@ def main():
     if "copy" in legs_wanted:
         legs["copy_256MiB"] = bench_copy(max(5, args.steps // 4), max(2, args.warmup // 4))
     cpu = None if (args.no_cpu_baseline or m1 is None) else cpu_baseline_w4(N, K)
+    extra_cpu = None if args.no_cpu_baseline else cpu_legs()
     head = m1 if m1 is not None else dec
     if head is None:                     # only auxiliary legs asked for: report them alone
         print(json.dumps({"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1,
@@ -610,6 +713,7 @@ def main():
                      "unit": "GB/s", "frac": head["frac_kernel"],
                      "traffic": MEASURED_TRAFFIC["w4_gemv_M1" if m1 is not None else "decode_b8_4k"]},
         "cpu_baseline": cpu,
+        "cpu_legs": extra_cpu,
         "legs": legs,
     }
     if "prefill_cfg3" in legs:
