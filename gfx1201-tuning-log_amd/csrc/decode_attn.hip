@@ -110,6 +110,7 @@ struct ChunkIds {
 };
 
 typedef __attribute__((address_space(4))) const int32_t const_i32_t;   // read-only for the launch
+typedef __attribute__((address_space(4))) const float const_f32_t;
 
 template <int NG>
 __device__ __forceinline__ ChunkIds<NG> load_chunk_ids(const Params& P, const int32_t* btrow, int c0, int last)
@@ -336,10 +337,32 @@ __device__ __forceinline__ void merge_all(const Params& P, const float* recs, in
     }
 }
 
+// seq_lens and qsl (also in P) lead the argument list: the library is built with kernel-argument
+// preloading, so the hardware places them in SGPRs before the first instruction, and the sequence
+// length (the head of the dependent chain seq_lens -> block ids -> K/V) and the query row are
+// requested together with the rest of P instead of after it.
 template <int W, int NG, int DEPTH, bool KF>
 __global__ void __launch_bounds__(W * 64)
-decode_kernel(Params P)
+decode_kernel(const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, Params P)
 {
+    // The two loads go out together with the loads of every argument the block-id, Q and K/V
+    // requests need (the asm takes all of them, so one wait covers them all) rather than after
+    // them; later reads of these fields reuse the loaded values.
+    int seqlen = seq_lens[blockIdx.z];
+    int qtok = qsl[blockIdx.z];
+    int nsplit = P.nsplit;
+    const int32_t* bt = P.bt;
+    int64_t bt_stride = P.bt_stride;
+    {
+        const __bf16* qp = P.q;
+        const uint8_t* kp = P.k;
+        const uint8_t* vp = P.v;
+        int64_t q_stride = P.q_stride, sk0 = P.sk0, sk1 = P.sk1, sk2 = P.sk2;
+        int64_t sv0 = P.sv0, sv1 = P.sv1, sv2 = P.sv2;
+        asm volatile("" : "+s"(seqlen), "+s"(qtok), "+s"(nsplit), "+s"(bt), "+s"(bt_stride),
+                          "+s"(qp), "+s"(kp), "+s"(vp), "+s"(q_stride), "+s"(sk0), "+s"(sk1),
+                          "+s"(sk2), "+s"(sv0), "+s"(sv1), "+s"(sv2));
+    }
     constexpr int CH = 16 * NG;                 // tokens per chunk
     constexpr int T = W * 64;
     constexpr int EPT = (kMaxGqa * kD + T - 1) / T;   // merge elements per thread (upper bound)
@@ -356,26 +379,38 @@ decode_kernel(Params P)
     const int lp = lane >> 4;
     const int gqa = P.gqa;
 
-    const int seqlen = P.seq_lens[seq];
-    const int qtok = P.qsl[seq];
     int lo, hi;
-    split_span(seqlen, P.nsplit, sp, lo, hi);
-    const int32_t* btrow = P.bt + (int64_t)seq * P.bt_stride;
+    split_span(seqlen, nsplit, sp, lo, hi);
+    const int32_t* btrow = bt + (int64_t)seq * bt_stride;
 
-    // Q^T fragments and the scales first (they do not depend on the block table): lane (h, p)
-    // holds head h at d = 16p + (0..15) and 64 + 16p + (0..15).
+    // The wave's chunks start at c_first and step by `stride`.
+    const int stride = CH * W;
+    const int c_first = lo + CH * wave;
+    const int last = (hi - 1) & ~15;
+    // The first pair's block ids go out right behind the span (they head the dependent chain to
+    // the K/V bytes); everything below is issued while they are in flight.
+    [[maybe_unused]] ChunkIds<NG> ia, ib;
+    if constexpr (DEPTH != 1) {
+        if (c_first < hi) {
+            ia = load_chunk_ids<NG>(P, btrow, c_first, last);
+            ib = load_chunk_ids<NG>(P, btrow, c_first + stride, last);
+        }
+    }
+
+    // Q^T fragments: lane (h, p) holds head h at d = 16p + (0..15) and 64 + 16p + (0..15).  Lanes
+    // h >= gqa load head 0 again: their columns of S and O are never stored, and unconditional
+    // loads leave no exec-masked write to a load's destination (which would make the compiler
+    // wait for every load in flight).  The scales are scalar loads (lgkmcnt, not vmcnt).
     u32x4_t qf[4];
     {
-        const u32x4_t zero = {0u, 0u, 0u, 0u};
-        const bool ok = lr < gqa;
-        const __bf16* qrow = P.q + (int64_t)qtok * P.q_stride + (int64_t)(kh * gqa + (ok ? lr : 0)) * kD;
-        qf[0] = ok ? load_16(qrow + 16 * lp) : zero;
-        qf[1] = ok ? load_16(qrow + 16 * lp + 8) : zero;
-        qf[2] = ok ? load_16(qrow + 64 + 16 * lp) : zero;
-        qf[3] = ok ? load_16(qrow + 64 + 16 * lp + 8) : zero;
+        const __bf16* qrow = P.q + (int64_t)qtok * P.q_stride + (int64_t)(kh * gqa + (lr < gqa ? lr : 0)) * kD;
+        qf[0] = load_16(qrow + 16 * lp);
+        qf[1] = load_16(qrow + 16 * lp + 8);
+        qf[2] = load_16(qrow + 64 + 16 * lp);
+        qf[3] = load_16(qrow + 64 + 16 * lp + 8);
     }
-    const float qk_scale = P.sm_scale * P.k_scale[0] * kLog2e;
-    const float vs = P.v_scale[0];
+    const float qk_scale = P.sm_scale * *(const_f32_t*)P.k_scale * kLog2e;
+    const float vs = *(const_f32_t*)P.v_scale;
 
     WaveState st;
     st.m_run = neg_inf();
@@ -383,10 +418,6 @@ decode_kernel(Params P)
 #pragma unroll
     for (int n = 0; n < 8; ++n) st.o[n] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 
-    // The wave's chunks start at c_first and step by `stride`.
-    const int stride = CH * W;
-    const int c_first = lo + CH * wave;
-    const int last = (hi - 1) & ~15;
     if (c_first < hi) {
         const LaneOffsets lofs = lane_offsets(P, lr, lp);
         ChunkRegs<NG> ca;
@@ -405,11 +436,13 @@ decode_kernel(Params P)
             // code up to the use of B keeps the compiler's wait counts exact.  A chunk B past hi
             // reads one broadcast line per instruction and is not used.
             do {
-                ChunkIds<NG> ia = load_chunk_ids<NG>(P, btrow, c0, last);
-                ChunkIds<NG> ib = load_chunk_ids<NG>(P, btrow, c0 + stride, last);
                 ids_ready(ia, ib);
                 issue_chunk<NG, KF>(ca, P, lofs, ia, kh, c0, hi, last);
                 issue_chunk<NG, KF>(cb, P, lofs, ib, kh, c0 + stride, hi, last);
+                if (c0 + 2 * stride < hi) {            // the next pair's ids, a round trip ahead
+                    ia = load_chunk_ids<NG>(P, btrow, c0 + 2 * stride, last);
+                    ib = load_chunk_ids<NG>(P, btrow, c0 + 3 * stride, last);
+                }
                 consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
                 if (c0 + stride >= hi) break;
                 consume_chunk<NG>(cb, st, qf, qk_scale, c0 + stride, hi, lp);
@@ -701,13 +734,13 @@ extern "C" int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
     switch (g_variant) {
-        case 0: launch_kernel(decode_kernel<8, 4, 1, false>, grid, dim3(8 * 64), 0, st, P); break;
-        case 1: launch_kernel(decode_kernel<8, 2, 1, false>, grid, dim3(8 * 64), 0, st, P); break;
-        case 2: launch_kernel(decode_kernel<4, 4, 1, false>, grid, dim3(4 * 64), 0, st, P); break;
-        case 3: launch_kernel(decode_kernel<4, 4, 2, false>, grid, dim3(4 * 64), 0, st, P); break;
-        case 5: launch_kernel(decode_kernel<8, 2, 2, false>, grid, dim3(8 * 64), 0, st, P); break;
-        case 6: launch_kernel(decode_kernel<8, 2, 1, true>, grid, dim3(8 * 64), 0, st, P); break;
-        default: launch_kernel(decode_kernel<8, 2, 2, true>, grid, dim3(8 * 64), 0, st, P); break;
+        case 0: launch_kernel(decode_kernel<8, 4, 1, false>, grid, dim3(8 * 64), 0, st, P.seq_lens, P.qsl, P); break;
+        case 1: launch_kernel(decode_kernel<8, 2, 1, false>, grid, dim3(8 * 64), 0, st, P.seq_lens, P.qsl, P); break;
+        case 2: launch_kernel(decode_kernel<4, 4, 1, false>, grid, dim3(4 * 64), 0, st, P.seq_lens, P.qsl, P); break;
+        case 3: launch_kernel(decode_kernel<4, 4, 2, false>, grid, dim3(4 * 64), 0, st, P.seq_lens, P.qsl, P); break;
+        case 5: launch_kernel(decode_kernel<8, 2, 2, false>, grid, dim3(8 * 64), 0, st, P.seq_lens, P.qsl, P); break;
+        case 6: launch_kernel(decode_kernel<8, 2, 1, true>, grid, dim3(8 * 64), 0, st, P.seq_lens, P.qsl, P); break;
+        default: launch_kernel(decode_kernel<8, 2, 2, true>, grid, dim3(8 * 64), 0, st, P.seq_lens, P.qsl, P); break;
     }
     return finish_launch();
 }
