@@ -307,10 +307,26 @@ __device__ __forceinline__ void merge_all(const Params& P, const float* recs, in
                 ov[j][s] = load_coherent(recs + (int64_t)(s < ns ? s : ns - 1) * rf + e);
         }
         if (e0 == 0) {
-            for (int i = tid; i < NSG; i += T) {
-                const int s = i / gqa, h = i - s * gqa;
-                wm[i] = load_coherent(recs + (int64_t)s * rf + E + h);
-                wl[i] = load_coherent(recs + (int64_t)s * rf + E + gqa + h);
+            // Every m and l value goes into registers first (unconditional loads, index clamped),
+            // then to LDS: one wait covers them and the o values above.  Storing each value as it
+            // arrives put a vmcnt(0) between the m and the l loads, a second round trip.
+            constexpr int NI = (SMAX * kMaxGqa + T - 1) / T;
+            float mv[NI], lv[NI];
+#pragma unroll
+            for (int k = 0; k < NI; ++k) {
+                const int i = tid + k * T;
+                const int ic = i < NSG ? i : NSG - 1;
+                const int s = ic / gqa, h = ic - s * gqa;
+                mv[k] = load_coherent(recs + (int64_t)s * rf + E + h);
+                lv[k] = load_coherent(recs + (int64_t)s * rf + E + gqa + h);
+            }
+#pragma unroll
+            for (int k = 0; k < NI; ++k) {
+                const int i = tid + k * T;
+                if (i < NSG) {
+                    wm[i] = mv[k];
+                    wl[i] = lv[k];
+                }
             }
         }
         __syncthreads();
