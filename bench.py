@@ -139,7 +139,9 @@ def bench_w4(N: int, K: int, M: int, steps: int, warmup: int):
 
 def bench_decode(ctx, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK=16, pool_blocks=5060,
                  seed=0):
-    """Decode attention over rotated engine-layout layer pools [NB, HKV, PBLK, 2D] (K | V)."""
+    """Decode attention over rotated engine-layout layer pools [NB, HKV, PBLK, 2D] (K | V), each
+    holding N(0,1) K and V quantised to e4m3 with its own per-tensor amax / 448 scales (the cache
+    BASELINE configs[0] specifies)."""
     import torch
     from fp8kv_amd import ops, workloads
     dev = torch.device("cuda")
@@ -149,10 +151,8 @@ def bench_decode(ctx, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK=16, poo
     g = torch.Generator(device=dev).manual_seed(seed)
     pools = []
     for _ in range(n_sets):
-        kv = torch.randint(0, 256, (pool_blocks, HKV, PBLK, 2 * D), dtype=torch.uint8, device=dev,
-                           generator=g)
-        kv[(kv & 0x7F) == 0x7F] = 0x3C                   # no NaN codes in the synthetic cache
-        pools.append(workloads.engine_views(kv, D) + (kv,))
+        kv, kss, vss = workloads.engine_pool_amax(pool_blocks, HKV, PBLK, D, g, dev)
+        pools.append(workloads.engine_views(kv, D) + (kv, kss, vss))
     gc = torch.Generator().manual_seed(seed)
     need = [math.ceil(c / PBLK) for c in ctx]
     perm = torch.randperm(pool_blocks, generator=gc)
@@ -166,12 +166,10 @@ def bench_decode(ctx, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK=16, poo
     out = torch.empty_like(q)
     qsl = torch.arange(NS + 1, dtype=torch.int32, device=dev)
     sl = torch.tensor(ctx, dtype=torch.int32, device=dev)
-    ks = torch.tensor([0.01], device=dev)
-    vs = torch.tensor([0.01], device=dev)
     nsplit = ops.decode_num_splits(NS, HKV, max(ctx))
 
     def launch(i):
-        kc, vc, _ = pools[i]
+        kc, vc, _, ks, vs = pools[i]
         ops.decode_attention(q, kc, vc, out, qsl, sl, bt, ks, vs, 1 / math.sqrt(D),
                              num_splits=nsplit)
 
@@ -334,7 +332,7 @@ def bench_stack(steps: int, warmup: int, layers: int = STACK_LAYERS, M: int = 8,
     the path), so a step is exactly the 5 x layers hot-path launches.  Timed eagerly and as one
     captured HIP graph replayed per step; tokens/s = M / step time."""
     import torch
-    from fp8kv_amd import ops
+    from fp8kv_amd import ops, workloads
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(4)
     nbl = ctx // PBLK
@@ -348,28 +346,23 @@ def bench_stack(steps: int, warmup: int, layers: int = STACK_LAYERS, M: int = 8,
                   for _, N, K in STACK_LINEARS])
         St.append([torch.randint(119, 124, (N, K // 32), dtype=torch.uint8, device=dev, generator=g)
                    for _, N, K in STACK_LINEARS])
-        pool = torch.randint(0, 256, (M * nbl, HKV, PBLK, 2 * D), dtype=torch.uint8, device=dev,
-                             generator=g)
-        pool[(pool & 0x7F) == 0x7F] = 0x3C
-        kv.append(pool)
+        pool, kss, vss = workloads.engine_pool_amax(M * nbl, HKV, PBLK, D, g, dev)
+        kv.append((pool, kss, vss))
         bts.append(torch.randperm(M * nbl, device=dev, generator=g).to(torch.int32).view(M, nbl))
     q = torch.randn(M, HQ, D, device=dev, generator=g).to(torch.bfloat16)
     out = torch.empty_like(q)
     qsl = torch.arange(M + 1, dtype=torch.int32, device=dev)
     sl = torch.full((M,), ctx, dtype=torch.int32, device=dev)
-    ks = torch.tensor([0.01], device=dev)
-    vs = torch.tensor([0.01], device=dev)
     nsplit = ops.decode_num_splits(M, HKV, ctx)
     scratch = ops.decode_scratch(ops.decode_scratch_bytes(M, HQ, HKV, nsplit, D), dev)
-    views = [(pool[:, :, :, :D].transpose(1, 2).view(torch.float8_e4m3fn),
-              pool[:, :, :, D:].transpose(1, 2).view(torch.float8_e4m3fn)) for pool in kv]
+    views = [workloads.engine_views(pool, D) + (kss, vss) for pool, kss, vss in kv]
 
     def step():
         for li in range(layers):
             for j, (_, N, K) in enumerate(STACK_LINEARS):
                 ops.h4mv(X[(N, K)], W[li][j], St[li][j], out=Y[(N, K)])
                 if j == 0:
-                    kc, vc = views[li]
+                    kc, vc, ks, vs = views[li]
                     ops.decode_attention(q, kc, vc, out, qsl, sl, bts[li], ks, vs, 1 / math.sqrt(D),
                                          num_splits=nsplit, scratch=scratch)
 
@@ -386,7 +379,7 @@ def bench_stack(steps: int, warmup: int, layers: int = STACK_LAYERS, M: int = 8,
 
     def attention_only():
         for li in range(layers):
-            kc, vc = views[li]
+            kc, vc, ks, vs = views[li]
             ops.decode_attention(q, kc, vc, out, qsl, sl, bts[li], ks, vs, 1 / math.sqrt(D),
                                  num_splits=nsplit, scratch=scratch)
 
@@ -460,8 +453,7 @@ def bench_prefill(qlens, q0s, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK
     need = [math.ceil(c / PBLK) for c in ctx]
     nb = sum(need)
     g = torch.Generator(device=dev).manual_seed(seed)
-    kv = torch.randint(0, 256, (nb, HKV, PBLK, 2 * D), dtype=torch.uint8, device=dev, generator=g)
-    kv[(kv & 0x7F) == 0x7F] = 0x3C
+    kv, ks, vs = workloads.engine_pool_amax(nb, HKV, PBLK, D, g, dev)   # N(0,1), amax / 448 scales
     kc, vc = workloads.engine_views(kv, D)
     gc = torch.Generator().manual_seed(seed)
     perm = torch.randperm(nb, generator=gc)
@@ -474,8 +466,6 @@ def bench_prefill(qlens, q0s, steps: int, warmup: int, HQ=24, HKV=4, D=128, PBLK
     T = sum(qlens)
     q = torch.randn(T, HQ, D, generator=gc).to(torch.bfloat16).to(dev)
     out = torch.empty_like(q)
-    ks = torch.tensor([0.02], device=dev)
-    vs = torch.tensor([0.02], device=dev)
     cu = torch.tensor([0] + list(torch.tensor(qlens).cumsum(0).tolist()), dtype=torch.int32, device=dev)
     sl = torch.tensor(ctx, dtype=torch.int32, device=dev)
 
@@ -576,12 +566,12 @@ def cpu_legs(budget_s: float = 4.0):
 
     # decode attention, one sequence of the b8@4k workload
     HQ, HKV, D, PBLK, ctx, nb = 24, 4, 128, 16, 4096, 5060
-    pool = torch.randint(0, 256, (nb, PBLK, HKV, 2 * D), dtype=torch.uint8, generator=g)
-    pool[(pool & 0x7F) == 0x7F] = 0x3C
+    pool_e, ks_t, vs_t = workloads.engine_pool_amax(nb, HKV, PBLK, D, g, "cpu")
+    pool = pool_e.transpose(1, 2).contiguous()           # [nb, PBLK, HKV, 2D]
     bt = torch.randperm(nb, generator=g)[:ctx // PBLK]
     q = torch.randn(HQ, D, generator=g).to(torch.bfloat16).float()
     e4 = torch.tensor(E4M3FN, dtype=torch.float32)
-    ks = vs = 0.01
+    ks, vs = float(ks_t), float(vs_t)
 
     def decode_once():
         kv = pool.index_select(0, bt).view(ctx, HKV, 2 * D)
@@ -601,8 +591,8 @@ def cpu_legs(budget_s: float = 4.0):
     q0, qlen, T = 2048, 2048, 64
     pos = torch.arange(q0 + qlen - T, q0 + qlen)
     ctxp = q0 + qlen
-    kvp = torch.randint(0, 256, (ctxp, HKV, 2 * D), dtype=torch.uint8, generator=g)
-    kvp[(kvp & 0x7F) == 0x7F] = 0x3C
+    kvp_e, _, _ = workloads.engine_pool_amax(ctxp, HKV, 1, D, g, "cpu")
+    kvp = kvp_e.view(ctxp, HKV, 2 * D)
     qp = torch.randn(T, HQ, D, generator=g).to(torch.bfloat16).float()
 
     def prefill_once():
@@ -705,7 +695,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "e2m1xbf16->f32" if m1 is not None else "e4m3xbf16->f32",
-        "data": "synthetic (seeded random codes/scales/activations and fp8 KV pools, rotated over >1 GB)",
+        "data": ("synthetic: seeded uniform e2m1 codes, e8m0 scales 2^-8..2^-4 and N(0,1) bf16 "
+                 "activations (configs[1]); fp8 KV pools of N(0,1) K/V with per-tensor amax/448 scales "
+                 "(configs[0]); rotated over >1 GB"),
         "config": {"workload": ("configs[1] MXFP4 W4A16 matvec K=4096 N=28672 M=1" if m1 is not None
                                 else "decode attention b8@4k, 24/4 heads, D=128, block 16"),
                    "rotation_sets": head["rotation_sets"]},

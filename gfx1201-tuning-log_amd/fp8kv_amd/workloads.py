@@ -63,6 +63,24 @@ def _make_cache(nb: int, pblk: int, hkv: int, d: int, g: torch.Generator, layout
     raise ValueError(layout)
 
 
+def engine_pool_amax(nb: int, hkv: int, pblk: int, d: int, generator: torch.Generator,
+                     device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """An engine-layout fp8 KV pool [nb, hkv, pblk, 2d] (K | V) built on `device` the way
+    BASELINE.json configs[0] specifies the cache: K and V ~ N(0,1), each quantised to e4m3 with a
+    per-tensor scale amax / 448.  Returns (pool, k_scale, v_scale), the scales as fp32 [1]
+    device tensors (the form the attention hooks pass)."""
+    pool = torch.empty(nb, hkv, pblk, 2 * d, dtype=torch.uint8, device=device)
+    scales = []
+    for half in (slice(0, d), slice(d, 2 * d)):
+        x = torch.randn(nb, hkv, pblk, d, device=device, generator=generator)
+        amax = x.abs().max()
+        scale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
+        pool[..., half] = (x / scale).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
+        scales.append(scale.reshape(1).to(torch.float32))
+        del x
+    return pool, scales[0], scales[1]
+
+
 def engine_views(kv_cache: torch.Tensor, head_size: int):
     """The K and V fp8 views the attention hook builds (vllm-fp8kv/fp8kv_override.py:82-85)."""
     kc = kv_cache.transpose(1, 2)
