@@ -92,17 +92,19 @@ __device__ __forceinline__ void dma_lane_rc(bool is_v, int lane, int& r, int& c)
     }
 }
 
-// global_load_lds_dwordx4 issued as inline assembly: lane i's 16 bytes land at lds_dst + 16 i.  The
-// compiler does not see this copy, so it inserts no wait for it: in particular no vmcnt(0)
-// before LDS reads it cannot prove disjoint from the copy's destination, which would drain the
-// whole prefetch ring each tile.  Completion is tracked only by the kernel's explicit
-// vmcnt waits (vmcnt counts in issue order, so the compiler's own waits for its loads stay
-// correct - at worst they wait longer).  lds_dst must be wave-uniform.
-__device__ __forceinline__ void dma16_untracked(const void* src, unsigned char* lds_dst)
+// global_load_lds_dwordx4 issued as inline assembly, in its scalar-base form: lane i's 16 bytes
+// from sbase + voff (sbase a wave-uniform 64-bit address, voff this lane's 32-bit offset, so no
+// 64-bit address arithmetic per lane) land at lds_dst + 16 i.  The compiler does not see this
+// copy, so it inserts no wait for it: in particular no vmcnt(0) before LDS reads it cannot prove
+// disjoint from the copy's destination, which would drain the whole prefetch ring each tile.
+// Completion is tracked only by the kernel's explicit vmcnt waits (vmcnt counts in issue order,
+// so the compiler's own waits for its loads stay correct - at worst they wait longer).  lds_dst
+// must be wave-uniform.
+__device__ __forceinline__ void dma16_saddr(const void* sbase, uint32_t voff, unsigned char* lds_dst)
 {
     const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_void_t*)lds_dst;
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :: "s"(lds_addr), "v"(src) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :: "s"(lds_addr), "v"(voff), "s"(sbase) : "memory", "m0");
 }
 
 // Block ids of 16-key groups 64 b .. 64 b + 63 (batch b), one per lane (0 past the context).
@@ -136,7 +138,7 @@ __device__ __forceinline__ void issue_tile(const Params& P, unsigned char* dst, 
         const uint8_t* base = is_v ? P.v + blk * P.sv0 + (int64_t)kh * P.sv2
                                    : P.k + blk * P.sk0 + (int64_t)kh * P.sk2;
         const uint32_t off = slot * (uint32_t)(is_v ? P.sv1 : P.sk1) + 16u * (uint32_t)c;
-        dma16_untracked(base + off, dst + I * 1024);
+        dma16_saddr(base, off, dst + I * 1024);
     }
 }
 
@@ -639,8 +641,13 @@ prefill_split_kernel(Params P)
     const int dma_rk = 8 * (wave & 3) + dma_r;                     // key offset within a tile
     const uint8_t* dma_base = dma_v ? P.v + (int64_t)kh * P.sv2 : P.k + (int64_t)kh * P.sk2;
     const int64_t dma_s0 = dma_v ? P.sv0 : P.sk0;
-    const uint64_t dma_s1 = (uint64_t)(dma_v ? P.sv1 : P.sk1);
-    const uint64_t dma_chunk = 16u * (uint32_t)dma_c;
+    const uint32_t dma_s1 = (uint32_t)(dma_v ? P.sv1 : P.sk1);    // < 2^32 / block size (host check)
+    const uint32_t dma_chunk = 16u * (uint32_t)dma_c;
+    // The wave's 8 rows start at a multiple of 8 and the block size is a power of two >= 16, so
+    // the slot of key 32 t + dma_rk is (32 t + 8 (wave & 3)) mod block size (wave-uniform, folded
+    // into the scalar base) plus dma_r (this lane's fixed offset).
+    const int dma_row0 = 8 * __builtin_amdgcn_readfirstlane(wave & 3);
+    const uint32_t voff_lane = (uint32_t)dma_r * dma_s1 + dma_chunk;
 
     for (int ph = 0; ph < nphase; ++ph) {
         const int blk = ph == 0 ? blk_b : blk_a;
@@ -685,12 +692,16 @@ prefill_split_kernel(Params P)
             for (int u = u0; u < u1; ++u) {
                 const int t = wi * NT + u;
                 if (t < ntiles) {
-                    int key = t * kBN + dma_rk;
-                    if (t * kBN + kBN > k_hi) key = min(key, k_hi - 1);
-                    const uint64_t off = (uint64_t)(uint32_t)(key & (P.pblk - 1)) * dma_s1 + dma_chunk;
                     const int64_t b = __builtin_amdgcn_readlane(bids, u);
-                    dma16_untracked(dma_base + b * dma_s0 + off,
-                                    ring + (wi % RW) * kWinBytes + u * kTileBytes + wave * 1024);
+                    const uint8_t* sb = dma_base + b * dma_s0;
+                    uint32_t voff = voff_lane;
+                    if (t * kBN + kBN > k_hi) {             // the tile holding the end of the keys
+                        const int key = min(t * kBN + dma_rk, k_hi - 1);
+                        voff = (uint32_t)(key & (P.pblk - 1)) * dma_s1 + dma_chunk;
+                    } else {
+                        sb += (uint32_t)((t * kBN + dma_row0) & (P.pblk - 1)) * dma_s1;
+                    }
+                    dma16_saddr(sb, voff, ring + (wi % RW) * kWinBytes + u * kTileBytes + wave * 1024);
                 }
             }
         };
@@ -996,6 +1007,9 @@ int check_common(const void* q, const void* k_cache, const void* v_cache, void* 
     if ((sk0 | sk1 | sk2) & 15) return FP8KV_ERR_ALIGN;
     if ((sv0 | sv1 | sv2) & 7) return FP8KV_ERR_ALIGN;
     if ((q_row_stride & 7) || (out_row_stride & 7)) return FP8KV_ERR_ALIGN;
+    // The tile copies address a row within its cache block with a 32-bit offset.
+    if (sk1 < 0 || sv1 < 0 || (int64_t)(block_size - 1) * (sk1 > sv1 ? sk1 : sv1) + 128 >= ((int64_t)1 << 32))
+        return FP8KV_ERR_SHAPE;
     return FP8KV_OK;
 }
 

@@ -132,6 +132,32 @@ def test_cache_write_zero_tokens_is_a_no_op(lib):
     assert lib.fp8kv_cache_write(*args) == 0
 
 
+# fp8kv_prefill_attn on the engine layout [NB, HKV, PBLK, 2D]: qlen = 0 returns before any launch.
+PF_OK = [A, 24 * 128, A, A + 128, 16384, 256, 4096, 16384, 256, 4096, A, 24 * 128, A, 64, A, A,
+         0.088, 24, 4, 128, 16, 0, 0, None]
+
+
+@pytest.mark.parametrize("changes,code", [
+    ({0: None}, 1), ({12: None}, 1), ({18: 0}, 1), ({21: -1}, 1), ({22: -1}, 1),
+    ({19: 64}, 2), ({17: 25}, 2), ({17: 68}, 2), ({20: 8}, 2), ({20: 48}, 2),
+    ({2: A + 8}, 3), ({3: A + 4}, 3), ({5: 264}, 3), ({8: 260}, 3), ({1: 24 * 128 + 4}, 3),
+    ({5: -256}, 2),                                  # negative slot stride
+    ({5: 1 << 28, 20: 32}, 2),                       # in-block offsets beyond 32 bits
+    ({8: 1 << 28, 20: 32}, 2),
+])
+def test_prefill_rejects_before_launch(lib, changes, code):
+    args = list(PF_OK)
+    for k, v in changes.items():
+        args[k] = v
+    assert lib.fp8kv_prefill_attn(*args) == code
+
+
+def test_prefill_accepts_largest_32_bit_block_offsets(lib):
+    args = list(PF_OK)
+    args[5] = args[8] = 1 << 27                      # 15 * 2^27 + 128 < 2^32 at block size 16
+    assert lib.fp8kv_prefill_attn(*args) == 0
+
+
 @pytest.mark.parametrize("args,code", [
     ((0, A, 64, 64, None), 1),            # null input
     ((A, A, 0, 64, None), 1),             # N = 0
