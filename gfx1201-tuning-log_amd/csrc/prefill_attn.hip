@@ -531,36 +531,50 @@ __device__ __forceinline__ float q_fp8_split(const u32x4_t (&qf)[4], uint32_t si
     return inv;
 }
 
-// Online softmax of the RS row-sets of one 32-key tile.  sc holds raw scores S^T (lane (q, p):
-// keys 16 kg + 4 p + e of query row q), -inf where masked; qkr[j] = this lane's query row's
-// factor from raw score to log2 units (|sm_scale * k_scale| * log2(e) over the row's Q scale,
-// positive: a negative scale is folded into Q's sign), so the row max of the raw scores times
-// it is the max of the scaled ones and each probability is exp2(fma(s, qk, -m)).  m_run
-// starts at kMaxFloor.  Returns the bf16 probabilities P^T as MFMA B fragments in pb.
+// Online softmax and P.V of the RS row-sets of one 32-key tile.  sc holds raw scores S^T
+// (lane (q, p): keys 16 kg + 4 p + e of query row q), -inf where masked; qkr[j] = this lane's
+// query row's factor from raw score to log2 units (|sm_scale * k_scale| * log2(e) over the row's
+// Q scale, positive: a negative scale is folded into Q's sign), so the row max of the raw scores
+// times it is the max of the scaled ones and each probability is exp2(fma(s, qk, -m)).  m_run
+// starts at kMaxFloor.  vf holds the tile's widened V^T fragments; o[j] += V^T.P^T with P in bf16.
+//
+// The row maxima of every row-set are taken first and the lazy rescale runs as one branch for
+// all of them (rows that need none get alpha = exp2(0) = 1, exact), so the exponentials of
+// row-set j and the P.V MFMAs of row-set j - 1 sit in one basic block and interleave.
 template <int RS>
-__device__ __forceinline__ void softmax_tile(const f32x4_t (&sc)[RS][2], float (&m_run)[RS],
-                                             float (&l_run)[RS], f32x4_t (&o)[RS][8],
-                                             const float (&qkr)[RS], u32x4_t (&pb)[RS])
+__device__ __forceinline__ void softmax_pv_tile(const f32x4_t (&sc)[RS][2], float (&m_run)[RS],
+                                                float (&l_run)[RS], f32x4_t (&o)[RS][8],
+                                                const float (&qkr)[RS], const u32x4_t (&vf)[8])
 {
+    float mc[RS];
+    bool need[RS];
+    bool any_need = false;
 #pragma unroll
     for (int j = 0; j < RS; ++j) {
-        const float qk = qkr[j];
         float m8 = max3_raw(sc[j][0][0], sc[j][0][1], sc[j][0][2]);
         m8 = max3_raw(m8, sc[j][0][3], sc[j][1][0]);
         m8 = max3_raw(m8, sc[j][1][1], sc[j][1][2]);
         const float mraw = max_xor16_32_raw(max_raw(m8, sc[j][1][3]));
-        const float mc = mraw * qk;                    // -inf for a fully masked row (qk > 0)
+        mc[j] = mraw * qkr[j];                         // -inf for a fully masked row (qk > 0)
         // Lazy rescale: the accumulators move to a new reference max only when the row max
         // grew by more than kRescaleSlack (then probabilities stay below 2^kRescaleSlack).
-        const bool need = mc > m_run[j] + kRescaleSlack;
-        if (__any(need)) {
-            const float m_new = need ? mc : m_run[j];
+        need[j] = mc[j] > m_run[j] + kRescaleSlack;
+        any_need |= need[j];
+    }
+    if (__any(any_need)) {
+#pragma unroll
+        for (int j = 0; j < RS; ++j) {
+            const float m_new = need[j] ? mc[j] : m_run[j];
             const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
             l_run[j] *= alpha;
 #pragma unroll
             for (int n = 0; n < 8; ++n) o[j][n] *= alpha;
             m_run[j] = m_new;
         }
+    }
+#pragma unroll
+    for (int j = 0; j < RS; ++j) {
+        const float qk = qkr[j];
         const float nm = -m_run[j];
         float p[2][4];
 #pragma unroll
@@ -569,10 +583,21 @@ __device__ __forceinline__ void softmax_tile(const f32x4_t (&sc)[RS][2], float (
             for (int e = 0; e < 4; ++e)
                 p[kg][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][kg][e], qk, nm));
         l_run[j] += ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
-        pb[j][0] = pack_bf16x2(p[0][0], p[0][1]);
-        pb[j][1] = pack_bf16x2(p[0][2], p[0][3]);
-        pb[j][2] = pack_bf16x2(p[1][0], p[1][1]);
-        pb[j][3] = pack_bf16x2(p[1][2], p[1][3]);
+        u32x4_t pb;
+        pb[0] = pack_bf16x2(p[0][0], p[0][1]);
+        pb[1] = pack_bf16x2(p[0][2], p[0][3]);
+        pb[2] = pack_bf16x2(p[1][0], p[1][1]);
+        pb[3] = pack_bf16x2(p[1][2], p[1][3]);
+#pragma unroll
+        for (int n = 0; n < 8; ++n) o[j][n] = mfma16x16x32_bf16(as_bf16x8(vf[n]), as_bf16x8(pb), o[j][n]);
+    }
+    // Interleave: the first row-set's exponentials alone, then each P.V MFMA with about three
+    // VALU instructions of the next row-set's softmax.
+    __builtin_amdgcn_sched_group_barrier(0x002, 28, 0);
+#pragma unroll
+    for (int g = 0; g < 8 * (RS - 1); ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
     }
 }
 
@@ -790,13 +815,7 @@ prefill_split_kernel(Params P)
                             for (int e = 0; e < 4; ++e)
                                 if (k0 + 16 * kg + 4 * lp + e > qpos) sc[j][kg][e] = neg_inf();
                 }
-                u32x4_t pb[RS];
-                softmax_tile<RS>(sc, m_run, l_run, o, qkr, pb);
-#pragma unroll
-                for (int j = 0; j < RS; ++j)
-#pragma unroll
-                    for (int n = 0; n < 8; ++n)
-                        o[j][n] = mfma16x16x32_bf16(as_bf16x8(vf[n]), as_bf16x8(pb[j]), o[j][n]);
+                softmax_pv_tile<RS>(sc, m_run, l_run, o, qkr, vf);
             }
             // Block ids for the next window's copies, after this iteration's LDS reads so that
             // no LDS wait in the tile work has to cover the scalar loads.
