@@ -538,33 +538,34 @@ __device__ __forceinline__ float q_fp8_split(const u32x4_t (&qf)[4], uint32_t si
 // times it is the max of the scaled ones and each probability is exp2(fma(s, qk, -m)).  m_run
 // starts at kMaxFloor.  vf holds the tile's widened V^T fragments; o[j] += V^T.P^T with P in bf16.
 //
-// The row maxima of every row-set are taken first and the lazy rescale runs as one branch for
-// all of them (rows that need none get alpha = exp2(0) = 1, exact), so the exponentials of
-// row-set j and the P.V MFMAs of row-set j - 1 sit in one basic block and interleave.
+// Lazy rescale: the accumulators move to a new reference max only when the row max grew by
+// more than kRescaleSlack (then probabilities stay below 2^kRescaleSlack).  qk > 0, so some lane
+// of a row has (its own max) * qk above m_run + kRescaleSlack exactly when the row max does: the
+// common path tests each lane's own maximum, and only the rescale branch reduces across the row's
+// four lane groups.  The branch covers all row-sets (rows that need no rescale get
+// alpha = exp2(0) = 1, exact), so the exponentials of row-set j and the P.V MFMAs of row-set
+// j - 1 sit in one basic block and interleave.
 template <int RS>
 __device__ __forceinline__ void softmax_pv_tile(const f32x4_t (&sc)[RS][2], float (&m_run)[RS],
                                                 float (&l_run)[RS], f32x4_t (&o)[RS][8],
                                                 const float (&qkr)[RS], const u32x4_t (&vf)[8])
 {
-    float mc[RS];
-    bool need[RS];
+    float m8[RS];
     bool any_need = false;
 #pragma unroll
     for (int j = 0; j < RS; ++j) {
-        float m8 = max3_raw(sc[j][0][0], sc[j][0][1], sc[j][0][2]);
-        m8 = max3_raw(m8, sc[j][0][3], sc[j][1][0]);
-        m8 = max3_raw(m8, sc[j][1][1], sc[j][1][2]);
-        const float mraw = max_xor16_32_raw(max_raw(m8, sc[j][1][3]));
-        mc[j] = mraw * qkr[j];                         // -inf for a fully masked row (qk > 0)
-        // Lazy rescale: the accumulators move to a new reference max only when the row max
-        // grew by more than kRescaleSlack (then probabilities stay below 2^kRescaleSlack).
-        need[j] = mc[j] > m_run[j] + kRescaleSlack;
-        any_need |= need[j];
+        float m = max3_raw(sc[j][0][0], sc[j][0][1], sc[j][0][2]);
+        m = max3_raw(m, sc[j][0][3], sc[j][1][0]);
+        m = max3_raw(m, sc[j][1][1], sc[j][1][2]);
+        m8[j] = max_raw(m, sc[j][1][3]);
+        any_need |= m8[j] * qkr[j] > m_run[j] + kRescaleSlack;
     }
     if (__any(any_need)) {
 #pragma unroll
         for (int j = 0; j < RS; ++j) {
-            const float m_new = need[j] ? mc[j] : m_run[j];
+            const float mc = max_xor16_32_raw(m8[j]) * qkr[j];    // -inf for a fully masked row
+            const bool need = mc > m_run[j] + kRescaleSlack;
+            const float m_new = need ? mc : m_run[j];
             const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
             l_run[j] *= alpha;
 #pragma unroll
