@@ -369,11 +369,13 @@ prefill_kernel(Params P)
                         mc = fmaxf(mc, x);
                     }
             }
-            mc = max_xor16_32(mc);
             // Lazy rescale: the accumulators move to a new reference max only when the row max
             // grew by more than kRescaleSlack (then probabilities stay below 2^kRescaleSlack).
-            const bool need = mc > m_run[j] + kRescaleSlack;
-            if (__any(need)) {
+            // Some lane of a row has its own max above the threshold exactly when the row max
+            // is, so the reduction across the row's four lane groups runs only in the branch.
+            if (__any(mc > m_run[j] + kRescaleSlack)) {
+                mc = max_xor16_32(mc);
+                const bool need = mc > m_run[j] + kRescaleSlack;
                 const float m_new = need ? mc : m_run[j];
                 const float alpha = __builtin_amdgcn_exp2f(m_run[j] - (m_new == neg_inf() ? 0.f : m_new));
                 l_run[j] *= alpha;
