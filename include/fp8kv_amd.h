@@ -128,6 +128,9 @@ size_t fp8kv_decode_scratch_bytes(int num_seqs, int num_q_heads, int num_kv_head
  *   for i in [0, qlen): query i is token q0 + i of a sequence whose context (q0 + qlen tokens,
  *   the new ones included) is mapped by block_table row 0.  Layouts, strides, scales and geometry
  *   limits as for fp8kv_decode_attn (out additionally 16-byte aligned with row stride % 8 == 0).
+ *   The slot strides sk1 and sv1 must be >= 0 with (block_size - 1) * max(sk1, sv1) + 128 < 2^32
+ *   (a row's offset within its cache block is 32-bit), else FP8KV_ERR_SHAPE; this holds for the
+ *   varlen entry point as well.
  *
  * Replaces: vllm-fp8kv/fp8kv_prefill.py:124-144, run(q, k_cache, v_cache, out, bt, kscale, vscale,
  * sm_scale, q0, qlen, BM, BN, warps, stages), the launch of the Triton kernel _prefill_attn
