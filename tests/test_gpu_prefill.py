@@ -200,6 +200,16 @@ def test_every_launch_shape(shape):
         lib.fp8kv_prefill_tune(-1)
 
 
+@pytest.mark.parametrize("PBLK", [64, 128])
+def test_large_cache_blocks(PBLK):
+    """Cache blocks larger than a 32-key tile: the copies' in-block slot offset is then a different
+    multiple of 32 for each tile of a block (key-split kernel at GQA 6 and 4, per-wave kernel
+    below 1024 keys)."""
+    _check_single(700, 600, HQ=24, HKV=4, seed=PBLK, PBLK=PBLK, layout="engine")
+    _check_single(1100, 300, HQ=16, HKV=4, seed=PBLK + 1, PBLK=PBLK, layout="engine")
+    _check_single(300, 77, HQ=24, HKV=4, seed=PBLK + 2, PBLK=PBLK, layout="engine")
+
+
 @pytest.mark.parametrize("split", range(len(SPLIT_GQA)))
 def test_every_split_shape(split):
     """Each key-split shape (row-sets per wave x head groups, keys split over the rest of the 8
