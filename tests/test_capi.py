@@ -152,6 +152,26 @@ def test_prefill_rejects_before_launch(lib, changes, code):
     assert lib.fp8kv_prefill_attn(*args) == code
 
 
+# fp8kv_prefill_attn_varlen, same cache geometry: max_query_len = 0 returns before any launch.
+PFV_OK = [A, 24 * 128, A, A + 128, 16384, 256, 4096, 16384, 256, 4096, A, 24 * 128, A, A, A, 64, A,
+          A, 0.088, 2, 24, 4, 128, 16, 0, None]
+
+
+@pytest.mark.parametrize("changes,code", [
+    ({12: None}, 1), ({13: None}, 1), ({19: 0}, 1), ({24: -1}, 1), ({19: 65536}, 2),
+    ({5: -256}, 2), ({5: 1 << 28, 23: 32}, 2), ({8: 1 << 28, 23: 32}, 2), ({2: A + 8}, 3),
+])
+def test_prefill_varlen_rejects_before_launch(lib, changes, code):
+    args = list(PFV_OK)
+    for k, v in changes.items():
+        args[k] = v
+    assert lib.fp8kv_prefill_attn_varlen(*args) == code
+
+
+def test_prefill_varlen_zero_query_is_a_no_op(lib):
+    assert lib.fp8kv_prefill_attn_varlen(*PFV_OK) == 0
+
+
 def test_prefill_accepts_largest_32_bit_block_offsets(lib):
     args = list(PF_OK)
     args[5] = args[8] = 1 << 27                      # 15 * 2^27 + 128 < 2^32 at block size 16
