@@ -942,6 +942,16 @@ inline int plan_nb(int gqa, const Shape& s)
 // Workgroups of the key-split kernel resident at once on a gfx950 part (256 CUs, one each).
 constexpr int kSplitRoundWorkgroups = 256;
 
+// Token-block ranks per (sequence, kv head) padded for the XCD-aware grid (8 % HKV == 0).
+inline int split_xcd_per(int hkv) { return (hkv <= 8 && 8 % hkv == 0) ? 8 / hkv : 1; }
+
+// True when one 16-token block per workgroup fits in one round of the key-split kernel.
+inline bool split_single_blocks_fit(int n16, int hkv, int num_seqs)
+{
+    const int per = split_xcd_per(hkv);
+    return (int64_t)((n16 + per - 1) / per * per) * hkv * num_seqs <= kSplitRoundWorkgroups;
+}
+
 int launch_split(const Params& P0, int ss, int num_seqs, int max_query_len, hipStream_t stream)
 {
     Params P = P0;
@@ -949,14 +959,14 @@ int launch_split(const Params& P0, int ss, int num_seqs, int max_query_len, hipS
     const int n16 = (max_query_len + 15) / 16;
     if (n16 == 0) return FP8KV_OK;
     P.xcd_map = (P.hkv <= 8 && 8 % P.hkv == 0) ? 1 : 0;
-    const int per = P.xcd_map ? 8 / P.hkv : 1;
+    const int per = split_xcd_per(P.hkv);
     auto round_up = [&](int n) { return (n + per - 1) / per * per; };
     // Pairs of token blocks (r, n16 - 1 - r) give every workgroup the same causal work; when one
     // block per workgroup still fits in one round of workgroups (one per CU: the ring takes most of
     // the LDS), single blocks finish sooner (the longest workgroup sees about q0 + qlen keys
     // instead of 2 q0 + qlen; measured at GQA 6: 1024 new tokens after 1024 cached 61.3 -> 38.7
     // us, 512 after 1024 52.6 -> 30.0 us).
-    P.paired = (int64_t)round_up(n16) * P.hkv * num_seqs <= kSplitRoundWorkgroups ? 0 : 1;
+    P.paired = split_single_blocks_fit(n16, P.hkv, num_seqs) ? 0 : 1;
     const int ntb = round_up(P.paired ? (n16 + 1) / 2 : n16);
     P.ntb_grid = ntb;
     const dim3 grid((unsigned)(ntb * P.hkv), 1u, (unsigned)num_seqs);
@@ -972,10 +982,14 @@ int launch_split(const Params& P0, int ss, int num_seqs, int max_query_len, hipS
     return finish_launch();
 }
 
-// Contexts (in keys) from which the key-split kernel beats the per-wave kernel (measured on
-// MI355X at GQA 6: 512 new tokens after 512 cached 42.8 vs 45.6 us, 512 tokens alone 28.0 vs
-// 24.4 us); below it the split kernel's per-block fixed costs dominate.
+// Contexts (in keys) from which the key-split kernel beats the per-wave kernel, measured on MI355X
+// at GQA 6.  With paired blocks: 1024 (512 new tokens after 512 cached 42.8 vs 45.6 us, 512
+// tokens alone 28.0 vs 24.4 us; 4 sequences of 512 32.0 vs 27.3 us).  With one block per
+// workgroup (the grid fits one round): 256 (512 tokens alone 17.4 vs 23.8 us, 1000 alone 24.7 vs
+// 42.5 us, 64 after 900 22.3 vs 42.3 us, 256 alone 13.6 vs 14.4 us, 128 alone 13.1 vs 9.8 us).
+// Below them the split kernel's per-block fixed costs dominate.
 constexpr int kSplitMinContext = 1024;
+constexpr int kSplitMinContextSingle = 256;
 
 // ctx_hint: the longest context when the host knows it (single sequence), else the longest query.
 int launch(const Params& P0, int num_seqs, int max_query_len, int ctx_hint, hipStream_t stream)
@@ -985,7 +999,10 @@ int launch(const Params& P0, int num_seqs, int max_query_len, int ctx_hint, hipS
     const int ss = split_shape_for(P0.gqa);
     if (g_shape >= kNumShapes) {
         if (g_shape - kNumShapes == ss) return launch_split(P0, ss, num_seqs, max_query_len, stream);
-    } else if (g_shape < 0 && ss >= 0 && ctx_hint >= kSplitMinContext) {
+    } else if (g_shape < 0 && ss >= 0 &&
+               (ctx_hint >= kSplitMinContext ||
+                (ctx_hint >= kSplitMinContextSingle &&
+                 split_single_blocks_fit((max_query_len + 15) / 16, P0.hkv, num_seqs)))) {
         return launch_split(P0, ss, num_seqs, max_query_len, stream);
     }
     Params P = P0;
