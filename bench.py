@@ -662,6 +662,9 @@ def main():
         legs["prefill_cfg3"] = bench_prefill([2048], [2048], pf_steps, max(2, args.warmup // 4))
         legs["prefill_cfg3_varlen_4x512"] = bench_prefill([512] * 4, [0] * 4, pf_steps,
                                                           max(2, args.warmup // 4), seed=1)
+        # a medium chunk: 1024 new tokens after 1024 cached (one token block per workgroup)
+        legs["prefill_1024_over_1024"] = bench_prefill([1024], [1024], pf_steps,
+                                                       max(2, args.warmup // 4), seed=2)
     if "cache" in legs_wanted:
         legs["cache_write_2048"] = bench_cache_write(2048, max(5, args.steps // 4), max(2, args.warmup // 4))
         legs["cache_write_8"] = bench_cache_write(8, args.steps, args.warmup)
