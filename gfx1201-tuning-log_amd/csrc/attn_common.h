@@ -65,4 +65,65 @@ __device__ __forceinline__ void v_fragments(const u32x2_t (&vr)[8], u32x4_t (&bf
     }
 }
 
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+// D += A . B^T over 128 k on the block-scaled MFMA with e4m3 A and B (both block scales 1.0):
+// lane (r, p) supplies row r's k 16p .. 16p+15 in bytes 0..15 and 64+16p .. +15 in bytes 16..31
+// of each operand; the products are exact and accumulate in fp32.
+__device__ __forceinline__ f32x4_t mfma_fp8_16x16x128(const v8i& a, const v8i& b, f32x4_t c)
+{
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// One query row's 32 bf16 values held by this lane (the 128-value row is spread over the four
+// lanes n, n + 16, n + 32, n + 48) -> e4m3 hi and lo parts with q * 2^e = hi + lo, where 2^e is
+// the row's scale: the largest |q| of the row times 2^e lies in [128, 256).  Returns 2^-e.
+// hi is q * 2^e rounded to 4 significant bits; the remainder lo is a multiple of the bf16 value's
+// last place below 2^-4 of it, exact in e4m3 whenever |q| >= 2^-9 of the row's largest |q| (the
+// subnormal range covers smaller values to 2^-10 of their place).  The products of the two MFMAs
+// with exact e4m3 K then sum to the bf16 path's S up to fp32 accumulation order.  sign_mask
+// (0x80808080 or 0) negates the row in e4m3 (exact).
+__device__ __forceinline__ float q_fp8_split(const u32x4_t (&qf)[4], uint32_t sign_mask, v8i& hi, v8i& lo)
+{
+    float amax = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            amax = fmaxf(amax, fabsf(__uint_as_float(qf[c][d] << 16)));
+            amax = fmaxf(amax, fabsf(__uint_as_float(qf[c][d] & 0xFFFF0000u)));
+        }
+    amax = max_xor16_32(amax);
+    // biased exponent of the scale 2^e = 2^(7 - floor(log2 amax)), kept where 2^-e is normal too
+    int be = 261 - (int)((__float_as_uint(amax) >> 23) & 0xFFu);
+    be = be < 1 ? 1 : (be > 253 ? 253 : be);
+    const float scale = __uint_as_float((uint32_t)be << 23);
+    const float inv = __uint_as_float((uint32_t)(254 - be) << 23);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {               // dword pair (2h, 2h + 1) of chunk c -> 4 values
+            float x[4];
+            x[0] = __uint_as_float(qf[c][2 * h] << 16) * scale;
+            x[1] = __uint_as_float(qf[c][2 * h] & 0xFFFF0000u) * scale;
+            x[2] = __uint_as_float(qf[c][2 * h + 1] << 16) * scale;
+            x[3] = __uint_as_float(qf[c][2 * h + 1] & 0xFFFF0000u) * scale;
+            uint32_t hw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+            hw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], (int)hw, true);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hw, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hw, true);
+            uint32_t lw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0] - h01[0], x[1] - h01[1], 0, false);
+            lw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2] - h23[0], x[3] - h23[1], (int)lw, true);
+            // chunk c holds d 16p + 8 (c & 1) + 4 h .. of the low half (c < 2) or the high half
+            const int slot = 4 * (c >> 1) + 2 * (c & 1) + h;
+            hw ^= sign_mask;
+            lw ^= sign_mask;
+            // opaque to the compiler, which would otherwise re-derive the parts inside the key loop
+            asm volatile("" : "+v"(hw), "+v"(lw));
+            hi[slot] = (int)hw;
+            lo[slot] = (int)lw;
+        }
+    return inv;
+}
+
 }  // namespace fp8kv

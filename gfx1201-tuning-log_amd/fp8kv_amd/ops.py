@@ -70,6 +70,14 @@ def h4mv(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor,
 # ------------------------------------------------------------------------------ decode attention
 
 _scratch_cache: dict = {}
+# Buffers replaced by a larger one stay alive for the life of the process: a graph captured while
+# one of them was current replays with its address, so freeing it would hand the graph's tickets
+# and records to whatever the allocator puts there next.
+_scratch_retired: list = []
+# First allocation per device.  The split planner's plans need at most
+# counters (256 KiB) + (2 * 256 - 1) records of 16 * 130 floats (4.25 MB at GQA 16), so a buffer of
+# this size never grows for planned splits; only explicit larger split counts grow it.
+DECODE_SCRATCH_MIN_BYTES = 8 << 20
 
 
 def decode_num_splits(num_seqs: int, num_kv_heads: int, max_seq_len: int) -> int:
@@ -85,8 +93,10 @@ def decode_scratch_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, num
 def decode_scratch(nbytes: int, device, allow_alloc: bool = True) -> torch.Tensor | None:
     """Zero-filled scratch of at least ``nbytes`` for ``device``, reused across calls.
 
-    The kernel leaves the buffer ready for the next call, so it is zeroed only when allocated.
-    With ``allow_alloc=False`` (e.g. during graph capture) a too-small cache returns None.
+    The kernel leaves its tickets zero again after every completed call, so it is zeroed only
+    when allocated.  The first buffer has DECODE_SCRATCH_MIN_BYTES; a larger request replaces it, and
+    the replaced buffer is kept alive (graphs captured with it keep replaying into it).  With
+    ``allow_alloc=False`` (e.g. during graph capture) a too-small cache returns None.
     """
     if nbytes <= 0:
         return None
@@ -99,10 +109,21 @@ def decode_scratch(nbytes: int, device, allow_alloc: bool = True) -> torch.Tenso
     if buf is None or buf.numel() < nbytes:
         if not allow_alloc:
             return None
-        size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
+        size = max(nbytes, 2 * buf.numel() if buf is not None else DECODE_SCRATCH_MIN_BYTES)
+        if buf is not None:
+            _scratch_retired.append(buf)
         buf = torch.zeros(size, dtype=torch.uint8, device=dev)
         _scratch_cache[key] = buf
     return buf
+
+
+def decode_scratch_reset(scratch: torch.Tensor) -> None:
+    """Zero a decode scratch buffer on the current stream with the library's fill kernel
+    (fp8kv_decode_scratch_reset): for a buffer whose last call did not complete."""
+    _require(scratch.is_cuda and scratch.is_contiguous(), "scratch must be a contiguous device tensor")
+    st = _lib.load().fp8kv_decode_scratch_reset(scratch.data_ptr(), scratch.numel() * scratch.element_size(),
+                                                _stream_ptr(scratch))
+    _lib.check("fp8kv_decode_scratch_reset", st)
 
 
 def _scale_tensor(x, device) -> torch.Tensor:

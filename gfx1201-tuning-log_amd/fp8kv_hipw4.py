@@ -6,14 +6,16 @@ down when ``radiance_mxfp4.WPERM`` is set (:50-52), steals the current CUDA body
 ``radiance::mxfp4_linear`` - ``_backend_fns["cuda"]`` or ``_init_fn`` (:54); calling the module
 attribute instead would recurse - and re-registers the op's CUDA implementation (:62).  The new
 implementation takes the fast path when the reference's gate holds (:70-76): x is a contiguous
-2-D bf16 tensor with 1 <= M <= FP8KV_HIPW4_MAX_M (default 4; the kernel accepts up to 16),
+2-D bf16 tensor with 1 <= M <= FP8KV_HIPW4_MAX_M (default 4; clamped to the kernel's 16),
 K % 32 == 0, N >= 8, weight_scale has K / 32 rows and the weight pointer is 16-byte aligned.  It
 then repacks weight_scale [K/32, N] -> [N, K/32] once per tensor with the library's
 h4mv_repack_scales (cached by data pointer and shape, cache cleared above 512 entries, never
 during graph capture: :32-43) and calls
 ``h4mv_launch`` of libfp8kv_amd.so through ctypes with the reference's exact binding (:21-23,
-81-83), returning a fresh bf16 [M, N] tensor (bias is applied outside, :9-10).  Anything else,
-or any exception, runs the stolen body (:91-94).
+81-83), returning a fresh bf16 [M, N] tensor (bias is applied outside, :9-10).  The void
+launcher records its status; the hook reads it (fp8kv_last_status) after each launch, so a
+rejected call falls back instead of returning an unwritten tensor.  Anything else, or any
+exception, runs the stolen body (:91-94).
 
 With FP8KV_HIPW4_GEMM=1 as well, larger batches (M > FP8KV_HIPW4_MAX_M, the prefill-sized
 linears the reference leaves to its fork's W4A8 GEMM) take the library's own GEMM path when its
@@ -56,6 +58,32 @@ def load_launcher(path: str | None = None):
     lib.h4mv_launch.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
     lib.h4mv_launch.restype = None
     return lib.h4mv_launch
+
+
+def load_status(path: str | None = None):
+    """ctypes handle of ``fp8kv_last_status``: the status the last ``h4mv_launch`` on this host
+    thread recorded (the reference's void entry point cannot return it)."""
+    import torch  # noqa: F401
+    if path is None:
+        from fp8kv_amd import _lib
+        path = _lib.lib_path()
+    lib = ctypes.CDLL(path)
+    lib.fp8kv_last_status.argtypes = []
+    lib.fp8kv_last_status.restype = ctypes.c_int
+    return lib.fp8kv_last_status
+
+
+# The matvec kernels take 1 <= M <= 16; h4mv_launch rejects anything larger and launches nothing.
+KERNEL_MAX_M = 16
+
+
+def clamp_max_m(value: str) -> int:
+    """FP8KV_HIPW4_MAX_M as an int in [1, KERNEL_MAX_M] (logged when clamped)."""
+    m = int(value)
+    c = min(max(m, 1), KERNEL_MAX_M)
+    if c != m:
+        _log(f"FP8KV_HIPW4_MAX_M={m} clamped to {c} (the matvec takes 1 <= M <= {KERNEL_MAX_M})")
+    return c
 
 
 def load_gemm(path: str | None = None):
@@ -141,9 +169,12 @@ def gemm_path_ok(x, weight, weight_scale, maxm: int, torch) -> bool:
             and weight.is_contiguous() and weight.data_ptr() % 16 == 0)
 
 
-def make_patched(body, launch, repack, maxm: int, torch, stream_ptr, gemm=None):
+def make_patched(body, launch, repack, maxm: int, torch, stream_ptr, gemm=None, last_status=None):
     """The replacement op body: fast path through ``launch`` (h4mv_launch), the opt-in GEMM path
-    through ``gemm`` for larger batches, else ``body``."""
+    through ``gemm`` for larger batches, else ``body``.  ``last_status()`` (fp8kv_last_status)
+    is read after every launch: a call the library rejected wrote nothing, so ``body`` runs
+    instead.  ``maxm`` is clamped to the kernel's limit."""
+    maxm = min(max(int(maxm), 1), KERNEL_MAX_M)
 
     def _patched(x, weight, weight_scale, wref):
         try:
@@ -158,6 +189,9 @@ def make_patched(body, launch, repack, maxm: int, torch, stream_ptr, gemm=None):
                     out = torch.empty((M, N), device=x.device, dtype=torch.bfloat16)
                     launch(weight.data_ptr(), st.data_ptr(), x.data_ptr(), out.data_ptr(), N, K, M,
                            ctypes.c_void_p(stream_ptr()))
+                    rc = last_status() if last_status is not None else 0
+                    if rc != 0:
+                        raise RuntimeError(f"h4mv_launch status {rc} (N={N} K={K} M={M})")
                     STATS["fast"] += 1
                     if not STATS["logged"]:
                         STATS["logged"] = True
@@ -190,7 +224,7 @@ def register(patched, torch):
     torch.library.impl("radiance::mxfp4_linear", "CUDA")(patched)
 
 
-def _poll(launch, maxm, tries: int = 1500, delay: float = 0.2, gemm=None):
+def _poll(launch, maxm, tries: int = 1500, delay: float = 0.2, gemm=None, last_status=None):
     import torch
     body = None
     for _ in range(tries):
@@ -208,7 +242,8 @@ def _poll(launch, maxm, tries: int = 1500, delay: float = 0.2, gemm=None):
         return
     repack = ScaleRepack(torch.cuda.is_current_stream_capturing)
     patched = make_patched(body, launch, repack, maxm, torch,
-                           lambda: torch.cuda.current_stream().cuda_stream, gemm=gemm)
+                           lambda: torch.cuda.current_stream().cuda_stream, gemm=gemm,
+                           last_status=last_status)
     register(patched, torch)
     _STATE.update(body=body, patched=patched)
     _log("op impl overridden")
@@ -219,17 +254,19 @@ def _install() -> bool:
         return False
     try:
         launch = load_launcher()
+        last_status = load_status()
     except Exception as e:
         _log(f"lib load fail: {e}")
         return False
-    maxm = int(os.environ.get("FP8KV_HIPW4_MAX_M", "4"))
+    maxm = clamp_max_m(os.environ.get("FP8KV_HIPW4_MAX_M", "4"))
     gemm = None
     if os.environ.get("FP8KV_HIPW4_GEMM", "0") == "1":
         try:
             gemm = load_gemm()
         except Exception as e:
             _log(f"gemm path unavailable: {e}")
-    threading.Thread(target=_poll, args=(launch, maxm), kwargs={"gemm": gemm}, daemon=True).start()
+    threading.Thread(target=_poll, args=(launch, maxm), kwargs={"gemm": gemm, "last_status": last_status},
+                     daemon=True).start()
     _STATE["installed"] = True
     _log("installed")
     return True

@@ -9,7 +9,9 @@ engine's KV tensor as separate K and V fp8 caches (fp8kv_override.py:82-85) and 
 runs.  As in the reference, decode-path errors propagate (fp8kv_override.py:102-106).
 
 Differences, all on the host side:
-  * the split count is planned from ``attn_metadata.max_seq_len`` (reference: fixed 8);
+  * the split count is planned from ``attn_metadata.max_seq_len`` (reference: fixed 8); while a
+    graph is captured it is planned from the batch shape alone, so the captured count suits every
+    context the graph replays;
   * the scratch buffer is the library's (zeroed once, reused); it is never allocated while the
     stream is being captured into a graph - a call that would need a bigger one during capture
     falls back to the original forward instead;
@@ -30,6 +32,9 @@ if _PKG not in sys.path:
     sys.path.insert(0, _PKG)
 
 TAG = "[fp8kv-override]"
+# Context length the split planner is given while a graph is being captured: long enough that the
+# plan depends only on the batch shape (sequences x kv heads).
+CAPTURE_PLAN_SEQ_LEN = 1 << 30
 COUNTERS = {"impl_forward": 0, "fallback": 0}
 _STATE = {"installed": False, "orig": None, "diag_done": False, "engaged": False}
 
@@ -93,9 +98,14 @@ def make_forward(orig, fp8_per_tensor, ops, is_capturing):
         NS = attn_metadata.query_start_loc.shape[0] - 1
         HKV = self.num_kv_heads
         HQ = query.shape[1]
-        nsplit = ops.decode_num_splits(NS, HKV, int(attn_metadata.max_seq_len))
+        capturing = is_capturing()
+        # Under capture the split count is baked into the graph and replayed for every later
+        # batch of this size, whatever its contexts: plan it from the batch shape alone (the
+        # planner's longest-context cap lifted), not from the capture's dummy max_seq_len.
+        plan_len = CAPTURE_PLAN_SEQ_LEN if capturing else int(attn_metadata.max_seq_len)
+        nsplit = ops.decode_num_splits(NS, HKV, plan_len)
         need = ops.decode_scratch_bytes(NS, HQ, HKV, nsplit, hs)
-        scratch = ops.decode_scratch(need, query.device, allow_alloc=not is_capturing())
+        scratch = ops.decode_scratch(need, query.device, allow_alloc=not capturing)
         if need > 0 and scratch is None:
             COUNTERS["fallback"] += 1
             _log(f"scratch of {need} bytes not allocated before graph capture; stock path")

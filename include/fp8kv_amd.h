@@ -89,9 +89,13 @@ int h4mv_repack_scales(const void* scale_kn, void* scale_nk, int N, int K, void*
  *   sizes), 1 <= num_splits <= 256.
  *   A sequence with seq_len 0 gets zeros.
  *
- * Scratch: fp8kv_decode_scratch_bytes() bytes (0 when num_splits == 1), 256-byte aligned.  It must be
- * zero-filled once after allocation; every call leaves it ready for the next one (its per-sequence
- * tickets return to zero).  Calls sharing one scratch buffer must not overlap in time.
+ * Scratch: fp8kv_decode_scratch_bytes() bytes (0 when num_splits == 1), 256-byte aligned: a fixed
+ * 256 KiB region of per-pair merge tickets, then the split records.  It must be zero-filled once
+ * after allocation (torch.zeros, or fp8kv_decode_scratch_reset); every completed call leaves the
+ * tickets zero again, and the records need no initial state.  Calls sharing one scratch buffer
+ * must not overlap in time.  A call that did not complete (a faulted or aborted launch) can leave
+ * tickets non-zero, and later calls then skip or misplace the merge: reset the buffer before
+ * reusing it.
  *
  * Replaces: vllm-fp8kv/fp8kv_v3.py:116-139, run(q, k_cache, v_cache, out, qsl, slens, bt, kscale,
  * vscale, sm_scale, TILE, warps, stages, nsplit, scratch), which launches the Triton kernels
@@ -120,6 +124,14 @@ int fp8kv_decode_num_splits(int num_seqs, int num_kv_heads, int max_seq_len);
  * vllm-fp8kv/fp8kv_v3.py:121-124 and vllm-fp8kv/fp8kv_override.py:87-96. */
 size_t fp8kv_decode_scratch_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
                                   int num_splits);
+
+/* Zero-fills `scratch_bytes` bytes of a decode scratch buffer (256-byte aligned) with a kernel on
+ * `stream` (not a memset, so it may be captured in a graph): the state fp8kv_decode_attn expects.
+ * For a fresh buffer, and after a call that did not complete.  No counterpart in the reference: its
+ * Triton split kernel overwrites every partial before the reduce kernel reads it, so its scratch
+ * starts as torch.empty (vllm-fp8kv/fp8kv_v3.py:119-122); this library's one-launch merge keeps
+ * its tickets in the scratch and needs them zero between calls. */
+int fp8kv_decode_scratch_reset(void* scratch, size_t scratch_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Paged fp8-e4m3 KV causal prefill attention, one sequence.

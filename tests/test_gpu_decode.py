@@ -206,3 +206,72 @@ def test_every_launch_variant(variant):
             _check(c, num_splits=splits)
     finally:
         lib.fp8kv_decode_tune(-1, 0)
+
+
+def test_graph_replay_after_scratch_grows():
+    """A graph captured with the cached scratch keeps replaying correctly after an eager call
+    needs a larger buffer (the old one is kept alive, tickets and records zero)."""
+    c = workloads.decode_case([2048, 4000], seed=16)
+    d = workloads.to_device(c, DEV)
+    ks = torch.tensor([c["k_scale"]], device=DEV)
+    vs = torch.tensor([c["v_scale"]], device=DEV)
+    out = torch.zeros_like(d["q"])
+    args = (d["q"], d["k_cache"], d["v_cache"], out, d["qsl"], d["seq_lens"], d["block_table"], ks, vs,
+            c["sm_scale"])
+    ops.decode_attention(*args, num_splits=16)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            ops.decode_attention(*args, num_splits=16)
+    torch.cuda.current_stream().wait_stream(s)
+    before = ops._scratch_cache[("cuda", torch.cuda.current_device())]
+    # 64 sequences x 4 kv heads x 64 splits of GQA-6 records: about 51 MB, beyond the cached buffer
+    big = workloads.decode_case([300] * 64, seed=17)
+    ref_big = _oracle(big)
+    torch.testing.assert_close(_rows(big, _run(big, num_splits=64)), ref_big, rtol=RTOL, atol=ATOL)
+    assert ops._scratch_cache[("cuda", torch.cuda.current_device())] is not before
+    for it in range(3):
+        d["q"].copy_(torch.randn(d["q"].shape, generator=torch.Generator().manual_seed(200 + it))
+                     .to(torch.bfloat16).to(DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        eager = torch.zeros_like(out)
+        ops.decode_attention(d["q"], d["k_cache"], d["v_cache"], eager, d["qsl"], d["seq_lens"],
+                             d["block_table"], ks, vs, c["sm_scale"], num_splits=16)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager), f"replay {it}"
+
+
+def test_scratch_reset_recovers_a_dirty_buffer():
+    """Non-zero tickets (as a launch that never completed would leave) misplace the merge;
+    fp8kv_decode_scratch_reset restores the zero state and the next calls are exact."""
+    c = workloads.decode_case([3000, 1500, 4096], seed=18)
+    ref = _oracle(c)
+    d = workloads.to_device(c, DEV)
+    ks = torch.tensor([c["k_scale"]], device=DEV)
+    vs = torch.tensor([c["v_scale"]], device=DEV)
+    need = ops.decode_scratch_bytes(3, 24, 4, 8)
+    scratch = torch.full((need + 100,), 0x5A, dtype=torch.uint8, device=DEV)
+    ops.decode_scratch_reset(scratch)
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(scratch)) == 0
+    for _ in range(2):
+        out = torch.zeros_like(d["q"])
+        ops.decode_attention(d["q"], d["k_cache"], d["v_cache"], out, d["qsl"], d["seq_lens"],
+                             d["block_table"], ks, vs, c["sm_scale"], num_splits=8, scratch=scratch)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(_rows(c, out), ref, rtol=RTOL, atol=ATOL)
+        assert int(torch.count_nonzero(scratch[:256 << 10])) == 0   # every call leaves the tickets zero
+
+
+def test_merge_is_independent_of_the_merging_split():
+    """The merging workgroup is whichever split of a pair finishes last, which varies from call to
+    call; the merge runs in split order, so 20 calls agree bit for bit."""
+    c = workloads.decode_case([4096] * 8, pool_blocks=5060, seed=19, layout="engine")
+    a = _run(c, num_splits=8).clone()
+    for _ in range(20):
+        assert torch.equal(_run(c, num_splits=8), a)

@@ -206,6 +206,41 @@ def test_decode_no_scratch_during_capture_falls_back(monkeypatch):
     assert calls == ["stock"] and rec.calls == []
 
 
+def test_decode_capture_plans_from_batch_shape(monkeypatch):
+    """While capturing, the split count (baked into the graph) ignores the capture's max_seq_len:
+    it is the plan for the batch shape with no context cap, the same for short and long dummies."""
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    cls, calls = _fake_vllm(monkeypatch)
+    rec = Recorder()
+    from fp8kv_amd import ops
+    monkeypatch.setattr(ops, "decode_attention", rec("decode"))
+    monkeypatch.setattr(ops, "_scratch_cache", {("cpu", 0): torch.zeros(ops.DECODE_SCRATCH_MIN_BYTES,
+                                                                          dtype=torch.uint8)})
+    ov = _fresh(monkeypatch, "fp8kv_override")
+    for ctx in ((1, 1, 1), (250, 250, 250)):
+        md, layer, kv, q, out = _batch(ctx=ctx)
+        cls.forward(_impl(cls), layer, q, None, None, kv, md, out)
+    assert calls == [] and len(rec.calls) == 2
+    want = ops.decode_num_splits(3, 4, ov.CAPTURE_PLAN_SEQ_LEN)
+    assert want > 1 and [kw["num_splits"] for _, _, kw in rec.calls] == [want, want]
+    assert ops.decode_num_splits(3, 4, 1) == 1                 # what the dummy context would give
+
+
+def test_decode_scratch_never_frees_a_replaced_buffer(monkeypatch):
+    """A larger request replaces the cached scratch but keeps the old buffer alive (graphs captured
+    with it replay into it)."""
+    from fp8kv_amd import ops
+    monkeypatch.setattr(ops, "_scratch_cache", {})
+    monkeypatch.setattr(ops, "_scratch_retired", [])
+    a = ops.decode_scratch(1000, "cpu")
+    assert a.numel() == ops.DECODE_SCRATCH_MIN_BYTES and int(a.sum()) == 0
+    assert ops.decode_scratch(5000, "cpu") is a
+    b = ops.decode_scratch(ops.DECODE_SCRATCH_MIN_BYTES + 1, "cpu")
+    assert b is not a and b.numel() >= ops.DECODE_SCRATCH_MIN_BYTES + 1
+    assert ops._scratch_retired == [a]
+    assert ops.decode_scratch(10, "cpu", allow_alloc=False) is b
+
+
 def test_decode_errors_propagate(monkeypatch, no_capture):
     """fp8kv_override.py:102-106 does not catch kernel errors; neither does this hook."""
     cls, calls = _fake_vllm(monkeypatch)
@@ -435,6 +470,50 @@ def test_hipw4_exception_falls_back(monkeypatch):
                              4, torch, lambda: 0)
     x, w, s = _lin()
     assert patched(x, w, s, None) == "body"
+
+
+def test_hipw4_rejected_launch_falls_back(monkeypatch):
+    """The void h4mv_launch only records a rejection; the hook reads that status and runs the
+    stolen body instead of returning its unwritten output tensor."""
+    h = _hipw4(monkeypatch)
+    launch = FakeLaunch()
+    status = {"rc": 2}
+    body_calls = []
+    patched = h.make_patched(lambda *a: body_calls.append(a) or "body", launch,
+                             h.ScaleRepack(lambda: False, transpose=lambda t: t.t().contiguous()),
+                             4, torch, lambda: 0, last_status=lambda: status["rc"])
+    x, w, s = _lin(M=3, N=64, K=256)
+    assert patched(x, w, s, None) == "body" and len(launch.calls) == 1 and len(body_calls) == 1
+    status["rc"] = 0
+    out = patched(x, w, s, None)
+    assert torch.is_tensor(out) and out.shape == (3, 64) and len(body_calls) == 1
+
+
+@pytest.mark.parametrize("env,expect", [("4", 4), ("16", 16), ("17", 16), ("64", 16), ("0", 1), ("-3", 1)])
+def test_hipw4_max_m_is_clamped(monkeypatch, capsys, env, expect):
+    h = _hipw4(monkeypatch)
+    assert h.clamp_max_m(env) == expect
+    assert ("clamped" in capsys.readouterr().err) == (int(env) != expect)
+
+
+def test_hipw4_batches_above_kernel_limit_never_launch(monkeypatch):
+    """Even with a configured limit above the kernel's 16 rows, M = 17 runs the stolen body."""
+    h = _hipw4(monkeypatch)
+    launch = FakeLaunch()
+    patched = h.make_patched(lambda *a: "body", launch,
+                             h.ScaleRepack(lambda: False, transpose=lambda t: t.t().contiguous()),
+                             64, torch, lambda: 0, last_status=lambda: 0)
+    x, w, s = _lin(M=17, N=64, K=256)
+    assert patched(x, w, s, None) == "body" and launch.calls == []
+    x, w, s = _lin(M=16, N=64, K=256)
+    assert torch.is_tensor(patched(x, w, s, None)) and len(launch.calls) == 1
+
+
+def test_hipw4_status_binding():
+    import ctypes
+    import fp8kv_hipw4 as h
+    fn = h.load_status()
+    assert fn.argtypes == [] and fn.restype is ctypes.c_int and isinstance(fn(), int)
 
 
 def test_hipw4_repack_cache_limit(monkeypatch):
