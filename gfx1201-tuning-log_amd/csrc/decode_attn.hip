@@ -39,6 +39,8 @@
 #include "fp8kv_diag.h"
 #include "attn_common.h"
 
+#include <mutex>
+
 namespace fp8kv {
 namespace decode_detail {
 
@@ -750,11 +752,11 @@ int decode_setup(Params& P, const void* q, int64_t q_row_stride, const void* k_c
     return FP8KV_OK;
 }
 
-void use_scratch(Params& P, void* scratch, size_t need)
+void use_scratch(Params& P, void* buf, size_t need)
 {
     if (need == 0) return;
-    P.counters = static_cast<uint32_t*>(scratch);
-    P.part = reinterpret_cast<float*>(static_cast<unsigned char*>(scratch) + counters_bytes());
+    P.counters = static_cast<uint32_t*>(buf);
+    P.part = reinterpret_cast<float*>(static_cast<unsigned char*>(buf) + counters_bytes());
 }
 
 int decode_launch(const Params& P, int num_seqs, hipStream_t st)
@@ -771,6 +773,49 @@ int decode_launch(const Params& P, int num_seqs, hipStream_t st)
         default: launch_kernel(decode_kernel<8, 2, 2, true>, grid, dim3(8 * 64), 0, st, P.seq_lens, P.qsl, P); break;
     }
     return finish_launch();
+}
+
+}  // namespace decode_detail
+}  // namespace fp8kv
+
+// Scratch of fp8kv_decode_attn_noalloc: tickets then split records, one copy per GPU the library
+// runs on, held until the process ends.  In host code this name is a host-side stand-in, not a
+// device address: the device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace fp8kv {
+namespace decode_detail {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device.  The first call on a device resolves it
+// and zeroes its ticket region with a kernel on `st` (the records need no initial state).
+int noalloc_scratch(hipStream_t st, void** out)
+{
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        g_last_hip_error = (int)e;
+        return FP8KV_ERR_LAUNCH;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return FP8KV_ERR_ARG;
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (g_noalloc_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr) {
+            g_last_hip_error = (int)e;
+            return FP8KV_ERR_LAUNCH;
+        }
+        const int rc = launch_scratch_zero(ptr, counters_bytes(), st);
+        if (rc != FP8KV_OK) return rc;
+        g_noalloc_ptr[dev] = ptr;
+    }
+    *out = g_noalloc_ptr[dev];
+    return FP8KV_OK;
 }
 
 }  // namespace decode_detail
@@ -793,10 +838,10 @@ extern "C" size_t fp8kv_decode_scratch_bytes(int num_seqs, int num_q_heads, int 
     return scratch_bytes(num_seqs, num_q_heads, num_kv_heads, num_splits);
 }
 
-extern "C" int fp8kv_decode_scratch_reset(void* scratch, size_t scratch_bytes_given, void* stream)
+extern "C" int fp8kv_decode_scratch_reset(void* scratch_buf, size_t scratch_bytes_given, void* stream)
 {
-    if (!scratch || !aligned(scratch, 256)) return FP8KV_ERR_ARG;
-    return launch_scratch_zero(scratch, scratch_bytes_given, reinterpret_cast<hipStream_t>(stream));
+    if (!scratch_buf || !aligned(scratch_buf, 256)) return FP8KV_ERR_ARG;
+    return launch_scratch_zero(scratch_buf, scratch_bytes_given, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
@@ -808,7 +853,7 @@ extern "C" int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
                                  const int32_t* block_table, int64_t bt_stride,
                                  const float* k_scale, const float* v_scale, float sm_scale,
                                  int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
-                                 int block_size, int num_splits, void* scratch,
+                                 int block_size, int num_splits, void* scratch_buf,
                                  size_t scratch_bytes_given, void* stream)
 {
     Params P;
@@ -818,10 +863,39 @@ extern "C" int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
                                 v_scale, sm_scale, num_seqs, num_q_heads, num_kv_heads, head_size, block_size,
                                 num_splits, need);
     if (rc != FP8KV_OK) return rc;
-    if (need > 0 && (!scratch || scratch_bytes_given < need || !aligned(scratch, 256)))
+    if (need > 0 && (!scratch_buf || scratch_bytes_given < need || !aligned(scratch_buf, 256)))
         return FP8KV_ERR_SCRATCH;
-    use_scratch(P, scratch, need);
+    use_scratch(P, scratch_buf, need);
     return decode_launch(P, num_seqs, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int fp8kv_decode_attn_noalloc(const void* q, int64_t q_row_stride,
+                                         const void* k_cache, const void* v_cache,
+                                         int64_t sk0, int64_t sk1, int64_t sk2,
+                                         int64_t sv0, int64_t sv1, int64_t sv2,
+                                         void* out, int64_t out_row_stride,
+                                         const int32_t* query_start_loc, const int32_t* seq_lens,
+                                         const int32_t* block_table, int64_t bt_stride,
+                                         const float* k_scale, const float* v_scale, float sm_scale,
+                                         int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
+                                         int block_size, int num_splits, void* stream)
+{
+    Params P;
+    size_t need = 0;
+    int rc = decode_setup(P, q, q_row_stride, k_cache, v_cache, sk0, sk1, sk2, sv0, sv1, sv2, out,
+                          out_row_stride, query_start_loc, seq_lens, block_table, bt_stride, k_scale,
+                          v_scale, sm_scale, num_seqs, num_q_heads, num_kv_heads, head_size, block_size,
+                          num_splits, need);
+    if (rc != FP8KV_OK) return rc;
+    if (need > kNoAllocScratchBytes) return FP8KV_ERR_SCRATCH;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    void* ptr = nullptr;
+    if (need > 0) {
+        rc = noalloc_scratch(st, &ptr);
+        if (rc != FP8KV_OK) return rc;
+    }
+    use_scratch(P, ptr, need);
+    return decode_launch(P, num_seqs, st);
 }
 
 extern "C" void fp8kv_decode_tune(int variant, int target_wgs)

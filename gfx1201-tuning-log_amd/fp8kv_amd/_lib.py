@@ -32,6 +32,8 @@ SIGNATURES: dict[str, tuple] = {
     "fp8kv_decode_num_splits": (_c_i, [_c_i] * 3),
     "fp8kv_decode_scratch_bytes": (_c_sz, [_c_i] * 5),
     "fp8kv_decode_scratch_reset": (_c_i, [_c_vp, _c_sz, _c_vp]),
+    "fp8kv_decode_attn_noalloc": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_i64] * 6 + [_c_vp, _c_i64]
+                                  + [_c_vp] * 3 + [_c_i64] + [_c_vp] * 2 + [_c_f] + [_c_i] * 6 + [_c_vp]),
     "fp8kv_decode_attn": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_i64] * 6 + [_c_vp, _c_i64]
                           + [_c_vp] * 3 + [_c_i64] + [_c_vp] * 2 + [_c_f] + [_c_i] * 6
                           + [_c_vp, _c_sz, _c_vp]),

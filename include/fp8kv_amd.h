@@ -114,6 +114,28 @@ int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
                       int block_size, int num_splits, void* scratch, size_t scratch_bytes,
                       void* stream);
 
+/* fp8kv_decode_attn without a scratch argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).  No
+ * counterpart in the reference.  The tickets and split records live in a file-scope device array
+ * of 8 MiB inside the library, one copy per GPU, held until the process ends; nothing is allocated
+ * or freed.  Same arguments, semantics and results as fp8kv_decode_attn (bit for bit) except that
+ * a call needing more than 8 MiB of scratch (fp8kv_decode_scratch_bytes) returns
+ * FP8KV_ERR_SCRATCH and launches nothing; every split count the library plans fits at any GQA.
+ * The first call on a device also launches a small kernel on `stream` that zeroes the array's
+ * ticket region (if that call is captured, the kernel is part of the graph).  Every call on one
+ * GPU shares that GPU's array: calls that overlap in time on one GPU (different streams, or
+ * graphs replayed concurrently) race and must be serialised by the caller. */
+int fp8kv_decode_attn_noalloc(const void* q, int64_t q_row_stride,
+                              const void* k_cache, const void* v_cache,
+                              int64_t sk0, int64_t sk1, int64_t sk2,
+                              int64_t sv0, int64_t sv1, int64_t sv2,
+                              void* out, int64_t out_row_stride,
+                              const int32_t* query_start_loc, const int32_t* seq_lens,
+                              const int32_t* block_table, int64_t bt_stride,
+                              const float* k_scale, const float* v_scale, float sm_scale,
+                              int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
+                              int block_size, int num_splits, void* stream);
+
 /* Split count the library would choose for a batch whose longest context is max_seq_len
  * (replaces the fixed NSPLIT = 8 of vllm-fp8kv/fp8kv_override.py:43).  Any value in [1, 256]
  * gives the same result up to rounding; this one fills the GPU. */
