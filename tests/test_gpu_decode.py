@@ -275,3 +275,18 @@ def test_merge_is_independent_of_the_merging_split():
     a = _run(c, num_splits=8).clone()
     for _ in range(20):
         assert torch.equal(_run(c, num_splits=8), a)
+
+
+def test_bf16_caches_are_rejected_not_misread():
+    """The reference's run() also takes bf16 caches (K_FP8 = False, vllm-fp8kv/fp8kv_v3.py:61-66);
+    this build reads e4m3 bytes only and refuses them before launching anything."""
+    import fp8kv_v3
+    c = workloads.decode_case([64, 100], seed=20)
+    d = workloads.to_device(c, DEV)
+    kb = d["k_cache"].view(torch.uint8).to(torch.bfloat16)
+    vb = d["v_cache"].view(torch.uint8).to(torch.bfloat16)
+    out = torch.full_like(d["q"], 5.0)
+    with pytest.raises(ValueError, match="float8_e4m3fn"):
+        fp8kv_v3.run(d["q"], kb, vb, out, d["qsl"], d["seq_lens"], d["block_table"], 1.0, 1.0, c["sm_scale"])
+    torch.cuda.synchronize()
+    assert torch.all(out == 5.0)

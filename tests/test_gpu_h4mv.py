@@ -104,7 +104,7 @@ def test_baseline_config1(M):
 
 @pytest.mark.parametrize("N,K,M", [
     (1, 32, 1), (8, 32, 3), (17, 96, 2), (100, 160, 7), (4096, 3584, 8), (3584, 3072, 8),
-    (3584, 18944, 1), (37888, 3584, 8), (33, 4096, 16), (1000, 4128, 5),
+    (3584, 18944, 1), (3584, 18944, 8), (37888, 3584, 8), (33, 4096, 16), (1000, 4128, 5),
 ])
 def test_shapes(N, K, M):
     case = workloads.w4_case(N=N, K=K, M=M, seed=N + K + M)
