@@ -437,6 +437,75 @@ def bench_copy(steps: int, warmup: int, nbytes: int = 256 << 20):
     return r
 
 
+LM_VOCAB, LM_HIDDEN = 128167, 3584
+
+
+def lm_head_bytes(N: int, K: int, M: int) -> int:
+    """Algorithmic bytes of the draft lm_head matvec: codes, scales, x, fp32 logits."""
+    return N * K // 2 + N * K // 32 + 2 * M * K + 4 * M * N
+
+
+def bench_lm_head(M: int, k: int, steps: int, warmup: int):
+    """h4mv_topk on the reference model's lm_head shape (vocab 128167 x hidden 3584): the MXFP4
+    matvec into fp32 logits (timed per launch, the roofline kernel) and the whole chain with the
+    two top-k kernels (wall time per call), over rotated weight sets."""
+    import torch
+    from fp8kv_amd import ops
+    dev = torch.device("cuda")
+    N, K = LM_VOCAB, LM_HIDDEN
+    per_set = N * K // 2 + N * K // 32
+    n_sets = max(3, -(-ROTATE_BYTES // per_set))
+    g = torch.Generator(device=dev).manual_seed(4321 + M)
+    Ws = [torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=dev, generator=g) for _ in range(n_sets)]
+    Ss = [torch.randint(119, 124, (N, K // 32), dtype=torch.uint8, device=dev, generator=g) for _ in range(n_sets)]
+    X = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    from fp8kv_amd import _lib
+    lib = _lib.load()
+    ws = torch.empty(int(lib.h4mv_topk_workspace_bytes(N, M, k)), dtype=torch.uint8, device=dev)
+    vals = torch.empty((M, k), dtype=torch.float32, device=dev)
+    idx = torch.empty((M, k), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch(i):
+        # the C ABI directly, outputs and workspace preallocated: the host cost per call stays
+        # below the GPU time, so us_step measures the three kernels back to back
+        _lib.check("h4mv_topk", lib.h4mv_topk(Ws[i].data_ptr(), Ss[i].data_ptr(), X.data_ptr(), N, K, M, k,
+                                               vals.data_ptr(), idx.data_ptr(), ws.data_ptr(), ws.numel(),
+                                               stream))
+
+    wall, per = time_launches(launch, n_sets, steps, warmup)
+    del Ws, Ss
+    torch.cuda.empty_cache()
+    r = _summary(wall, per, lm_head_bytes(N, K, M))
+    r.update({"rotation_sets": n_sets, "k": k, "us_chain_step": r["us_step"],
+              "note": "us_kernel: the matvec into fp32 logits; us_step: matvec + 2 top-k kernels"})
+    return r
+
+
+def bench_stream_read(nbytes: int, steps: int, warmup: int):
+    """fp8kv_stream_read of nbytes over rotated buffers (> 512 MB): what one read-only launch of
+    that size reaches on this box."""
+    import torch
+    from fp8kv_amd import _lib
+    dev = torch.device("cuda")
+    nbytes = nbytes // 16 * 16
+    n_sets = max(4, -(-2 * (256 << 20) // nbytes) + 1)
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(n_sets)]
+    sink = torch.empty(4096, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+
+    def launch(i):
+        _lib.check("fp8kv_stream_read", lib.fp8kv_stream_read(bufs[i].data_ptr(), nbytes, sink.data_ptr(),
+                                                                torch.cuda.current_stream().cuda_stream))
+
+    wall, per = time_launches(launch, n_sets, steps, warmup)
+    del bufs
+    torch.cuda.empty_cache()
+    r = _summary(wall, per, nbytes)
+    r["rotation_sets"] = n_sets
+    return r
+
+
 def prefill_flops(qlens, q0s, HQ: int, D: int) -> int:
     """Algorithmic FLOPs of causal prefill: 4 D HQ per visible (query, key) pair."""
     pairs = sum(sum(q0 + i + 1 for i in range(n)) for n, q0 in zip(qlens, q0s))
@@ -629,8 +698,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--legs", default="w4,decode,prefill,cache,epi,gemm,stack,copy",
-                    help="comma list of legs to run (w4, decode, prefill, cache, epi, gemm, stack, copy)")
+    ap.add_argument("--legs", default="w4,decode,prefill,cache,epi,gemm,stack,lmhead,stream,copy",
+                    help="comma list of legs to run (w4, decode, prefill, cache, epi, gemm, stack, lmhead, "
+                         "stream, copy)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one GPU; "
@@ -677,6 +747,14 @@ def main():
         legs["w4a8_gemm_cfg4_linears_M2048"] = bench_w4a8_gemm(2048, max(5, args.steps // 4), max(2, args.warmup // 4))
     if "stack" in legs_wanted:
         legs["stack_cfg4_28_layers_b8"] = bench_stack(max(3, args.steps // 20), max(2, args.warmup // 10))
+    if "lmhead" in legs_wanted:
+        legs["lm_head_topk_vocab128167_M1_k64"] = bench_lm_head(1, 64, max(10, args.steps // 4), max(2, args.warmup // 4))
+        legs["lm_head_topk_vocab128167_M8_k64"] = bench_lm_head(8, 64, max(10, args.steps // 4), max(2, args.warmup // 4))
+    if "stream" in legs_wanted:
+        # the byte counts of the headline legs: cfg1 M = 1 matvec and decode b8@4k
+        legs["stream_read_cfg1_bytes"] = bench_stream_read(w4_bytes(N, K, 1), args.steps, args.warmup)
+        legs["stream_read_b8_4k_bytes"] = bench_stream_read(decode_bytes([4096] * 8, 24, 4, 128, 16),
+                                                            args.steps, args.warmup)
     if "copy" in legs_wanted:
         legs["copy_256MiB"] = bench_copy(max(5, args.steps // 4), max(2, args.warmup // 4))
     cpu = None if (args.no_cpu_baseline or m1 is None) else cpu_baseline_w4(N, K)
@@ -711,6 +789,18 @@ def main():
         "cpu_legs": extra_cpu,
         "legs": legs,
     }
+    # What one read-only launch of the same byte count reaches on this box (fp8kv_stream_read):
+    # the practical single-launch ceiling beside the 8 TB/s peak.
+    ref_w4 = legs.get("stream_read_cfg1_bytes")
+    ref_dec = legs.get("stream_read_b8_4k_bytes")
+    if ref_w4 is not None and m1 is not None:
+        line["roofline"]["read_reference_GBps"] = ref_w4["GBps_kernel"]
+        line["roofline"]["frac_of_read_reference"] = round(m1["GBps_kernel"] / ref_w4["GBps_kernel"], 4)
+    if "lm_head_topk_vocab128167_M1_k64" in legs:
+        lm = legs["lm_head_topk_vocab128167_M1_k64"]
+        line["roofline_lm_head_M1"] = {"bound": "hbm", "achieved": lm["GBps_kernel"], "peak": HBM_PEAK_GBS,
+                                       "unit": "GB/s", "frac": lm["frac_kernel"],
+                                       "us_chain": lm["us_step"], "traffic": None}
     if "prefill_cfg3" in legs:
         pf = legs["prefill_cfg3"]
         line["roofline_prefill_cfg3"] = {"bound": "mfma", "achieved": pf["TFLOPs_kernel"],
@@ -722,6 +812,9 @@ def main():
                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                          "frac": dec["frac_kernel"], "us_per_layer": dec["us_kernel"],
                                          "traffic": MEASURED_TRAFFIC["decode_b8_4k"]}
+        if ref_dec is not None:
+            line["roofline_decode_b8_4k"]["read_reference_GBps"] = ref_dec["GBps_kernel"]
+            line["roofline_decode_b8_4k"]["frac_of_read_reference"] = round(dec["GBps_kernel"] / ref_dec["GBps_kernel"], 4)
     print(json.dumps(line))
 
 

@@ -55,6 +55,11 @@ SIGNATURES: dict[str, tuple] = {
     # MXFP4 x MXFP8 GEMM (csrc/w4a8_gemm.hip)
     "h4a8_quant_act": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp, _c_i, _c_i, _c_vp]),
     "h4a8_gemm": (_c_i, [_c_vp] * 5 + [_c_i] * 3 + [_c_vp]),
+    # lm_head top-k and exact rerank (csrc/lm_head.hip)
+    "h4mv_topk_workspace_bytes": (_c_sz, [_c_i] * 3),
+    "h4mv_topk": (_c_i, [_c_vp] * 3 + [_c_i] * 4 + [_c_vp] * 3 + [_c_sz, _c_vp]),
+    "fp8kv_rerank_exact": (_c_i, [_c_vp, _c_i64, _c_i, _c_vp, _c_i64, _c_vp, _c_i, _c_i, _c_i, _c_vp, _c_vp,
+                                  _c_vp]),
     # host-only diagnostics (csrc/fp8kv_diag.h)
     "fp8kv_h4mv_audit": (_c_i, [_c_i] * 3),
     "fp8kv_h4mv_tune": (None, [_c_i] * 4),
@@ -63,6 +68,7 @@ SIGNATURES: dict[str, tuple] = {
     "fp8kv_prefill_tune": (None, [_c_i]),
     "fp8kv_gemm_tune": (None, [_c_i, _c_i]),
     "fp8kv_time_next_launch": (None, [_c_vp, _c_vp]),
+    "fp8kv_stream_read": (_c_i, [_c_vp, _c_sz, _c_vp, _c_vp]),
 }
 
 _lock = threading.Lock()

@@ -433,3 +433,61 @@ def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor)
     """x [M, K] bf16 -> [M, N] bf16 through the MXFP8 quantiser and the block-scaled GEMM."""
     xq, sx = quant_mxfp8(x)
     return h4a8_gemm(xq, sx, weight, scales_nk)
+
+
+# ------------------------------------------------------------------------------ lm_head, top-k, rerank
+
+_topk_ws: dict = {}
+
+
+def lm_head_topk(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor, k: int,
+                 workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(values fp32 [M, k], indices int32 [M, k]) of the k largest logits x . dequant(W)^T per row,
+    in rank order (value descending, NaN first, ties by lower index).  h4mv_topk; the workspace
+    defaults to a per-device cached buffer."""
+    _require(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(),
+             "x must be a contiguous 2-D bf16 device tensor")
+    M, K = x.shape
+    N = weight.shape[0]
+    _require(weight.dtype == torch.uint8 and tuple(weight.shape) == (N, K // 2) and weight.is_contiguous(),
+             "weight must be contiguous uint8 [N, K/2]")
+    _require(scales_nk.dtype == torch.uint8 and tuple(scales_nk.shape) == (N, K // 32)
+             and scales_nk.is_contiguous(), f"scales must be contiguous uint8 [{N}, {K // 32}]")
+    lib = _lib.load()
+    need = int(lib.h4mv_topk_workspace_bytes(N, M, int(k)))
+    _require(need > 0, f"k={k} outside [1, 64]")
+    if workspace is None:
+        key = (x.device.index if x.device.index is not None else torch.cuda.current_device())
+        workspace = _topk_ws.get(key)
+        if workspace is None or workspace.numel() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+            _topk_ws[key] = workspace
+    vals = torch.empty((M, k), dtype=torch.float32, device=x.device)
+    idx = torch.empty((M, k), dtype=torch.int32, device=x.device)
+    st = lib.h4mv_topk(weight.data_ptr(), scales_nk.data_ptr(), x.data_ptr(), N, K, M, int(k),
+                       vals.data_ptr(), idx.data_ptr(), workspace.data_ptr(),
+                       workspace.numel() * workspace.element_size(), _stream_ptr(x))
+    _lib.check("h4mv_topk", st)
+    return vals, idx
+
+
+def rerank_exact(embedding: torch.Tensor, x: torch.Tensor, candidates: torch.Tensor
+                 ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(values fp32 [M, C], indices int32 [M, C]): candidates[m] rescored as fp32 dot products of
+    x[m] with the bf16 embedding rows and sorted in rank order (fp8kv_rerank_exact)."""
+    _bf16_rows(embedding, "embedding")
+    _bf16_rows(x, "x")
+    V, H = embedding.shape
+    M = x.shape[0]
+    _require(x.shape[1] == H, "x and embedding widths differ")
+    _require(candidates.is_cuda and candidates.dtype == torch.int32 and candidates.dim() == 2
+             and candidates.shape[0] == M and candidates.is_contiguous(), "candidates must be int32 [M, C]")
+    C = candidates.shape[1]
+    vals = torch.empty((M, C), dtype=torch.float32, device=x.device)
+    idx = torch.empty((M, C), dtype=torch.int32, device=x.device)
+    st = _lib.load().fp8kv_rerank_exact(embedding.data_ptr(), embedding.stride(0), V, x.data_ptr(), x.stride(0),
+                                        candidates.data_ptr(), C, M, H, vals.data_ptr(), idx.data_ptr(),
+                                        _stream_ptr(x))
+    _lib.check("fp8kv_rerank_exact", st)
+    return vals, idx
+

@@ -307,6 +307,43 @@ int h4a8_quant_act(const void* X, int64_t x_row_stride, void* Xq, void* Sx, int 
 int h4a8_gemm(const void* W, const void* St, const void* Xq, const void* Sx, void* Out, int N, int K,
               int M, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * lm_head over the tied embedding, top-k and exact rerank (the end of a decode step).
+ *
+ * The reference engine runs an int2 "draft" lm_head over the tied embedding (vocab 128167), an
+ * exact rerank of its candidates and torch's top-k (kernels _draft_head_int2, _rerank_exact,
+ * aten::topk in profiling/prof_h4mv.txt:6,10,19; docs/06-w4gemm-hip-roadmap.md:116).  Its int2
+ * format is the closed fork's; this library's draft is the embedding in MXFP4 (the layout
+ * h4mv_launch reads), and the rerank reads the bf16 embedding rows.
+ * Rank order everywhere: value descending, NaN above every number (as torch.topk), +0 == -0,
+ * then index ascending.
+ * ------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes h4mv_topk needs (fp32 logits [M, N] + per-chunk candidates); 0 for k outside
+ * [1, 64] or a non-positive size. */
+size_t h4mv_topk_workspace_bytes(int N, int M, int k);
+
+/* out_val / out_idx [M, k] = the k largest of logits[m, :] = X[m] . dequant(W, St)^T (fp32
+ * accumulation, the fp32 output of h4mv_f32_launch_status), in rank order.  W, St, Xb as for
+ * h4mv_launch (1 <= M <= 16); 1 <= k <= min(64, N) and ceil(N / 4096) * k <= 2048 (every k up to
+ * 64 at vocab sizes up to 131072); workspace 256-byte aligned, at least
+ * h4mv_topk_workspace_bytes(N, M, k) bytes (no initial state).  Three kernels on `stream`.
+ * Replaces: the draft lm_head (_draft_head_int2) and aten::topk of the reference engine's decode
+ * step (profiling/prof_h4mv.txt:6,10). */
+int h4mv_topk(const void* W, const void* St, const void* Xb, int N, int K, int M, int k,
+              float* out_val, int32_t* out_idx, void* workspace, size_t workspace_bytes, void* stream);
+
+/* out_val / out_idx [M, C] = the candidates cand_idx[m, 0..C) rescored as fp32 dot products of
+ * X[m, :] with bf16 embedding rows E[idx, :] (H elements each, rows row_stride elements apart,
+ * multiples of 8, 16-byte aligned) and sorted in rank order; an index outside [0, V) sorts last
+ * with index -1 and value -inf, repeated indices keep their candidate order.  1 <= C <= 64,
+ * H % 8 == 0.
+ * Replaces: the exact rerank of the draft head's candidates (_rerank_exact,
+ * profiling/prof_h4mv.txt:19). */
+int fp8kv_rerank_exact(const void* E, int64_t e_row_stride, int V, const void* X, int64_t x_row_stride,
+                       const int32_t* cand_idx, int C, int M, int H, float* out_val, int32_t* out_idx,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,4 +9,4 @@ cites the reference file:line it follows.  How each function is pinned (checked 
 something other than itself) is listed in its module docstring; every function here has at
 least one such check in ``tests/test_oracle.py``.
 """
-from . import formats, matvec, attention, kv_cache, epilogues, w4a8  # noqa: F401
+from . import formats, matvec, attention, kv_cache, epilogues, w4a8, lm_head  # noqa: F401
