@@ -33,8 +33,19 @@ void fp8kv_h4mv_kslice_tune(int mode, int depth, int order, int workgroups);
 void fp8kv_decode_tune(int variant, int target_wgs);
 
 /* Tuning hook for sweeps of the prefill attention launch: index of the (waves, row-sets per wave,
- * LDS ring depth) shape to use for every GQA, or -1 for the per-GQA default. */
+ * LDS ring depth) shape to use for every GQA (0..7), 8 + s for key-split shape s (0..4, used only
+ * at its own GQA: 6, 12, 4, 8, 16) with the default block pairing, 13 + s for the same with paired
+ * token blocks (r, n16 - 1 - r) at any grid size, or -1 for the per-GQA default. */
 void fp8kv_prefill_tune(int shape);
+
+/* Planner query of the prefill attention launch (host only, no GPU call): the plan the entry
+ * points would launch for this shape under the current tuning hook.  ctx_hint is the longest
+ * context (q0 + qlen) for fp8kv_prefill_attn and max_query_len for the varlen entry point.
+ * out[8] = {kernel (1 key-split, 0 per-wave), shape index, token blocks per workgroup, paired
+ * (blocks r and n16 - 1 - r in one workgroup), token-block ranks per kv head, grid x, grid z,
+ * threads per workgroup}; all zero sizes when there is nothing to launch. */
+int fp8kv_prefill_plan(int num_q_heads, int num_kv_heads, int num_seqs, int max_query_len,
+                       int ctx_hint, int* out);
 
 /* Tuning hook for the MXFP4 x MXFP8 GEMM: kernel variant (0..8; any other value selects the
  * default, which picks variant 6 or 5 from the shape) and tile order

@@ -850,7 +850,9 @@ struct SplitShape {
 };
 constexpr SplitShape kSplitShapes[] = {{3, 2}, {3, 4}, {2, 2}, {2, 4}, {2, 8}};
 constexpr int kNumSplitShapes = sizeof(kSplitShapes) / sizeof(kSplitShapes[0]);
-int g_shape = -1;              // -1: choose by GQA; kNumShapes + s: key-split shape s
+// -1: choose by GQA; kNumShapes + s: key-split shape s; kNumShapes + kNumSplitShapes + s: the
+// same with paired token blocks whatever the grid size.
+int g_shape = -1;
 
 inline int split_shape_for(int gqa)
 {
@@ -891,36 +893,6 @@ inline bool split_single_blocks_fit(int n16, int hkv, int num_seqs)
     return (int64_t)((n16 + per - 1) / per * per) * hkv * num_seqs <= kSplitRoundWorkgroups;
 }
 
-int launch_split(const Params& P0, int ss, int num_seqs, int max_query_len, hipStream_t stream)
-{
-    Params P = P0;
-    P.nb = 2;
-    const int n16 = (max_query_len + 15) / 16;
-    if (n16 == 0) return FP8KV_OK;
-    P.xcd_map = (P.hkv <= 8 && 8 % P.hkv == 0) ? 1 : 0;
-    const int per = split_xcd_per(P.hkv);
-    auto round_up = [&](int n) { return (n + per - 1) / per * per; };
-    // Pairs of token blocks (r, n16 - 1 - r) give every workgroup the same causal work; when one
-    // block per workgroup still fits in one round of workgroups (one per CU: the ring takes most of
-    // the LDS), single blocks finish sooner (the longest workgroup sees about q0 + qlen keys
-    // instead of 2 q0 + qlen; measured at GQA 6: 1024 new tokens after 1024 cached 61.3 -> 38.7
-    // us, 512 after 1024 52.6 -> 30.0 us).
-    P.paired = split_single_blocks_fit(n16, P.hkv, num_seqs) ? 0 : 1;
-    const int ntb = round_up(P.paired ? (n16 + 1) / 2 : n16);
-    P.ntb_grid = ntb;
-    const dim3 grid((unsigned)(ntb * P.hkv), 1u, (unsigned)num_seqs);
-    const dim3 block(64 * kSplitWaves);
-    begin_launch();
-    switch (ss) {
-        case 0: launch_kernel(prefill_split_kernel<3, 2, 2>, grid, block, 0, stream, P); break;
-        case 1: launch_kernel(prefill_split_kernel<3, 4, 2>, grid, block, 0, stream, P); break;
-        case 2: launch_kernel(prefill_split_kernel<2, 2, 2>, grid, block, 0, stream, P); break;
-        case 3: launch_kernel(prefill_split_kernel<2, 4, 2>, grid, block, 0, stream, P); break;
-        default: launch_kernel(prefill_split_kernel<2, 8, 2>, grid, block, 0, stream, P); break;
-    }
-    return finish_launch();
-}
-
 // Contexts (in keys) from which the key-split kernel beats the per-wave kernel, measured on MI355X
 // at GQA 6.  With paired blocks: 1024 (512 new tokens after 512 cached 42.8 vs 45.6 us, 512
 // tokens alone 28.0 vs 24.4 us; 4 sequences of 512 32.0 vs 27.3 us).  With one block per
@@ -930,47 +902,91 @@ int launch_split(const Params& P0, int ss, int num_seqs, int max_query_len, hipS
 constexpr int kSplitMinContext = 1024;
 constexpr int kSplitMinContextSingle = 256;
 
+// One launch as planned from the shape alone (no pointers): kernel, block pairing and grid.
+struct Plan {
+    int split;          // key-split shape index, or -1 for the per-wave kernel
+    int shape;          // per-wave kernel shape index (split < 0)
+    int nb, paired, xcd_map, ntb_grid;
+    dim3 grid, block;
+};
+
+// Plans the launch; FP8KV_OK with ntb_grid == 0 means there is nothing to launch.
 // ctx_hint: the longest context when the host knows it (single sequence), else the longest query.
-int launch(const Params& P0, int num_seqs, int max_query_len, int ctx_hint, hipStream_t stream)
+int plan_launch(int gqa, int hkv, int num_seqs, int max_query_len, int ctx_hint, Plan& L)
 {
+    L = Plan{-1, 0, 1, 0, 0, 0, dim3(0u), dim3(0u)};
+    const int n16 = (max_query_len + 15) / 16;
+    if (n16 == 0) return FP8KV_OK;
+    L.xcd_map = (hkv <= 8 && 8 % hkv == 0) ? 1 : 0;
+    const int per = split_xcd_per(hkv);                // token-block ranks per kv head per XCD round
+    auto round_up = [&](int n) { return (n + per - 1) / per * per; };
+
     // Key-split kernel when the GQA has a split shape and the context is long enough, unless the
     // tuning hook forces another.
-    const int ss = split_shape_for(P0.gqa);
+    const int ss = split_shape_for(gqa);
+    bool split = false, force_paired = false;
     if (g_shape >= kNumShapes) {
-        if (g_shape - kNumShapes == ss) return launch_split(P0, ss, num_seqs, max_query_len, stream);
-    } else if (g_shape < 0 && ss >= 0 &&
-               (ctx_hint >= kSplitMinContext ||
-                (ctx_hint >= kSplitMinContextSingle &&
-                 split_single_blocks_fit((max_query_len + 15) / 16, P0.hkv, num_seqs)))) {
-        return launch_split(P0, ss, num_seqs, max_query_len, stream);
+        split = (g_shape - kNumShapes) % kNumSplitShapes == ss;
+        force_paired = g_shape >= kNumShapes + kNumSplitShapes;
+    } else if (g_shape < 0 && ss >= 0) {
+        split = ctx_hint >= kSplitMinContext ||
+                (ctx_hint >= kSplitMinContextSingle && split_single_blocks_fit(n16, hkv, num_seqs));
     }
+    if (split) {
+        // Pairs of token blocks (r, n16 - 1 - r) give every workgroup the same causal work; when
+        // one block per workgroup still fits in one round of workgroups (one per CU: the ring
+        // takes most of the LDS), single blocks finish sooner (the longest workgroup sees about
+        // q0 + qlen keys instead of 2 q0 + qlen; measured at GQA 6: 1024 new tokens after 1024
+        // cached 61.3 -> 38.7 us, 512 after 1024 52.6 -> 30.0 us).
+        L.split = ss;
+        L.nb = 2;
+        L.paired = (force_paired || !split_single_blocks_fit(n16, hkv, num_seqs)) ? 1 : 0;
+        L.ntb_grid = round_up(L.paired ? (n16 + 1) / 2 : n16);
+        L.block = dim3(64 * kSplitWaves);
+    } else {
+        L.shape = choose_shape(gqa);
+        const Shape sh = kShapes[L.shape];
+        if (sh.waves * sh.rs < gqa) return FP8KV_ERR_SHAPE;
+        L.nb = plan_nb(gqa, sh);
+        L.paired = sh.paired && L.nb == 2 ? 1 : 0;
+        const int ntb = L.paired ? (n16 + 1) / 2 : (n16 + L.nb - 1) / L.nb;
+        L.ntb_grid = L.xcd_map ? (ntb + per - 1) / per * per : ntb;
+        L.block = dim3(64 * sh.waves);
+    }
+    L.grid = dim3((unsigned)(L.ntb_grid * hkv), 1u, (unsigned)num_seqs);
+    return FP8KV_OK;
+}
+
+int launch(const Params& P0, int num_seqs, int max_query_len, int ctx_hint, hipStream_t stream)
+{
+    Plan L;
+    const int st = plan_launch(P0.gqa, P0.hkv, num_seqs, max_query_len, ctx_hint, L);
+    if (st != FP8KV_OK || L.ntb_grid == 0) return st;
     Params P = P0;
-    const int si = choose_shape(P.gqa);
-    const Shape sh = kShapes[si];
-    if (sh.waves * sh.rs < P.gqa) return FP8KV_ERR_SHAPE;
-    P.nb = plan_nb(P.gqa, sh);
-    P.paired = sh.paired && P.nb == 2 ? 1 : 0;
-    const int n16 = (max_query_len + 15) / 16;
-    int ntb = P.paired ? (n16 + 1) / 2 : (n16 + P.nb - 1) / P.nb;
-    if (ntb == 0) return FP8KV_OK;
-    P.xcd_map = (P.hkv <= 8 && 8 % P.hkv == 0) ? 1 : 0;
-    if (P.xcd_map) {
-        const int per = 8 / P.hkv;                    // token-block ranks per kv head per XCD round
-        ntb = (ntb + per - 1) / per * per;
-    }
-    P.ntb_grid = ntb;
-    const dim3 grid((unsigned)(ntb * P.hkv), 1u, (unsigned)num_seqs);
-    const dim3 block(64 * sh.waves);
+    P.nb = L.nb;
+    P.paired = L.paired;
+    P.xcd_map = L.xcd_map;
+    P.ntb_grid = L.ntb_grid;
     begin_launch();
-    switch (si) {
-        case 0: launch_kernel(prefill_kernel<4, 3, 4>, grid, block, 0, stream, P); break;
-        case 1: launch_kernel(prefill_kernel<4, 3, 6>, grid, block, 0, stream, P); break;
-        case 2: launch_kernel(prefill_kernel<8, 2, 4>, grid, block, 0, stream, P); break;
-        case 3: launch_kernel(prefill_kernel<4, 4, 4>, grid, block, 0, stream, P); break;
-        case 4: launch_kernel(prefill_kernel<4, 2, 4>, grid, block, 0, stream, P); break;
-        case 6: launch_kernel(prefill_kernel<6, 2, 4>, grid, block, 0, stream, P); break;
-        case 7: launch_kernel(prefill_kernel<8, 2, 4>, grid, block, 0, stream, P); break;
-        default: launch_kernel(prefill_kernel<4, 1, 4>, grid, block, 0, stream, P); break;
+    if (L.split >= 0) {
+        switch (L.split) {
+            case 0: launch_kernel(prefill_split_kernel<3, 2, 2>, L.grid, L.block, 0, stream, P); break;
+            case 1: launch_kernel(prefill_split_kernel<3, 4, 2>, L.grid, L.block, 0, stream, P); break;
+            case 2: launch_kernel(prefill_split_kernel<2, 2, 2>, L.grid, L.block, 0, stream, P); break;
+            case 3: launch_kernel(prefill_split_kernel<2, 4, 2>, L.grid, L.block, 0, stream, P); break;
+            default: launch_kernel(prefill_split_kernel<2, 8, 2>, L.grid, L.block, 0, stream, P); break;
+        }
+        return finish_launch();
+    }
+    switch (L.shape) {
+        case 0: launch_kernel(prefill_kernel<4, 3, 4>, L.grid, L.block, 0, stream, P); break;
+        case 1: launch_kernel(prefill_kernel<4, 3, 6>, L.grid, L.block, 0, stream, P); break;
+        case 2: launch_kernel(prefill_kernel<8, 2, 4>, L.grid, L.block, 0, stream, P); break;
+        case 3: launch_kernel(prefill_kernel<4, 4, 4>, L.grid, L.block, 0, stream, P); break;
+        case 4: launch_kernel(prefill_kernel<4, 2, 4>, L.grid, L.block, 0, stream, P); break;
+        case 6: launch_kernel(prefill_kernel<6, 2, 4>, L.grid, L.block, 0, stream, P); break;
+        case 7: launch_kernel(prefill_kernel<8, 2, 4>, L.grid, L.block, 0, stream, P); break;
+        default: launch_kernel(prefill_kernel<4, 1, 4>, L.grid, L.block, 0, stream, P); break;
     }
     return finish_launch();
 }
@@ -1065,7 +1081,24 @@ extern "C" int fp8kv_prefill_attn(const void* q, int64_t q_row_stride,
 
 extern "C" void fp8kv_prefill_tune(int shape)
 {
-    g_shape = (shape >= 0 && shape < kNumShapes + kNumSplitShapes) ? shape : -1;
+    g_shape = (shape >= 0 && shape < kNumShapes + 2 * kNumSplitShapes) ? shape : -1;
+}
+
+extern "C" int fp8kv_prefill_plan(int num_q_heads, int num_kv_heads, int num_seqs,
+                                  int max_query_len, int ctx_hint, int* out)
+{
+    if (!out || num_q_heads < 1 || num_kv_heads < 1 || num_seqs < 1 || max_query_len < 0)
+        return FP8KV_ERR_ARG;
+    if (num_q_heads % num_kv_heads != 0 || num_q_heads / num_kv_heads > kMaxGqa)
+        return FP8KV_ERR_SHAPE;
+    Plan L;
+    const int st = plan_launch(num_q_heads / num_kv_heads, num_kv_heads, num_seqs, max_query_len,
+                               ctx_hint, L);
+    if (st != FP8KV_OK) return st;
+    const int v[8] = {L.split >= 0 ? 1 : 0, L.split >= 0 ? L.split : L.shape, L.nb, L.paired,
+                      L.ntb_grid, (int)L.grid.x, (int)L.grid.z, (int)L.block.x};
+    for (int i = 0; i < 8; ++i) out[i] = v[i];
+    return FP8KV_OK;
 }
 
 extern "C" int fp8kv_prefill_attn_varlen(const void* q, int64_t q_row_stride,

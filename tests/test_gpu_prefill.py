@@ -189,6 +189,7 @@ def test_rejects_bad_arguments():
 
 SHAPE_CAP = [12, 12, 16, 16, 8, 4, 12, 16]      # waves x row-sets of each launch shape
 SPLIT_GQA = [6, 12, 4, 8, 16]                   # GQA of each key-split shape (tuning index 8 + s)
+SPLIT_PAIRED = 8 + len(SPLIT_GQA)               # tuning index 13 + s: shape s, paired token blocks
 
 
 @pytest.mark.parametrize("shape", [0, 1, 2, 3, 4, 5, 6, 7])
@@ -220,17 +221,35 @@ def test_large_cache_blocks(PBLK):
     _check_single(300, 77, HQ=24, HKV=4, seed=PBLK + 2, PBLK=PBLK, layout="engine")
 
 
+@pytest.mark.parametrize("paired", [False, True])
 @pytest.mark.parametrize("split", range(len(SPLIT_GQA)))
-def test_every_split_shape(split):
+def test_every_split_shape(split, paired):
     """Each key-split shape (row-sets per wave x head groups, keys split over the rest of the 8
-    waves) at its GQA: odd and even token-block counts, a tail block, varlen, block size 32."""
+    waves) at its GQA: a tail block, varlen, block size 32, and odd (11, 13, 33; varlen 3, 7, 19)
+    and even (16) token-block counts.  These grids fit one round of 256 workgroups, so the
+    default plan gives every workgroup one 16-token block; ``paired`` forces the two-phase plan
+    (blocks r and n16 - 1 - r in one workgroup, the middle block alone when n16 is odd) that
+    larger grids take."""
     lib = _lib.load()
     gqa = SPLIT_GQA[split]
     try:
-        lib.fp8kv_prefill_tune(8 + split)
+        lib.fp8kv_prefill_tune((SPLIT_PAIRED if paired else 8) + split)
         _check_single(161, 45, HQ=4 * gqa, HKV=4, seed=split * 10)
         _check_single(200, 0, HQ=4 * gqa, HKV=4, seed=split * 10 + 1)
+        _check_single(250, 7, HQ=4 * gqa, HKV=4, seed=split * 10 + 3)
         _check_single(513, 1000, HQ=2 * gqa, HKV=2, seed=split * 10 + 2, PBLK=32, layout="engine")
         _check_varlen([40, 97, 300], [3, 200, 0], seed=split + 60, HQ=4 * gqa, HKV=4)
     finally:
         lib.fp8kv_prefill_tune(-1)
+
+
+@pytest.mark.parametrize("gqa", SPLIT_GQA)
+def test_split_paired_default_plan(gqa):
+    """Grids above one round of 256 workgroups take paired token blocks on the default plan:
+    600 new tokens after 1000 cached at 8 kv heads (38 blocks x 8 heads = 304 workgroups)."""
+    _check_single(600, 1000, HQ=8 * gqa, HKV=8, seed=gqa + 70, layout="engine")
+
+
+def test_split_paired_varlen_default_plan():
+    """Varlen on the paired plan: 69, 65 and 19 token blocks (odd), 4 kv heads, GQA 6."""
+    _check_varlen([1100, 1030, 300], [0, 40, 900], seed=81, HQ=24, HKV=4, layout="engine")
