@@ -325,9 +325,10 @@ def bench_gate_up_silu(M: int, steps: int, warmup: int, N: int = 37888, K: int =
 MFMA_FP8_PEAK_TFLOPS = 5000.0      # dense fp8 (and fp8 x fp4) MFMA peak of MI355X
 
 
-def bench_w4a8_gemm(M: int, steps: int, warmup: int, variant: int = -1, order: int = 0):
-    """The configs[4] linears at M tokens (a prefill chunk) through the MXFP8 quantiser and the
-    MXFP4 x MXFP8 block-scaled GEMM; weights rotated above the MALL."""
+def bench_w4a8_gemm(M: int, steps: int, warmup: int, variant: int = -1, order: int = 0, act: str = "mx"):
+    """The configs[4] linears at M tokens (a prefill chunk) through an fp8 activation quantiser
+    (``act`` "mx": MXFP8 blocks; "token": per-token fp8, the engine's format) and the block-scaled
+    MXFP4 x fp8 GEMM; weights rotated above the MALL."""
     import torch
     from fp8kv_amd import ops, workloads
     dev = torch.device("cuda")
@@ -342,12 +343,18 @@ def bench_w4a8_gemm(M: int, steps: int, warmup: int, variant: int = -1, order: i
         for i in range(n_sets):
             c = workloads.w4_case(N, K, 1, seed=60 + i)
             ws.append((c["W"].to(dev), c["St"].to(dev)))
-        xq, sx = ops.quant_mxfp8(x[:, :K].contiguous())
-        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        wall, per = time_launches(lambda i: ops.h4a8_gemm(xq, sx, ws[i][0], ws[i][1], out=y), n_sets,
-                                  steps, warmup)
         xc = x[:, :K].contiguous()
-        wq, perq = time_launches(lambda i: ops.quant_mxfp8(xc, out=(xq, sx)), 1, steps, warmup)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        if act == "token":
+            xq, sx = ops.quant_fp8_per_token(xc)
+            gemm = lambda i: ops.h4a8_gemm_token(xq, sx, ws[i][0], ws[i][1], out=y)    # noqa: E731
+            quant = lambda i: ops.quant_fp8_per_token(xc, out=(xq, sx))              # noqa: E731
+        else:
+            xq, sx = ops.quant_mxfp8(xc)
+            gemm = lambda i: ops.h4a8_gemm(xq, sx, ws[i][0], ws[i][1], out=y)          # noqa: E731
+            quant = lambda i: ops.quant_mxfp8(xc, out=(xq, sx))                      # noqa: E731
+        wall, per = time_launches(gemm, n_sets, steps, warmup)
+        wq, perq = time_launches(quant, 1, steps, warmup)
         flops = 2.0 * M * N * K
         k_us = statistics.mean(per) * 1e3
         out[name] = {"N": N, "K": K, "us_kernel": round(k_us, 3), "us_step": round(wall * 1e3, 3),
@@ -787,6 +794,8 @@ def main():
         legs["gate_up_silu_cfg4_M8"] = bench_gate_up_silu(8, args.steps, args.warmup)
     if "gemm" in legs_wanted:
         legs["w4a8_gemm_cfg4_linears_M2048"] = bench_w4a8_gemm(2048, max(5, args.steps // 4), max(2, args.warmup // 4))
+        legs["w4a8_gemm_token_cfg4_linears_M2048"] = bench_w4a8_gemm(2048, max(5, args.steps // 4),
+                                                                     max(2, args.warmup // 4), act="token")
     if "stack" in legs_wanted:
         legs["stack_cfg4_28_layers_b8"] = bench_stack(max(3, args.steps // 20), max(2, args.warmup // 10))
     if "lmhead" in legs_wanted:

@@ -48,9 +48,10 @@ int fp8kv_prefill_plan(int num_q_heads, int num_kv_heads, int num_seqs, int max_
                        int ctx_hint, int* out);
 
 /* Tuning hook for the MXFP4 x MXFP8 GEMM: kernel variant (0..8; any other value selects the
- * default, which picks variant 6 or 5 from the shape) and tile order
- * (0 = XCDs split the token blocks, the default; 1 = XCDs split the weight blocks only).
- * Affects later launches. */
+ * default, which picks variant 6 or 5 from the shape; the per-token entry point runs only 5 and 6
+ * and takes its default for the others) and XCD split (0 = chosen by the traffic model, the
+ * default; 1 = XCDs split the weight blocks only; 2 = XCDs split the token blocks as far as their
+ * count allows).  Affects later launches. */
 void fp8kv_gemm_tune(int variant, int order);
 
 /* Measurement hook: the next kernel launched by this host thread through any entry point records

@@ -52,13 +52,15 @@ constexpr int kXcds = 8;
 constexpr int kDefaultVariant = -1;
 int g_gemm_variant = kDefaultVariant;
 
-inline int pick_variant(int N, int K, int M)
+inline int default_variant(int N, int K, int M)
 {
-    if (g_gemm_variant >= 0) return g_gemm_variant;
     const int64_t tiles6 = (int64_t)((N + 255) / 256) * ((M + 127) / 128);
     return (tiles6 >= 256 || K >= 8192) ? 6 : 5;
 }
-// 0: XCDs split the token blocks (default); 1: XCDs split the weight blocks only.
+
+inline int pick_variant(int N, int K, int M) { return g_gemm_variant >= 0 ? g_gemm_variant : default_variant(N, K, M); }
+// 0: XCD split by the traffic model of pick_split (default); 1: XCDs split the weight blocks
+// only; 2: XCDs split the token blocks as far as their count allows.
 int g_gemm_order = 0;
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -81,6 +83,7 @@ struct Params {
     const uint8_t* Xq;
     const uint8_t* Sx;
     __bf16* Out;
+    const float* tok_scale;   // per-token mode: fp32 scale of each activation row (Sx unused)
     int N, K, M;
     int nblk, mblk;
     int gm, gn;          // tile order: the 8 XCDs split the token blocks gm ways and the weight blocks gn ways
@@ -128,6 +131,7 @@ __device__ __forceinline__ f32x4_t mfma_tile(const Frags& f, uint32_t sa, uint32
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, f.b[J], acc, 4, 0, I, (int)sa, J, (int)sb);
 }
 
+template <bool TOK = false>
 __device__ __forceinline__ void compute(const Frags& f, f32x4_t (&acc)[4][4], int j)
 {
     // this lane's scale byte (k block j) of each tile, packed: tile i in byte i (op_sel picks it)
@@ -139,7 +143,8 @@ __device__ __forceinline__ void compute(const Frags& f, f32x4_t (&acc)[4][4], in
     const uint32_t b01 = __builtin_amdgcn_perm(f.sb[1], f.sb[0], sel);
     const uint32_t b23 = __builtin_amdgcn_perm(f.sb[3], f.sb[2], sel);
     const uint32_t sa = (a01 & 0xFFFFu) | (a23 << 16);
-    const uint32_t sb = (b01 & 0xFFFFu) | (b23 << 16);
+    // per-token mode: unit block scales (e8m0 127) on the activations
+    const uint32_t sb = TOK ? 0x7F7F7F7Fu : (b01 & 0xFFFFu) | (b23 << 16);
     acc[0][0] = mfma_tile<0, 0>(f, sa, sb, acc[0][0]);
     acc[0][1] = mfma_tile<0, 1>(f, sa, sb, acc[0][1]);
     acc[0][2] = mfma_tile<0, 2>(f, sa, sb, acc[0][2]);
@@ -258,7 +263,10 @@ struct LdsGeom {
 // DB: fragments double-buffered in registers (one workgroup per CU) or single-buffered with two
 // workgroups per CU (registers capped at 256 per lane, so two waves share each SIMD and one
 // wave's MFMAs cover the other's waits).
-template <int WN, int WM, int S, bool DB>
+// TOK: per-token mode (activation block scales fixed at 2^0, each output row multiplied by
+// P.tok_scale[m]); the activation-scale copies then read weight-scale rows of the tile (clamped
+// into the operand) so that every wave still issues the same copies and the waits stay exact.
+template <int WN, int WM, int S, bool DB, bool TOK>
 __device__ __forceinline__ void gemm_lds_body(const Params& P)
 {
     using G = LdsGeom<WN, WM, S>;
@@ -282,7 +290,7 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
     const uint8_t* const wtile = P.W + (int64_t)N0 * kh;
     const uint8_t* const xtile = P.Xq + (int64_t)M0 * P.K;
     const uint8_t* const swtile = P.St + (int64_t)N0 * ks;
-    const uint8_t* const sxtile = P.Sx + (int64_t)M0 * ks;
+    const uint8_t* const sxtile = TOK ? swtile : P.Sx + (int64_t)M0 * ks;
     uint32_t loff[G::DPW];
     int ldsoff[G::DPW];
 #pragma unroll
@@ -310,7 +318,8 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
             } else {
                 const int e2 = e - G::BN / 64;
                 int m = 64 * e2 + lane;
-                m = M0 + m < P.M ? m : P.M - 1 - M0;
+                if constexpr (TOK) m = N0 + m < P.N ? m : P.N - 1 - N0;
+                else m = M0 + m < P.M ? m : P.M - 1 - M0;
                 loff[c] = (uint32_t)m * (uint32_t)ks;
                 ldsoff[c] = G::W_BYTES + G::X_BYTES + G::SW_BYTES + 256 * e2;
             }
@@ -381,16 +390,16 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
         // odd last step
         for (int s = 0; s + 1 < nsteps; s += 2) {
             sync_read(fb, s + 1);
-            compute(fa, acc, j);                     // MFMAs on step s while step s + 1 is read
+            compute<TOK>(fa, acc, j);                // MFMAs on step s while step s + 1 is read
             if (s + 2 < nsteps) sync_read(fa, s + 2);
-            compute(fb, acc, j);
+            compute<TOK>(fb, acc, j);
         }
-        if (nsteps & 1) compute(fa, acc, j);
+        if (nsteps & 1) compute<TOK>(fa, acc, j);
     } else {
         Frags f;
         for (int s = 0; s < nsteps; ++s) {
             sync_read(f, s);
-            compute(f, acc, j);
+            compute<TOK>(f, acc, j);
         }
     }
 
@@ -400,11 +409,13 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
         const int m = m0 + 16 * im + r;
         if (m >= P.M) continue;
         __bf16* orow = P.Out + (int64_t)m * P.N;
+        const float ts = TOK ? P.tok_scale[m] : 1.f;
 #pragma unroll
         for (int in = 0; in < 4; ++in) {
             const int n = n0 + 16 * in + 4 * j;
             if (n >= P.N) continue;
-            const f32x4_t v = acc[in][im];
+            f32x4_t v = acc[in][im];
+            if constexpr (TOK) v = v * ts;
             *reinterpret_cast<u32x2_t*>(orow + n) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
     }
@@ -414,14 +425,14 @@ template <int WN, int WM, int S>
 __global__ void __launch_bounds__(64 * WN * WM)
 gemm_lds_kernel(Params P)
 {
-    gemm_lds_body<WN, WM, S, true>(P);
+    gemm_lds_body<WN, WM, S, true, false>(P);
 }
 
-template <int WN, int WM, int S>
+template <int WN, int WM, int S, bool TOK = false>
 __global__ void __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_lds2_kernel(Params P)
 {
-    gemm_lds_body<WN, WM, S, false>(P);
+    gemm_lds_body<WN, WM, S, false, TOK>(P);
 }
 
 // ---- larger wave tiles -------------------------------------------------------------------------
@@ -467,7 +478,7 @@ __device__ __forceinline__ void big_mfmas(const BigFrags<TN, TM>& f, const uint3
           (int)sb[(Is % TM) / 4])), ...);
 }
 
-template <int TN, int TM>
+template <int TN, int TM, bool TOK>
 __device__ __forceinline__ void big_compute(const BigFrags<TN, TM>& f, f32x4_t (&acc)[TN][TM], int j)
 {
     const uint32_t sel = (uint32_t)j | ((uint32_t)(j + 4) << 8);
@@ -482,12 +493,13 @@ __device__ __forceinline__ void big_compute(const BigFrags<TN, TM>& f, f32x4_t (
     for (int g = 0; g < TM / 4; ++g) {
         const uint32_t lo = __builtin_amdgcn_perm(f.sb[4 * g + 1], f.sb[4 * g], sel);
         const uint32_t hi = __builtin_amdgcn_perm(f.sb[4 * g + 3], f.sb[4 * g + 2], sel);
-        sb[g] = (lo & 0xFFFFu) | (hi << 16);
+        sb[g] = TOK ? 0x7F7F7F7Fu : (lo & 0xFFFFu) | (hi << 16);
     }
     big_mfmas<TN, TM>(f, sa, sb, acc, std::make_integer_sequence<int, TN * TM>{});
 }
 
-template <int WN, int WM, int TN, int TM, int S>
+// TOK: per-token mode, as in gemm_lds_body.
+template <int WN, int WM, int TN, int TM, int S, bool TOK = false>
 __global__ void __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_big_kernel(Params P)
 {
@@ -506,7 +518,7 @@ gemm_big_kernel(Params P)
     const uint8_t* const wtile = P.W + (int64_t)N0 * kh;
     const uint8_t* const xtile = P.Xq + (int64_t)M0 * P.K;
     const uint8_t* const swtile = P.St + (int64_t)N0 * ks;
-    const uint8_t* const sxtile = P.Sx + (int64_t)M0 * ks;
+    const uint8_t* const sxtile = TOK ? swtile : P.Sx + (int64_t)M0 * ks;
     uint32_t loff[G::DPW];
     int ldsoff[G::DPW];
     bool from_w[G::DPW];
@@ -538,7 +550,8 @@ gemm_big_kernel(Params P)
             } else {
                 const int e2 = e - G::NW_SW;
                 int m = 64 * e2 + lane;
-                m = M0 + m < P.M ? m : P.M - 1 - M0;
+                if constexpr (TOK) m = N0 + m < P.N ? m : P.N - 1 - N0;
+                else m = M0 + m < P.M ? m : P.M - 1 - M0;
                 loff[c] = (uint32_t)m * (uint32_t)ks;
                 ldsoff[c] = G::W_BYTES + G::X_BYTES + G::SW_BYTES + 256 * e2;
             }
@@ -602,7 +615,7 @@ gemm_big_kernel(Params P)
     BigFrags<TN, TM> f;
     for (int s = 0; s < nsteps; ++s) {
         sync_read(f, s);
-        big_compute<TN, TM>(f, acc, j);
+        big_compute<TN, TM, TOK>(f, acc, j);
     }
 
     const int n0 = N0 + wn * 16 * TN, m0 = M0 + wm * 16 * TM;
@@ -611,11 +624,13 @@ gemm_big_kernel(Params P)
         const int m = m0 + 16 * im + r;
         if (m >= P.M) continue;
         __bf16* orow = P.Out + (int64_t)m * P.N;
+        const float ts = TOK ? P.tok_scale[m] : 1.f;
 #pragma unroll
         for (int in = 0; in < TN; ++in) {
             const int n = n0 + 16 * in + 4 * j;
             if (n >= P.N) continue;
-            const f32x4_t v = acc[in][im];
+            f32x4_t v = acc[in][im];
+            if constexpr (TOK) v = v * ts;
             *reinterpret_cast<u32x2_t*>(orow + n) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
     }
@@ -683,66 +698,167 @@ quant_kernel(const uint16_t* __restrict__ X, int64_t x_stride, uint8_t* __restri
     }
 }
 
-}  // namespace w4a8_detail
-}  // namespace fp8kv
+// ---- per-token activation quantiser: bf16 [M, K] -> e4m3fn [M, K] + fp32 scale [M] ------------
+// vLLM's dynamic_per_token_scaled_fp8_quant (csrc/quantization/fp8/common.cu, the kernel the
+// reference engine runs before its W4A8 GEMM: profiling/prof_engine.txt:8): per row,
+// scale = max(max|x| / 448, 1 / (448 * 512)) and q = e4m3fn(clamp(x / scale, -448, 448)), the
+// division correctly rounded, max and clamp NaN-ignoring (fmaxf / fminf).  One workgroup of 256
+// threads per row.  Rows of up to 2048 R elements stay in registers (R 16-byte pieces per thread:
+// one HBM read per element); longer rows take a second pass over the same bytes.
+constexpr float kTokFp8Max = 448.f;
+constexpr int kTokThreads = 256;
+constexpr int kTokMaxR = 16;
 
-using namespace fp8kv;
-using namespace fp8kv::w4a8_detail;
-
-extern "C" int h4a8_quant_act(const void* X, int64_t x_row_stride, void* Xq, void* Sx, int M, int K,
-                              void* stream)
+__device__ __forceinline__ float amax8(const u32x4_t& v, float amax)
 {
-    if (!X || !Xq || !Sx || M < 0 || K < 32) return FP8KV_ERR_ARG;
-    if (M == 0) return FP8KV_OK;
-    if (K % 32 != 0) return FP8KV_ERR_SHAPE;
-    if (x_row_stride < K) return FP8KV_ERR_ARG;
-    if (!aligned(X, 16) || !aligned(Xq, 16) || (x_row_stride & 7)) return FP8KV_ERR_ALIGN;
-    const int64_t items = (int64_t)M * (K / 32);
-    int64_t blocks = (items + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    begin_launch();
-    launch_kernel(quant_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
-                  static_cast<const uint16_t*>(X), x_row_stride, static_cast<uint8_t*>(Xq),
-                  static_cast<uint8_t*>(Sx), M, K);
-    return finish_launch();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        amax = fmaxf(amax, fabsf(__uint_as_float(v[i] << 16)));
+        amax = fmaxf(amax, fabsf(__uint_as_float(v[i] & 0xFFFF0000u)));
+    }
+    return amax;
 }
 
-extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const void* Sx, void* Out,
-                         int N, int K, int M, void* stream)
+// e4m3fn bytes of the 8 bf16 values in v divided by scale
+__device__ __forceinline__ u32x2_t token_codes8(const u32x4_t& v, float scale)
 {
-    if (!W || !St || !Xq || !Sx || !Out || N < 1 || K < 1 || M < 0) return FP8KV_ERR_ARG;
-    if (M == 0) return FP8KV_OK;
-    if (K % kBK != 0 || N % 4 != 0) return FP8KV_ERR_SHAPE;
-    if (!aligned(W, 16) || !aligned(Xq, 16) || !aligned(St, 4) || !aligned(Sx, 4) || !aligned(Out, 8))
-        return FP8KV_ERR_ALIGN;
-    Params P;
-    P.W = static_cast<const uint8_t*>(W);
-    P.St = static_cast<const uint8_t*>(St);
-    P.Xq = static_cast<const uint8_t*>(Xq);
-    P.Sx = static_cast<const uint8_t*>(Sx);
-    P.Out = static_cast<__bf16*>(Out);
-    P.N = N;
-    P.K = K;
-    P.M = M;
-    const int variant = pick_variant(N, K, M);
+    uint32_t out[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float a[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            a[2 * i] = __uint_as_float(v[2 * h + i] << 16);
+            a[2 * i + 1] = __uint_as_float(v[2 * h + i] & 0xFFFF0000u);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = fmaxf(-kTokFp8Max, fminf(__fdiv_rn(a[i], scale), kTokFp8Max));
+        const uint32_t p0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a[0], a[1], 0, false) & 0xFFFFu;
+        const uint32_t p1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a[2], a[3], 0, false) & 0xFFFFu;
+        out[h] = p0 | (p1 << 16);
+    }
+    return (u32x2_t){out[0], out[1]};
+}
+
+// Row maximum over the workgroup, then the row's scale (thread 0 stores it).
+__device__ __forceinline__ float token_scale(float amax, float* red, float* scales, int m)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float min_scale = 1.f / (kTokFp8Max * 512.f);
+    const float scale = fmaxf(__fdiv_rn(amax, kTokFp8Max), min_scale);
+    if (threadIdx.x == 0) scales[m] = scale;
+    return scale;
+}
+
+// R > 0: the row in registers (K <= 2048 R); R == 0: two passes over the row.
+template <int R>
+__global__ void __launch_bounds__(kTokThreads)
+quant_token_kernel(const uint16_t* __restrict__ X, int64_t x_stride, uint8_t* __restrict__ Xq,
+                   float* __restrict__ scales, int K)
+{
+    __shared__ float red[kTokThreads / 64];
+    const int m = blockIdx.x;
+    const uint16_t* row = X + (int64_t)m * x_stride;
+    uint8_t* qrow = Xq + (int64_t)m * K;
+    float amax = 0.f;
+    if constexpr (R > 0) {
+        u32x4_t v[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int k = 8 * (threadIdx.x + i * kTokThreads);
+            v[i] = k < K ? load_16(row + k) : (u32x4_t){0u, 0u, 0u, 0u};     // |0| leaves the max
+            amax = amax8(v[i], amax);
+        }
+        const float scale = token_scale(amax, red, scales, m);
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int k = 8 * (threadIdx.x + i * kTokThreads);
+            if (k < K) *reinterpret_cast<u32x2_t*>(qrow + k) = token_codes8(v[i], scale);
+        }
+    } else {
+        for (int k = 8 * threadIdx.x; k < K; k += 8 * kTokThreads) amax = amax8(load_16(row + k), amax);
+        const float scale = token_scale(amax, red, scales, m);
+        for (int k = 8 * threadIdx.x; k < K; k += 8 * kTokThreads)
+            *reinterpret_cast<u32x2_t*>(qrow + k) = token_codes8(load_16(row + k), scale);
+    }
+}
+
+// Variants the per-token entry point runs (the tuning hook's forced variant applies when it is
+// one of them).
+inline bool has_token_variant(int v) { return v == 5 || v == 6; }
+
+constexpr int64_t kL2Bytes = (int64_t)4 << 20;        // per XCD
+constexpr int kLdsPerCu = 160 * 1024;
+constexpr int kCusPerXcd = 32;
+
+// Split of the 8 XCDs between token blocks (gm ways) and weight blocks (gn = 8 / gm ways).  The
+// XCDs of one token group read its activations, those of one weight group its weights, so a
+// launch fetches about gn * X + gm * W bytes into the L2s (X, W: activation and weight bytes
+// with scales).  Pick the gm in {1, 2, 4, 8} dividing the token-block count with the least of
+// that, among the splits under which an XCD's activation share is reused from its L2: either all
+// the XCD's tiles run in one round of resident workgroups (the tiles of a round stream K together)
+// or the share fits half an L2 (it then survives the weight tiles streamed between rounds).
+// Measured at the configs[4] linears, M = 2048, against the token-block split as far as the
+// count allows (bytes fetched into the L2s, FETCH_SIZE): qkv 70 -> 46 MB, o 53 -> 36 MB, gate/up
+// 667 -> 419 MB, down 332 -> 226 MB; kernel time 1-4 % lower (qkv 42.3 -> 40.5 us, down 193.9 ->
+// 188.4 us).
+int pick_split(const Params& P, int BM, int lds_bytes, bool act_scales)
+{
+    if (g_gemm_order == 1) return 1;
+    int gm_max = 1;
+    while (gm_max < kXcds && P.mblk % (2 * gm_max) == 0) gm_max *= 2;
+    if (g_gemm_order == 2) return gm_max;
+    const int64_t xb = (int64_t)P.M * P.K + (act_scales ? (int64_t)P.M * (P.K / 32) : 0);
+    const int64_t wb = (int64_t)P.N * (P.K / 2) + (int64_t)P.N * (P.K / 32);
+    const int64_t resident = (int64_t)kCusPerXcd * (lds_bytes > 0 ? kLdsPerCu / lds_bytes : 1);
+    int best = gm_max;
+    int64_t best_cost = -1;
+    for (int gm = 1; gm <= gm_max; gm *= 2) {
+        const int gn = kXcds / gm;
+        const int64_t tiles = (int64_t)(P.mblk / gm) * ((P.nblk + gn - 1) / gn);
+        const int64_t share = (int64_t)(P.mblk / gm) * BM * (P.K + P.K / 32);
+        if (tiles > resident && 2 * share > kL2Bytes) continue;
+        const int64_t cost = gn * xb + gm * wb;
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = gm;
+        }
+    }
+    return best;
+}
+
+int launch_gemm(Params& P, int variant, bool tok, hipStream_t st)
+{
     const int BN = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::BN : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::BN
                  : variant == 8 ? BigGeom<2, 4, 8, 4, 3>::BN : 128;
     const int BM = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::BM : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::BM
                  : variant == 8 ? BigGeom<2, 4, 8, 4, 3>::BM : 128;
-    P.nblk = (N + BN - 1) / BN;
-    P.mblk = (M + BM - 1) / BM;
+    P.nblk = (P.N + BN - 1) / BN;
+    P.mblk = (P.M + BM - 1) / BM;
     if ((int64_t)P.nblk * P.mblk > 0x7FFFFFFF - kXcds) return FP8KV_ERR_SHAPE;
-    // token blocks split over up to 8 XCDs (the largest power of two dividing their count, so
-    // every XCD gets the same number), the weight blocks over the rest
-    int gm = 1;
-    while (gm < kXcds && P.mblk % (2 * gm) == 0) gm *= 2;
-    if (g_gemm_order == 1) gm = 1;                         // weight-block split only
+    const int lds = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::LDS : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::LDS
+                  : variant == 8 ? BigGeom<2, 4, 8, 4, 3>::LDS : variant == 1 ? 0
+                  : variant == 0 ? LdsGeom<2, 2, 4>::LDS : variant == 2 || variant == 4 ? LdsGeom<2, 2, 3>::LDS
+                  : variant == 3 ? LdsGeom<2, 2, 5>::LDS : LdsGeom<2, 2, 2>::LDS;
+    const int gm = pick_split(P, BM, lds, !tok);
     P.gm = gm;
     P.gn = kXcds / gm;
     const int64_t per_xcd = (int64_t)((P.mblk + gm - 1) / gm) * ((P.nblk + P.gn - 1) / P.gn);
     const int64_t grid = per_xcd * kXcds;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
+    if (tok) {
+        if (variant == 6)
+            launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2, true>, dim3((unsigned)grid), dim3(256),
+                          BigGeom<2, 2, 8, 4, 2>::LDS, st, P);
+        else
+            launch_kernel(gemm_lds2_kernel<2, 2, 2, true>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 2>::LDS,
+                          st, P);
+        return finish_launch();
+    }
     switch (variant) {
         case 1:
             launch_kernel(gemm_kernel, dim3((unsigned)grid), dim3(256), 0, st, P);
@@ -778,8 +894,98 @@ extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const vo
     return finish_launch();
 }
 
+Params make_params(const void* W, const void* St, const void* Xq, const void* Sx, const float* tok_scale,
+                   void* Out, int N, int K, int M)
+{
+    Params P;
+    P.W = static_cast<const uint8_t*>(W);
+    P.St = static_cast<const uint8_t*>(St);
+    P.Xq = static_cast<const uint8_t*>(Xq);
+    P.Sx = static_cast<const uint8_t*>(Sx);
+    P.tok_scale = tok_scale;
+    P.Out = static_cast<__bf16*>(Out);
+    P.N = N;
+    P.K = K;
+    P.M = M;
+    return P;
+}
+
+}  // namespace w4a8_detail
+}  // namespace fp8kv
+
+using namespace fp8kv;
+using namespace fp8kv::w4a8_detail;
+
+extern "C" int h4a8_quant_act(const void* X, int64_t x_row_stride, void* Xq, void* Sx, int M, int K,
+                              void* stream)
+{
+    if (!X || !Xq || !Sx || M < 0 || K < 32) return FP8KV_ERR_ARG;
+    if (M == 0) return FP8KV_OK;
+    if (K % 32 != 0) return FP8KV_ERR_SHAPE;
+    if (x_row_stride < K) return FP8KV_ERR_ARG;
+    if (!aligned(X, 16) || !aligned(Xq, 16) || (x_row_stride & 7)) return FP8KV_ERR_ALIGN;
+    const int64_t items = (int64_t)M * (K / 32);
+    int64_t blocks = (items + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    begin_launch();
+    launch_kernel(quant_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                  static_cast<const uint16_t*>(X), x_row_stride, static_cast<uint8_t*>(Xq),
+                  static_cast<uint8_t*>(Sx), M, K);
+    return finish_launch();
+}
+
+extern "C" int h4a8_gemm(const void* W, const void* St, const void* Xq, const void* Sx, void* Out,
+                         int N, int K, int M, void* stream)
+{
+    if (!W || !St || !Xq || !Sx || !Out || N < 1 || K < 1 || M < 0) return FP8KV_ERR_ARG;
+    if (M == 0) return FP8KV_OK;
+    if (K % kBK != 0 || N % 4 != 0) return FP8KV_ERR_SHAPE;
+    if (!aligned(W, 16) || !aligned(Xq, 16) || !aligned(St, 4) || !aligned(Sx, 4) || !aligned(Out, 8))
+        return FP8KV_ERR_ALIGN;
+    Params P = make_params(W, St, Xq, Sx, nullptr, Out, N, K, M);
+    return launch_gemm(P, pick_variant(N, K, M), false, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int h4a8_quant_act_token(const void* X, int64_t x_row_stride, void* Xq, float* scales, int M,
+                                    int K, void* stream)
+{
+    if (!X || !Xq || !scales || M < 0 || K < 8) return FP8KV_ERR_ARG;
+    if (M == 0) return FP8KV_OK;
+    if (K % 8 != 0) return FP8KV_ERR_SHAPE;
+    if (x_row_stride < K) return FP8KV_ERR_ARG;
+    if (!aligned(X, 16) || !aligned(Xq, 8) || (x_row_stride & 7) || !aligned(scales, 4)) return FP8KV_ERR_ALIGN;
+    const int r = (K + 8 * kTokThreads - 1) / (8 * kTokThreads);     // 16-byte pieces per thread
+    const dim3 grid((unsigned)M), block(kTokThreads);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const uint16_t* x = static_cast<const uint16_t*>(X);
+    uint8_t* xq = static_cast<uint8_t*>(Xq);
+    begin_launch();
+    if (r <= 1) launch_kernel(quant_token_kernel<1>, grid, block, 0, st, x, x_row_stride, xq, scales, K);
+    else if (r <= 2) launch_kernel(quant_token_kernel<2>, grid, block, 0, st, x, x_row_stride, xq, scales, K);
+    else if (r <= 4) launch_kernel(quant_token_kernel<4>, grid, block, 0, st, x, x_row_stride, xq, scales, K);
+    else if (r <= 8) launch_kernel(quant_token_kernel<8>, grid, block, 0, st, x, x_row_stride, xq, scales, K);
+    else if (r <= 12) launch_kernel(quant_token_kernel<12>, grid, block, 0, st, x, x_row_stride, xq, scales, K);
+    else if (r <= kTokMaxR) launch_kernel(quant_token_kernel<kTokMaxR>, grid, block, 0, st, x, x_row_stride, xq, scales, K);
+    else launch_kernel(quant_token_kernel<0>, grid, block, 0, st, x, x_row_stride, xq, scales, K);
+    return finish_launch();
+}
+
+extern "C" int h4a8_gemm_token(const void* W, const void* St, const void* Xq, const float* token_scales,
+                               void* Out, int N, int K, int M, void* stream)
+{
+    if (!W || !St || !Xq || !token_scales || !Out || N < 1 || K < 1 || M < 0) return FP8KV_ERR_ARG;
+    if (M == 0) return FP8KV_OK;
+    if (K % kBK != 0 || N % 4 != 0) return FP8KV_ERR_SHAPE;
+    if (!aligned(W, 16) || !aligned(Xq, 16) || !aligned(St, 4) || !aligned(token_scales, 4) || !aligned(Out, 8))
+        return FP8KV_ERR_ALIGN;
+    Params P = make_params(W, St, Xq, nullptr, token_scales, Out, N, K, M);
+    int variant = pick_variant(N, K, M);
+    if (!has_token_variant(variant)) variant = default_variant(N, K, M);
+    return launch_gemm(P, variant, true, reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" void fp8kv_gemm_tune(int variant, int order)
 {
     fp8kv::w4a8_detail::g_gemm_variant = (variant >= 0 && variant <= 8) ? variant : -1;
-    fp8kv::w4a8_detail::g_gemm_order = order == 1 ? 1 : 0;
+    fp8kv::w4a8_detail::g_gemm_order = (order == 1 || order == 2) ? order : 0;
 }

@@ -55,6 +55,8 @@ SIGNATURES: dict[str, tuple] = {
     # MXFP4 x MXFP8 GEMM (csrc/w4a8_gemm.hip)
     "h4a8_quant_act": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp, _c_i, _c_i, _c_vp]),
     "h4a8_gemm": (_c_i, [_c_vp] * 5 + [_c_i] * 3 + [_c_vp]),
+    "h4a8_quant_act_token": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp, _c_i, _c_i, _c_vp]),
+    "h4a8_gemm_token": (_c_i, [_c_vp] * 5 + [_c_i] * 3 + [_c_vp]),
     # lm_head top-k and exact rerank (csrc/lm_head.hip)
     "h4mv_topk_workspace_bytes": (_c_sz, [_c_i] * 3),
     "h4mv_topk": (_c_i, [_c_vp] * 3 + [_c_i] * 4 + [_c_vp] * 3 + [_c_sz, _c_vp]),

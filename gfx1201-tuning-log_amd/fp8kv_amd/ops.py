@@ -429,8 +429,55 @@ def h4a8_gemm(xq: torch.Tensor, sx: torch.Tensor, weight: torch.Tensor, scales_n
     return out
 
 
-def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor) -> torch.Tensor:
-    """x [M, K] bf16 -> [M, N] bf16 through the MXFP8 quantiser and the block-scaled GEMM."""
+def quant_fp8_per_token(x: torch.Tensor, out: tuple[torch.Tensor, torch.Tensor] | None = None):
+    """bf16 [M, K] -> (e4m3fn codes uint8 [M, K], fp32 scales [M]), one scale per row:
+    max(max|x| / 448, 1 / (448 * 512)), codes e4m3fn(clamp(x / scale)).  h4a8_quant_act_token
+    (vLLM's dynamic_per_token_scaled_fp8_quant)."""
+    _bf16_rows(x, "x")
+    M, K = x.shape
+    if out is None:
+        out = (torch.empty((M, K), dtype=torch.uint8, device=x.device),
+               torch.empty((M,), dtype=torch.float32, device=x.device))
+    xq, sc = out
+    _require(xq.dtype == torch.uint8 and tuple(xq.shape) == (M, K) and xq.is_contiguous(), "codes must be uint8 [M, K]")
+    _require(sc.dtype == torch.float32 and tuple(sc.shape) == (M,) and sc.is_contiguous(), "scales must be fp32 [M]")
+    st = _lib.load().h4a8_quant_act_token(x.data_ptr(), x.stride(0), xq.data_ptr(), sc.data_ptr(), M, K,
+                                          _stream_ptr(x))
+    _lib.check("h4a8_quant_act_token", st)
+    return xq, sc
+
+
+def h4a8_gemm_token(xq: torch.Tensor, token_scales: torch.Tensor, weight: torch.Tensor,
+                    scales_nk: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 [M, N] = token_scales[:, None] * (e4m3(xq) . dequant(weight, scales_nk)^T)."""
+    M, K = xq.shape
+    N = weight.shape[0]
+    _require(xq.is_cuda and xq.dtype == torch.uint8 and xq.is_contiguous(), "xq must be contiguous uint8 [M, K]")
+    _require(token_scales.dtype == torch.float32 and tuple(token_scales.shape) == (M,) and token_scales.is_contiguous(),
+             "token scales must be fp32 [M]")
+    _require(weight.dtype == torch.uint8 and tuple(weight.shape) == (N, K // 2) and weight.is_contiguous(),
+             "weight must be contiguous uint8 [N, K/2]")
+    _require(scales_nk.dtype == torch.uint8 and tuple(scales_nk.shape) == (N, K // 32) and scales_nk.is_contiguous(),
+             "scales must be contiguous uint8 [N, K/32]")
+    _require(xq.device == token_scales.device == weight.device == scales_nk.device, "tensors on different devices")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=xq.device)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (M, N) and out.is_contiguous(),
+             "out must be contiguous bf16 [M, N]")
+    st = _lib.load().h4a8_gemm_token(weight.data_ptr(), scales_nk.data_ptr(), xq.data_ptr(), token_scales.data_ptr(),
+                                     out.data_ptr(), N, K, M, _stream_ptr(xq))
+    _lib.check("h4a8_gemm_token", st)
+    return out
+
+
+def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor,
+                 act: str = "mx") -> torch.Tensor:
+    """x [M, K] bf16 -> [M, N] bf16 through an fp8 activation quantiser and the block-scaled GEMM:
+    ``act`` "mx" (MXFP8 blocks of 32) or "token" (per-token fp8, the engine's format)."""
+    if act == "token":
+        xq, sc = quant_fp8_per_token(x)
+        return h4a8_gemm_token(xq, sc, weight, scales_nk)
+    _require(act == "mx", f"unknown activation format {act!r}")
     xq, sx = quant_mxfp8(x)
     return h4a8_gemm(xq, sx, weight, scales_nk)
 

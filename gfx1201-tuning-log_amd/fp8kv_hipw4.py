@@ -20,9 +20,11 @@ exception, runs the stolen body (:91-94).
 With FP8KV_HIPW4_GEMM=1 as well, larger batches (M > FP8KV_HIPW4_MAX_M, the prefill-sized
 linears the reference leaves to its fork's W4A8 GEMM) take the library's own GEMM path when its
 gate holds (contiguous 2-D bf16 x, K % 128 == 0, N % 4 == 0, K / 32 scale rows, 16-byte aligned
-weight): x is quantised to MXFP8 (h4a8_quant_act) and multiplied on the block-scaled MFMA
-(h4a8_gemm).  This path is opt-in: its activations are MXFP8 (per-32 block scales), not the
-fork's per-token fp8, so its results differ from the fork's within fp8 rounding.
+weight): x is quantised to fp8 and multiplied on the block-scaled MFMA.  FP8KV_HIPW4_GEMM_ACT
+picks the activation format: "token" (the default; per-token fp8 as the engine's
+dynamic_per_token_scaled_fp8_quant makes it, h4a8_quant_act_token + h4a8_gemm_token) or "mx"
+(MXFP8 blocks of 32, h4a8_quant_act + h4a8_gemm).  The fork's GEMM library is closed, so even the
+per-token path matches it only to fp32-accumulation rounding, not bit for bit.
 
 The library path is FP8KV_AMD_LIB if set, else the in-tree build (the reference hard-codes
 /opt/fp8kv/libh4mv.so).
@@ -86,10 +88,13 @@ def clamp_max_m(value: str) -> int:
     return c
 
 
-def load_gemm(path: str | None = None):
-    """Callable gemm(x, weight, st, out, stream) running h4a8_quant_act then h4a8_gemm through
-    ctypes (status checked; quantised activations in fresh torch buffers)."""
+def load_gemm(path: str | None = None, act: str = "token"):
+    """Callable gemm(x, weight, st, out, stream) running an activation quantiser then the GEMM
+    through ctypes (status checked; quantised activations in fresh torch buffers): ``act``
+    "token" (h4a8_quant_act_token + h4a8_gemm_token) or "mx" (h4a8_quant_act + h4a8_gemm)."""
     import torch
+    if act not in ("token", "mx"):
+        raise ValueError(f"unknown activation format {act!r}")
     if path is None:
         from fp8kv_amd import _lib
         path = _lib.lib_path()
@@ -99,6 +104,26 @@ def load_gemm(path: str | None = None):
     lib.h4a8_quant_act.restype = ci
     lib.h4a8_gemm.argtypes = [vp] * 5 + [ci] * 3 + [vp]
     lib.h4a8_gemm.restype = ci
+    lib.h4a8_quant_act_token.argtypes = [vp, i64, vp, vp, ci, ci, vp]
+    lib.h4a8_quant_act_token.restype = ci
+    lib.h4a8_gemm_token.argtypes = [vp] * 5 + [ci] * 3 + [vp]
+    lib.h4a8_gemm_token.restype = ci
+
+    def gemm_token(x, weight, st, out, stream):
+        M, K = x.shape
+        N = weight.shape[0]
+        xq = torch.empty((M, K), dtype=torch.uint8, device=x.device)
+        sc = torch.empty((M,), dtype=torch.float32, device=x.device)
+        rc = lib.h4a8_quant_act_token(x.data_ptr(), K, xq.data_ptr(), sc.data_ptr(), M, K, stream)
+        if rc != 0:
+            raise RuntimeError(f"h4a8_quant_act_token status {rc}")
+        rc = lib.h4a8_gemm_token(weight.data_ptr(), st.data_ptr(), xq.data_ptr(), sc.data_ptr(), out.data_ptr(),
+                                 N, K, M, stream)
+        if rc != 0:
+            raise RuntimeError(f"h4a8_gemm_token status {rc}")
+
+    if act == "token":
+        return gemm_token
 
     def gemm(x, weight, st, out, stream):
         M, K = x.shape
@@ -262,7 +287,7 @@ def _install() -> bool:
     gemm = None
     if os.environ.get("FP8KV_HIPW4_GEMM", "0") == "1":
         try:
-            gemm = load_gemm()
+            gemm = load_gemm(act=os.environ.get("FP8KV_HIPW4_GEMM_ACT", "token"))
         except Exception as e:
             _log(f"gemm path unavailable: {e}")
     threading.Thread(target=_poll, args=(launch, maxm), kwargs={"gemm": gemm, "last_status": last_status},

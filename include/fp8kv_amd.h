@@ -286,8 +286,10 @@ int h4mv_silu_mul(const void* W, const void* St, const void* Xb, void* Out, int 
  * The reference engine's prefill linears run its vLLM fork's W4A8 GEMM on per-token fp8
  * activations (radiance_mxfp4_fp8_gemm; profiling/prof_engine.txt:3-4, profiling/prof_prefill.txt:8,
  * docs/06-w4gemm-hip-roadmap.md:140; the activations come from vLLM's
- * dynamic_per_token_scaled_fp8_quant, profiling/prof_engine.txt:8).  That library is closed, so
- * these entry points define the operator on gfx950's native MXFP8 block format instead.
+ * dynamic_per_token_scaled_fp8_quant, profiling/prof_engine.txt:8).  That GEMM library is
+ * closed, so two activation formats are offered: gfx950's native MXFP8 block format
+ * (h4a8_quant_act + h4a8_gemm) and the engine's per-token fp8 (h4a8_quant_act_token +
+ * h4a8_gemm_token), whose quantiser restates vLLM's published kernel.
  * ------------------------------------------------------------------------------------------- */
 
 /* Xq[m, k] = e4m3fn(X[m, k] / 2^(Sx[m, k/32] - 127)) per 32-wide block of k, with the e8m0
@@ -306,6 +308,23 @@ int h4a8_quant_act(const void* X, int64_t x_row_stride, void* Xq, void* Sx, int 
  * Replaces: radiance_mxfp4_fp8_gemm (the fork's W4A8 prefill GEMM, profiling/prof_prefill.txt:8). */
 int h4a8_gemm(const void* W, const void* St, const void* Xq, const void* Sx, void* Out, int N, int K,
               int M, void* stream);
+
+/* Per-token fp8: per row m, scales[m] = max(max_k |X[m, k]| / 448, 1 / (448 * 512)) and
+ * Xq[m, k] = e4m3fn(clamp(X[m, k] / scales[m], -448, 448)), the division correctly rounded, the
+ * maximum and the clamp ignoring NaN (fmaxf / fminf), round to nearest even.  X bf16 [M, K] (row
+ * stride in elements, multiple of 8, 16-byte aligned), Xq uint8 [M, K] (8-byte aligned), scales
+ * fp32 [M]; K % 8 == 0.
+ * Replaces: vLLM's dynamic_per_token_scaled_fp8_quant (csrc/quantization/fp8/common.cu, no
+ * static upper bound), the engine's activation quantiser (profiling/prof_engine.txt:8). */
+int h4a8_quant_act_token(const void* X, int64_t x_row_stride, void* Xq, float* scales, int M, int K,
+                         void* stream);
+
+/* Out[m, n] = bf16( token_scales[m] * sum_k e4m3(Xq[m, k]) * dq(W, St)[n, k] ), f32 accumulation,
+ * the scale applied to the accumulator before the bf16 rounding.  Same W / St layout, shape and
+ * alignment rules as h4a8_gemm; token_scales fp32 [M].
+ * Replaces: radiance_mxfp4_fp8_gemm on per-token fp8 activations (profiling/prof_prefill.txt:8). */
+int h4a8_gemm_token(const void* W, const void* St, const void* Xq, const float* token_scales, void* Out,
+                    int N, int K, int M, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * lm_head over the tied embedding, top-k and exact rerank (the end of a decode step).

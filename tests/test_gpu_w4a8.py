@@ -1,5 +1,8 @@
 """GPU parity of the MXFP8 quantiser (h4a8_quant_act) and the MXFP4 x MXFP8 GEMM (h4a8_gemm).
 
+The per-token fp8 path (h4a8_quant_act_token, h4a8_gemm_token) meets the same bars: codes and
+fp32 scales bit-exact, the GEMM on the same operands within the bf16 bar, end to end within 5e-2.
+
 Bars: quantiser codes and scale bytes bit-exact against the oracle; GEMM output (on the same
 quantised operands) within half a bf16 ulp of the fp64 oracle plus 1e-4 * max|ref| (fp32
 accumulation inside the MFMA, the matvec's bf16 bar); end to end (bf16 x through the quantiser
@@ -90,17 +93,90 @@ def test_nan_scale_block_gives_nan_rows():
     assert torch.isfinite(torch.cat([got[:3], got[4:]])).all()
 
 
-def test_linear_hook_gemm_path_matches_ops():
-    """The opt-in large-batch path of the MXFP4 linear hook (ctypes into h4a8_quant_act and
-    h4a8_gemm, scales repacked on the device) gives the same bits as ops.mxfp4_linear."""
+@pytest.mark.parametrize("act", ["token", "mx"])
+def test_linear_hook_gemm_path_matches_ops(act):
+    """The opt-in large-batch path of the MXFP4 linear hook (ctypes into the quantiser and the
+    GEMM of either activation format, scales repacked on the device) gives the same bits as
+    ops.mxfp4_linear."""
     import fp8kv_hipw4 as h
     N, K, M = 512, 1024, 40
     c = workloads.w4_case(N, K, M, seed=23)
     x, w, s_kn = c["X"].to(DEV), c["W"].to(DEV), c["S_kn"].to(DEV)
     repack = h.ScaleRepack(lambda: False)
     patched = h.make_patched(lambda *a: None, h.load_launcher(), repack, 8, torch,
-                             lambda: torch.cuda.current_stream().cuda_stream, gemm=h.load_gemm())
+                             lambda: torch.cuda.current_stream().cuda_stream, gemm=h.load_gemm(act=act))
     got = patched(x, w, s_kn, None)
-    want = ops.mxfp4_linear(x, w, c["St"].to(DEV))
+    want = ops.mxfp4_linear(x, w, c["St"].to(DEV), act=act)
     torch.cuda.synchronize()
     assert got is not None and torch.equal(got, want)
+
+
+# ---- per-token fp8 activations -----------------------------------------------------------------
+
+@pytest.mark.parametrize("M,K,spread", [(1, 8, 0), (16, 512, 0), (300, 3584, 20.0), (7, 18944, 5.0), (33, 2056, 40.0),
+                                         (5, 8192, 3.0), (3, 16384, 0), (2, 32768, 1.0), (3, 40000, 2.0)])
+def test_token_quant_bit_exact(M, K, spread):
+    """Row lengths for every register-resident variant (2048 R elements, R = 1, 2, 4, 8, 12, 16)
+    and the two-pass fallback above 32768."""
+    g = torch.Generator().manual_seed(M * 7 + K)
+    x = torch.randn(M, K, generator=g)
+    if spread:
+        x = x * torch.exp(torch.empty(M, 1).uniform_(-spread, spread, generator=g))
+    x = x.to(torch.bfloat16)
+    xq, sc = ops.quant_fp8_per_token(x.to(DEV))
+    torch.cuda.synchronize()
+    rc, rs = w4a8.quant_fp8_per_token(x.float().numpy())
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(xq.cpu().numpy(), rc)
+
+
+def test_token_quant_special_rows():
+    """All-zero and tiny rows (scale floor), a NaN element, an infinite element, a strided input."""
+    x = torch.ones(6, 256)
+    x[0] = 0
+    x[1] = 1e-7
+    x[2, 17] = float("nan")
+    x[3, 200] = float("inf")
+    x[4, 9] = -float("inf")
+    x[5] = torch.linspace(-3000, 3000, 256)
+    xb = x.to(torch.bfloat16)
+    big = torch.zeros(6, 264, dtype=torch.bfloat16)
+    big[:, :256] = xb
+    xq, sc = ops.quant_fp8_per_token(big.to(DEV)[:, :256])
+    torch.cuda.synchronize()
+    rc, rs = w4a8.quant_fp8_per_token(xb.float().numpy())
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(xq.cpu().numpy(), rc)
+
+
+def _token_case(N, K, M, seed):
+    c = workloads.w4_case(N, K, M, seed=seed)
+    rc, rs = w4a8.quant_fp8_per_token(c["X"].float().numpy())
+    return c, rc, rs
+
+
+@pytest.mark.parametrize("variant,order", [(-1, 0), (5, 0), (5, 1), (6, 0), (6, 1), (2, 0)])
+@pytest.mark.parametrize("N,K,M", [(256, 512, 16), (200, 1024, 37), (4096, 3584, 300), (512, 18944, 64),
+                                   (128, 128, 1), (1024, 3072, 129), (384, 256, 200)])
+def test_token_gemm_parity(N, K, M, variant, order):
+    """Forced variants outside the per-token set (2) fall back to the default choice."""
+    lib = _lib.load()
+    c, rc, rs = _token_case(N, K, M, seed=N + 3 * M)
+    try:
+        lib.fp8kv_gemm_tune(variant, order)
+        out = ops.h4a8_gemm_token(torch.from_numpy(rc).to(DEV), torch.from_numpy(rs).to(DEV), c["W"].to(DEV),
+                                  c["St"].to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        lib.fp8kv_gemm_tune(-1, 0)
+    ref = w4a8.gemm_token(c["W"].numpy(), c["St"].numpy(), rc, rs)
+    got = out.float().cpu().numpy()
+    assert matvec.bf16_excess_error(got, ref) < 1e-4
+
+
+def test_token_end_to_end_against_w4a16_product():
+    N, K, M = 1024, 3584, 64
+    c = workloads.w4_case(N, K, M, seed=31)
+    got = ops.mxfp4_linear(c["X"].to(DEV), c["W"].to(DEV), c["St"].to(DEV), act="token").float().cpu().numpy()
+    ref = matvec.w4mv(c["W"].numpy(), c["St"].numpy(), c["X"].float().numpy())
+    assert matvec.rel_to_max_error(got, ref) < 5e-2
