@@ -15,7 +15,11 @@ Drop-in for vllm-fp8kv/fp8kv_prefill.py:
 Extension: the reference takes exactly one sequence (fp8kv_prefill.py:163); batches of several
 sequences go to ``fp8kv_prefill_attn_varlen`` here (each sequence's q0 is seq_lens[s] - qlen_s on
 the device).  FP8KV_PREFILL_VARLEN=0 restores the single-sequence gate; FP8KV_PREFILL_MIN_Q
-(default 64) is the max_query_len threshold.
+(default 64) is the max_query_len threshold.  Cascade batches (requests sharing a prefix), which
+the reference leaves to stock vLLM (fp8kv_prefill.py:168), also go to the varlen kernel: vLLM's
+cascade metadata keeps every sequence's full block table and length next to the shared-prefix
+fields, and attention over each full context is exactly what the prefix / suffix decomposition
+computes.  FP8KV_PREFILL_CASCADE=0 (or FP8KV_PREFILL_VARLEN=0) leaves them to stock.
 """
 from __future__ import annotations
 
@@ -41,12 +45,15 @@ def run(q, k_cache, v_cache, out, bt, kscale, vscale, sm_scale, q0, qlen,
     return ops.prefill_attention(q, k_cache, v_cache, out, bt, kscale, vscale, sm_scale, q0, qlen)
 
 
-def prefill_gate(impl, attn_metadata, fp8_per_tensor, min_q: int = 64, varlen: bool = True) -> bool:
+def prefill_gate(impl, attn_metadata, fp8_per_tensor, min_q: int = 64, varlen: bool = True,
+                 cascade: bool = True) -> bool:
     """The reference's prefill gate (fp8kv_prefill.py:158-172), optionally without the
-    single-sequence condition; missing attributes mean no."""
+    single-sequence condition and, on the varlen path, without the no-cascade condition; missing
+    attributes mean no."""
     try:
         nseq_ok = (attn_metadata.query_start_loc.shape[0] >= 2 if varlen
                    else attn_metadata.query_start_loc.shape[0] == 2)
+        cascade_ok = not getattr(attn_metadata, "use_cascade", False) or (cascade and varlen)
         return bool(
             attn_metadata is not None
             and impl._kv_quant_mode == fp8_per_tensor
@@ -59,26 +66,27 @@ def prefill_gate(impl, attn_metadata, fp8_per_tensor, min_q: int = 64, varlen: b
             and impl.sinks is None
             and impl.alibi_slopes is None
             and impl.logits_soft_cap == 0
-            and not getattr(attn_metadata, "use_cascade", False)
+            and cascade_ok
         )
     except AttributeError:
         return False
 
 
-def make_forward(nxt, fp8_per_tensor, ops, min_q: int = 64, varlen: bool = True):
+def make_forward(nxt, fp8_per_tensor, ops, min_q: int = 64, varlen: bool = True, cascade: bool = True):
     """Build the prefill forward wrapping ``nxt`` (the forward in place before this hook)."""
     from fp8kv_override import engine_cache_views
 
     def _forward(self, layer, query, key, value, kv_cache, attn_metadata, output,
                  output_scale=None, output_block_scale=None):
-        if prefill_gate(self, attn_metadata, fp8_per_tensor, min_q, varlen):
+        if prefill_gate(self, attn_metadata, fp8_per_tensor, min_q, varlen, cascade):
             try:
                 n = int(attn_metadata.num_actual_tokens)
                 hs = self.head_size
                 key_cache, value_cache = engine_cache_views(kv_cache, hs, self.fp8_dtype)
                 nseq = attn_metadata.query_start_loc.shape[0] - 1
                 done = False
-                if nseq == 1:
+                use_cascade = bool(getattr(attn_metadata, "use_cascade", False))
+                if nseq == 1 and not use_cascade:
                     q0 = int(attn_metadata.max_seq_len) - n       # no num_computed_tokens in this vLLM
                     if 0 <= q0 and n >= min_q:
                         ops.prefill_attention(query[:n], key_cache, value_cache, output[:n],
@@ -93,7 +101,7 @@ def make_forward(nxt, fp8_per_tensor, ops, min_q: int = 64, varlen: bool = True)
                                                  layer._k_scale, layer._v_scale, self.scale,
                                                  max_query_len=int(attn_metadata.max_query_len))
                     done = True
-                    desc = f"varlen nseq={nseq} tokens={n}"
+                    desc = f"varlen nseq={nseq} tokens={n}" + (" cascade" if use_cascade else "")
                 if done:
                     if not _STATE["engaged"]:
                         _STATE["engaged"] = True
@@ -123,7 +131,8 @@ def _install() -> bool:
     TritonAttentionImpl.forward = make_forward(
         nxt, KVQuantMode.FP8_PER_TENSOR, ops,
         min_q=int(os.environ.get("FP8KV_PREFILL_MIN_Q", "64")),
-        varlen=os.environ.get("FP8KV_PREFILL_VARLEN", "1") != "0")
+        varlen=os.environ.get("FP8KV_PREFILL_VARLEN", "1") != "0",
+        cascade=os.environ.get("FP8KV_PREFILL_CASCADE", "1") != "0")
     _STATE.update(installed=True, next=nxt)
     _log("installed")
     return True

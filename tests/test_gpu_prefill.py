@@ -253,3 +253,24 @@ def test_split_paired_default_plan(gqa):
 def test_split_paired_varlen_default_plan():
     """Varlen on the paired plan: 69, 65 and 19 token blocks (odd), 4 kv heads, GQA 6."""
     _check_varlen([1100, 1030, 300], [0, 40, 900], seed=81, HQ=24, HKV=4, layout="engine")
+
+
+@pytest.mark.parametrize("layout", ["standalone", "engine"])
+def test_cascade_shared_prefix_batch(layout):
+    """A cascade batch as vLLM describes it (the hook sends it to the varlen kernel): three
+    requests share the first 40 cache blocks (640 tokens) of their block tables, each with its own
+    suffix and new tokens; the varlen kernel over the full tables equals the oracle."""
+    c = workloads.prefill_case([300, 130, 257], [500, 700, 900], seed=33, layout=layout)
+    bt = c["block_table"]
+    bt[1:, :40] = bt[0, :40]                      # the shared prefix: same blocks, same K/V bytes
+    c["block_table"] = bt
+    d = workloads.to_device(c, DEV)
+    out = torch.full_like(d["q"], 7.0)
+    ops.prefill_attention_varlen(d["q"], d["k_cache"], d["v_cache"], out, d["cu_seqlens_q"], d["seq_lens"],
+                                 d["block_table"], torch.tensor([c["k_scale"]], device=DEV),
+                                 torch.tensor([c["v_scale"]], device=DEV), c["sm_scale"])
+    torch.cuda.synchronize()
+    ref = attention.varlen_prefill_attention(c["q"], c["k_cache"], c["v_cache"], c["cu_seqlens_q"],
+                                             c["seq_lens"], c["block_table"], c["k_scale"], c["v_scale"],
+                                             c["sm_scale"])
+    torch.testing.assert_close(out.cpu().to(torch.float64), ref.to(torch.float64), rtol=RTOL, atol=ATOL)

@@ -335,14 +335,37 @@ def test_prefill_multi_sequence_reference_gate(monkeypatch, no_capture):
     assert calls == ["stock"] and rec.calls == []
 
 
-def test_prefill_negative_q0_and_cascade_fall_through(monkeypatch, no_capture):
+def test_prefill_negative_q0_falls_through(monkeypatch, no_capture):
     cls, calls, rec, *_ = _chain(monkeypatch)
     md, layer, kv, q, out = _batch(ns=1, qlens=[100], ctx=(90,))     # max_seq_len < tokens
     cls.forward(_impl(cls), layer, q, None, None, kv, md, out)
-    md, layer, kv, q, out = _batch(ns=1, qlens=[100], ctx=(300,))
+    assert calls == ["stock"] and rec.calls == []
+
+
+def test_prefill_cascade_batch_runs_varlen_on_full_contexts(monkeypatch, no_capture):
+    """A cascade batch (shared prefix) goes to the varlen kernel with the full per-sequence
+    metadata, whatever its sequence count."""
+    cls, calls, rec, *_ = _chain(monkeypatch)
+    md, layer, kv, q, out = _batch(ns=3, qlens=[70, 80, 64], ctx=(600, 610, 700))
     md.use_cascade = True
     cls.forward(_impl(cls), layer, q, None, None, kv, md, out)
-    assert calls == ["stock", "stock"] and rec.calls == []
+    md1, layer, kv, q, out = _batch(ns=1, qlens=[100], ctx=(300,))
+    md1.use_cascade = True
+    cls.forward(_impl(cls), layer, q, None, None, kv, md1, out)
+    assert calls == [] and [c[0] for c in rec.calls] == ["varlen", "varlen"]
+    a = rec.calls[0][1]
+    assert a[4] is md.query_start_loc and a[5] is md.seq_lens and a[6] is md.block_table
+
+
+@pytest.mark.parametrize("env", [{"FP8KV_PREFILL_CASCADE": "0"}, {"FP8KV_PREFILL_VARLEN": "0"}])
+def test_prefill_cascade_left_to_stock_when_disabled(monkeypatch, no_capture, env):
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    cls, calls, rec, *_ = _chain(monkeypatch, varlen=env.get("FP8KV_PREFILL_VARLEN", "1"))
+    md, layer, kv, q, out = _batch(ns=2, qlens=[70, 80], ctx=(600, 610))
+    md.use_cascade = True
+    cls.forward(_impl(cls), layer, q, None, None, kv, md, out)
+    assert calls == ["stock"] and rec.calls == []
 
 
 def test_prefill_exception_falls_back(monkeypatch, no_capture, capsys):
