@@ -12,8 +12,8 @@
 //   * h4mv_topk: logits[m, n] = X[m] . dequant(W[n])^T in fp32 (h4mv_f32_launch_status, into the
 //     workspace), then the k largest per row, in two kernels: every 4096-logit chunk of a row
 //     gives its own top k (chunk_topk_kernel), and one workgroup per row picks the top k of those
-//     candidates (merge_topk_kernel).  Each selection is a wave-level threshold search over
-//     64-bit rank keys held in registers (no workgroup barrier per selected key).
+//     candidates (merge_topk_kernel).  Each selection is a workgroup radix select over 64-bit
+//     rank keys held in registers (block_topk), 8 bits per round with an LDS histogram.
 //   * rank order: value descending, NaN above every number (as torch.topk), +0 and -0 equal, then
 //     index ascending.  Keys are unique (they carry the index), so every round has one winner.
 //   * fp8kv_rerank_exact: out = the C candidates of each row rescored as fp32 dot products of X[m]
@@ -55,143 +55,138 @@ __device__ __forceinline__ int32_t key_index(uint64_t key)
     return (int32_t)(0xffffffffu - (uint32_t)key);
 }
 
-// Sum over the 64 lanes of a wave, in every lane: DPP within rows of 16, then the gfx950 row swaps.
-__device__ __forceinline__ uint32_t wave_sum(uint32_t v)
+// Inclusive prefix sum over the lanes of a wave (lane order).
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v, int lane)
 {
-    v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);    // quad_perm [1,0,3,2]
-    v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);    // quad_perm [2,3,0,1]
-    v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);   // row_half_mirror
-    v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);   // row_mirror
-    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    v = r[0] + r[1];
-    const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return q[0] + q[1];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)v, d);
+        if (lane >= d) v += o;
+    }
+    return v;
 }
 
-// The k (<= 64) largest of the 64 * NPL keys one wave holds (unique; 0 = none), written in no
-// particular order to out[0 .. k) (0 past the number of non-zero keys).  The k-th largest key T
-// is found by binary search, bit by bit from the top, for the largest T with at least k keys
-// >= T: first on the keys' high words (the logit), then, only when several keys share the k-th
-// high word, on the low words (the index) of those keys.  Then every key >= T is written, at
-// positions from a ballot prefix count.  All lanes of the wave take part.
+// The k (<= kMaxK) largest of the kThreads * NPL keys the workgroup holds (unique; 0 = none),
+// written in no particular order to out[0 .. k) (0 past the number of non-zero keys).  Radix
+// select from the top, 8 bits per round: a 256-bucket LDS histogram of the keys that match the
+// digits fixed so far, then one wave finds the bucket holding the k-th largest of them.  The
+// search stops as soon as that bucket holds exactly the keys still needed (they are all taken;
+// with unique keys this happens by the 8th round, usually after two or three), and every key at
+// or above the threshold is written at a position from an LDS counter.
 template <int NPL>
-__device__ __forceinline__ void wave_topk(const uint64_t (&keys)[NPL], int k, uint64_t* out)
+__device__ __forceinline__ void block_topk(const uint64_t (&keys)[NPL], int k, uint64_t* out)
 {
-    uint32_t hi[NPL], lo[NPL];
+    static_assert(kThreads == 256, "one histogram bucket per thread");
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_digit, s_above, s_in_bucket, s_total, s_cnt;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint64_t prefix = 0, mask = 0, T = 0;
+    uint32_t need = (uint32_t)k;
+    bool found = false;
+    if (tid == 0) s_cnt = 0;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        hist[tid] = 0;
+        __syncthreads();
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-        hi[j] = (uint32_t)(keys[j] >> 32);
-        lo[j] = (uint32_t)keys[j];
-    }
-    auto count_hi = [&](uint32_t t) {
-        uint32_t c = 0;
+        for (int j = 0; j < NPL; ++j)
+            if (keys[j] != 0 && (keys[j] & mask) == prefix)
+                atomicAdd(&hist[(uint32_t)(keys[j] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (wave == 0) {
+            // lane l holds buckets 255 - 4l .. 252 - 4l, so lane order is descending key order
+            uint32_t h[4];
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) c += hi[j] >= t ? 1u : 0u;
-        return wave_sum(c);
-    };
-    uint32_t th = 0;
-    for (int b = 31; b >= 0; --b) {
-        const uint32_t cand = th | (1u << b);
-        if (count_hi(cand) >= (uint32_t)k) th = cand;
-    }
-    // th: the high word of the k-th largest key (0 when fewer than k keys have one above 0).
-    uint32_t tl = 0;
-    const uint32_t above = th == 0xffffffffu ? 0u : count_hi(th + 1);
-    if (count_hi(th) > (uint32_t)k) {              // ties at the k-th high word: search the low words
-        auto count_lo = [&](uint32_t t) {
-            uint32_t c = 0;
+            for (int i = 0; i < 4; ++i) h[i] = hist[255 - 4 * lane - i];
+            const uint32_t tot = (h[0] + h[1]) + (h[2] + h[3]);
+            const uint32_t incl = wave_inclusive_sum(tot, lane);
+            const uint32_t excl = incl - tot;
+            if (lane == 63) s_total = incl;
+            if (excl < need && incl >= need) {          // the lane holding the need-th key
+                uint32_t cum = excl;
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) c += (hi[j] == th && lo[j] >= t) ? 1u : 0u;
-            return wave_sum(c);
-        };
-        for (int b = 31; b >= 0; --b) {
-            const uint32_t cand = tl | (1u << b);
-            if (above + count_lo(cand) >= (uint32_t)k) tl = cand;
+                for (int i = 0; i < 4; ++i) {
+                    if (cum + h[i] >= need) {
+                        s_digit = 255u - 4u * (uint32_t)lane - (uint32_t)i;
+                        s_above = cum;
+                        s_in_bucket = h[i];
+                        break;
+                    }
+                    cum += h[i];
+                }
+            }
         }
+        __syncthreads();
+        if (s_total < need) {                          // fewer keys than asked for: take them all
+            T = 1;
+            found = true;
+            break;
+        }
+        const uint32_t d = s_digit;
+        need -= s_above;
+        prefix |= (uint64_t)d << shift;
+        mask |= (uint64_t)0xffu << shift;
+        if (s_in_bucket == need) {                     // the whole bucket is taken
+            T = prefix;
+            found = true;
+            break;
+        }
+        __syncthreads();                               // everyone has read the bucket state
     }
-    const uint64_t T = ((uint64_t)th << 32) | tl;
-    const uint64_t lanes_below = __lanemask_lt();
-    uint32_t base = 0;
+    if (!found) T = prefix;
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-        const bool sel = keys[j] != 0 && keys[j] >= T;
-        const uint64_t bal = __ballot(sel);
-        if (sel) out[base + __popcll(bal & lanes_below)] = keys[j];
-        base += (uint32_t)__popcll(bal);
-    }
-    for (uint32_t p = base + (threadIdx.x & 63); p < (uint32_t)k; p += 64) out[p] = 0;
+    for (int j = 0; j < NPL; ++j)
+        if (keys[j] != 0 && keys[j] >= T) out[atomicAdd(&s_cnt, 1u)] = keys[j];
+    __syncthreads();
+    for (uint32_t p = s_cnt + (uint32_t)tid; p < (uint32_t)k; p += kThreads) out[p] = 0;
 }
 
 // grid (nchunks, M): the top k of logits[m, 4096 c .. +4096) as keys in cand[m][c][0..k), in no
-// particular order.  Wave w selects the top k of its 1024 logits into LDS, then wave 0 the top k
-// of those 4 k.
+// particular order.  Loads are unconditional (indices clamped into the row, keys past it masked
+// to 0), so all 16 of a thread are in flight together.
 __global__ void __launch_bounds__(kThreads)
 chunk_topk_kernel(const float* __restrict__ logits, int N, int k, uint64_t* __restrict__ cand)
 {
-    __shared__ uint64_t part[4 * kMaxK];
     const int c = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
     const float* row = logits + (size_t)m * (size_t)N;
+    float v[kPerThread];
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) v[j] = row[min(c * kChunk + j * kThreads + tid, N - 1)];
     uint64_t keys[kPerThread];
 #pragma unroll
     for (int j = 0; j < kPerThread; ++j) {
-        const int n = c * kChunk + wave * 1024 + j * 64 + lane;
-        keys[j] = n < N ? rank_key(row[n], (uint32_t)n) : 0;
+        const int n = c * kChunk + j * kThreads + tid;
+        keys[j] = n < N ? rank_key(v[j], (uint32_t)n) : 0;
     }
-    wave_topk<kPerThread>(keys, k, part + wave * k);
-    __syncthreads();
-    if (wave == 0) {
-        uint64_t p4[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = j * 64 + lane;
-            p4[j] = i < 4 * k ? part[i] : 0;
-        }
-        wave_topk<4>(p4, k, cand + ((size_t)m * gridDim.x + c) * (size_t)k);
-    }
+    block_topk<kPerThread>(keys, k, cand + ((size_t)m * gridDim.x + c) * (size_t)k);
 }
 
 // grid (M): the top k of a row's ncand (<= 2048) candidate keys, written as values and indices
-// in rank order (positions past the valid candidates: index -1, value -inf).  Wave w selects
-// from 512 candidates, wave 0 from the 4 k survivors; each survivor's position is the number of
-// keys above it.
+// in rank order (positions past the valid candidates: index -1, value -inf): the workgroup
+// selects them, then each one's position is the number of keys above it.
 __global__ void __launch_bounds__(kThreads)
 merge_topk_kernel(const uint64_t* __restrict__ cand, int ncand, int k, float* __restrict__ out_val,
                   int32_t* __restrict__ out_idx)
 {
-    __shared__ uint64_t part[4 * kMaxK];
     __shared__ uint64_t top[kMaxK];
     const int m = blockIdx.x, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
     const uint64_t* row = cand + (size_t)m * (size_t)ncand;
     uint64_t keys[kMaxMergePerThread];
 #pragma unroll
-    for (int j = 0; j < kMaxMergePerThread; ++j) {
-        const int i = wave * 512 + j * 64 + lane;
-        keys[j] = i < ncand ? row[i] : 0;
-    }
-    wave_topk<kMaxMergePerThread>(keys, k, part + wave * k);
-    __syncthreads();
-    if (wave == 0) {
-        uint64_t p4[4];
+    for (int j = 0; j < kMaxMergePerThread; ++j) keys[j] = row[min(j * kThreads + tid, ncand - 1)];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = j * 64 + lane;
-            p4[j] = i < 4 * k ? part[i] : 0;
+    for (int j = 0; j < kMaxMergePerThread; ++j)
+        if (j * kThreads + tid >= ncand) keys[j] = 0;
+    block_topk<kMaxMergePerThread>(keys, k, top);
+    __syncthreads();
+    if (tid < k) {
+        const uint64_t mine = top[tid];
+        int rank = 0;
+        for (int j = 0; j < k; ++j) {
+            const uint64_t o = top[j];
+            rank += (o > mine || (o == mine && j < tid)) ? 1 : 0;
         }
-        wave_topk<4>(p4, k, top);
-        __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): this wave's LDS writes done
-        __builtin_amdgcn_wave_barrier();
-        if (lane < k) {
-            const uint64_t mine = top[lane];
-            int rank = 0;
-            for (int j = 0; j < k; ++j) {
-                const uint64_t o = top[j];
-                rank += (o > mine || (o == mine && j < lane)) ? 1 : 0;
-            }
-            out_val[(size_t)m * k + rank] = mine ? key_value(mine) : -__builtin_inff();
-            out_idx[(size_t)m * k + rank] = mine ? key_index(mine) : -1;
-        }
+        out_val[(size_t)m * k + rank] = mine ? key_value(mine) : -__builtin_inff();
+        out_idx[(size_t)m * k + rank] = mine ? key_index(mine) : -1;
     }
 }
 
