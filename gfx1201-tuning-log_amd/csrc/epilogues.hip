@@ -52,27 +52,38 @@ add_rmsnorm_kernel(NormParams P)
     uint16_t* rr = P.res + (int64_t)row * P.res_stride;
     uint16_t* orow = P.out + (int64_t)row * P.out_stride;
 
+    // Every load is issued unconditionally (chunks past H re-read the row's last 16 bytes and are
+    // masked to zero): a load under a divergent branch would wait for its data at the join, one
+    // HBM round trip per chunk.  The weight chunks are fetched here too, so all 3*C loads of a
+    // thread are in flight together.
     float z[C][8];
+    u32x4_t wv[C];
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
         const int e0 = (tid + c * kNormThreads) * 8;
-        if (e0 < P.H) {
-            const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xr + e0);
-            const u32x4_t rv = *reinterpret_cast<const u32x4_t*>(rr + e0);
+        const int el = min(e0, P.H - 8);
+        const bool in = e0 < P.H;
+        u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xr + el);
+        u32x4_t rv = *reinterpret_cast<const u32x4_t*>(rr + el);
+        wv[c] = *reinterpret_cast<const u32x4_t*>(P.w + el);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                float a = bf_lo(xv[k]) + bf_lo(rv[k]);
-                float b = bf_hi(xv[k]) + bf_hi(rv[k]);
-                if (P.mode == 1) {
-                    a = round_to_bf16(a);
-                    b = round_to_bf16(b);
-                }
-                z[c][2 * k] = a;
-                z[c][2 * k + 1] = b;
-                ss += a * a;
-                ss += b * b;
+        for (int k = 0; k < 4; ++k) {
+            xv[k] = in ? xv[k] : 0u;
+            rv[k] = in ? rv[k] : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float a = bf_lo(xv[k]) + bf_lo(rv[k]);
+            float b = bf_hi(xv[k]) + bf_hi(rv[k]);
+            if (P.mode == 1) {
+                a = round_to_bf16(a);
+                b = round_to_bf16(b);
             }
+            z[c][2 * k] = a;
+            z[c][2 * k + 1] = b;
+            ss += a * a;
+            ss += b * b;
         }
     }
     // sum of squares over the workgroup: xor-shuffles in each wave, then the four wave sums
@@ -89,14 +100,13 @@ add_rmsnorm_kernel(NormParams P)
     for (int c = 0; c < C; ++c) {
         const int e0 = (tid + c * kNormThreads) * 8;
         if (e0 < P.H) {
-            const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(P.w + e0);
             u32x4_t rs, os;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const float a = z[c][2 * k], b = z[c][2 * k + 1];
                 rs[k] = pack_bf16x2(a, b);
                 const float ya = round_to_bf16(a * r), yb = round_to_bf16(b * r);
-                os[k] = pack_bf16x2(ya * bf_lo(wv[k]), yb * bf_hi(wv[k]));
+                os[k] = pack_bf16x2(ya * bf_lo(wv[c][k]), yb * bf_hi(wv[c][k]));
             }
             *reinterpret_cast<u32x4_t*>(rr + e0) = rs;
             *reinterpret_cast<u32x4_t*>(orow + e0) = os;

@@ -404,18 +404,32 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
     }
 
     const int n0 = N0 + wn * 64, m0 = M0 + wm * 64;
+    // per-token mode: the wave's row scales are loaded together at clamped rows and applied to
+    // every accumulator before the guarded stores (a product the compiler sinks into a guarded
+    // store waits there for all earlier memory operations, the stores included)
+    if constexpr (TOK) {
+        float ts[4];
+#pragma unroll
+        for (int im = 0; im < 4; ++im) ts[im] = P.tok_scale[min(m0 + 16 * im + r, P.M - 1)];
+#pragma unroll
+        for (int im = 0; im < 4; ++im) {
+#pragma unroll
+            for (int in = 0; in < 4; ++in) {
+                acc[in][im] = acc[in][im] * ts[im];
+                asm volatile("" : "+v"(acc[in][im]));   // keeps the product out of the store branch
+            }
+        }
+    }
 #pragma unroll
     for (int im = 0; im < 4; ++im) {
         const int m = m0 + 16 * im + r;
         if (m >= P.M) continue;
         __bf16* orow = P.Out + (int64_t)m * P.N;
-        const float ts = TOK ? P.tok_scale[m] : 1.f;
 #pragma unroll
         for (int in = 0; in < 4; ++in) {
             const int n = n0 + 16 * in + 4 * j;
             if (n >= P.N) continue;
-            f32x4_t v = acc[in][im];
-            if constexpr (TOK) v = v * ts;
+            const f32x4_t v = acc[in][im];
             *reinterpret_cast<u32x2_t*>(orow + n) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
     }
@@ -619,18 +633,29 @@ gemm_big_kernel(Params P)
     }
 
     const int n0 = N0 + wn * 16 * TN, m0 = M0 + wm * 16 * TM;
+    if constexpr (TOK) {                           // row scales applied before the guarded stores
+        float ts[TM];
+#pragma unroll
+        for (int im = 0; im < TM; ++im) ts[im] = P.tok_scale[min(m0 + 16 * im + r, P.M - 1)];
+#pragma unroll
+        for (int im = 0; im < TM; ++im) {
+#pragma unroll
+            for (int in = 0; in < TN; ++in) {
+                acc[in][im] = acc[in][im] * ts[im];
+                asm volatile("" : "+v"(acc[in][im]));
+            }
+        }
+    }
 #pragma unroll
     for (int im = 0; im < TM; ++im) {
         const int m = m0 + 16 * im + r;
         if (m >= P.M) continue;
         __bf16* orow = P.Out + (int64_t)m * P.N;
-        const float ts = TOK ? P.tok_scale[m] : 1.f;
 #pragma unroll
         for (int in = 0; in < TN; ++in) {
             const int n = n0 + 16 * in + 4 * j;
             if (n >= P.N) continue;
-            f32x4_t v = acc[in][im];
-            if constexpr (TOK) v = v * ts;
+            const f32x4_t v = acc[in][im];
             *reinterpret_cast<u32x2_t*>(orow + n) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
     }
