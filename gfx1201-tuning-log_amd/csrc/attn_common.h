@@ -65,6 +65,22 @@ __device__ __forceinline__ void v_fragments(const u32x2_t (&vr)[8], u32x4_t (&bf
     }
 }
 
+// The same fragments from bf16 V (no widening): vr[j] = d = 8c .. 8c+7 of k-slot j's token (four
+// dwords, d pair (2w, 2w + 1) in dword w).  v_perm_b32 pairs the two tokens' halves: fragment
+// 2w + h (d row 8c + 2w + h) dword k is (k-slot 2k, k-slot 2k + 1) at that d.
+__device__ __forceinline__ void v_fragments_b16(const u32x4_t (&vr)[8], u32x4_t (&bf)[8])
+{
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t a = vr[2 * k][w], b = vr[2 * k + 1][w];
+            bf[2 * w + 0][k] = __builtin_amdgcn_perm(b, a, 0x05040100u);   // a.lo b.lo
+            bf[2 * w + 1][k] = __builtin_amdgcn_perm(b, a, 0x07060302u);   // a.hi b.hi
+        }
+    }
+}
+
 typedef int v8i __attribute__((ext_vector_type(8)));
 
 // D += A . B^T over 128 k on the block-scaled MFMA with e4m3 A and B (both block scales 1.0):

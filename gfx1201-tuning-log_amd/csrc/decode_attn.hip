@@ -38,11 +38,14 @@
 #include "fp8kv_status.h"
 #include "fp8kv_diag.h"
 #include "attn_common.h"
+#include "kv_chunk.h"
 
 #include <mutex>
 
 namespace fp8kv {
 namespace decode_detail {
+
+using namespace kv_chunk;
 
 constexpr int kD = 128;
 constexpr int kMaxGqa = 16;
@@ -88,209 +91,6 @@ __host__ __device__ inline void split_span(int seqlen, int nsplit, int sp, int& 
     span = (span + 15) & ~15;
     lo = sp * span;
     hi = seqlen < lo + span ? seqlen : lo + span;
-}
-
-// K and V registers of one chunk of NG 16-token groups (lane (r, p) = (lane % 16, lane / 16)):
-//   kr[g][j]: 16 bytes of token c0 + 16 g + r at d = 64 j + 16 p;
-//   vr[G][j]: 8 bytes (d = 8 r .. 8 r + 7) of token c0 + 32 G + 4 p + j (j < 4) or
-//             c0 + 32 G + 16 + 4 p + (j - 4) (j >= 4): the k-slot order of the P^T fragments.
-template <int NG>
-struct ChunkRegs {
-    u32x4_t kr[NG][2];
-    u32x2_t vr[NG / 2][8];
-};
-
-// Per-lane softmax state of one wave: running max and this lane's share of the running sum of
-// head lr (log2 domain), and o[n][i] = head lr at d = 32 lp + 8 i + n.
-struct WaveState {
-    float m_run;
-    float l_run;
-    f32x4_t o[8];
-};
-
-// Block ids of one chunk, one per 16-token group, read with scalar loads (their waits count
-// lgkmcnt and never hold back the K and V loads in flight).  A group that starts at or past hi
-// takes the id of the span's last group (`last`: the start of the 16-token group holding token
-// hi - 1), so every address formed from the ids lies in a block the sequence owns.
-template <int NG>
-struct ChunkIds {
-    int blk[NG];
-};
-
-typedef __attribute__((address_space(4))) const int32_t const_i32_t;   // read-only for the launch
-typedef __attribute__((address_space(4))) const float const_f32_t;
-
-template <int NG>
-__device__ __forceinline__ ChunkIds<NG> load_chunk_ids(const Params& P, const int32_t* btrow, int c0, int last)
-{
-    // The constant address space makes the compiler use scalar loads for these uniform reads,
-    // whatever stores or fences come before them in the kernel.
-    const_i32_t* row = (const_i32_t*)btrow;
-    ChunkIds<NG> ids;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        const int t0 = c0 + 16 * g;
-        ids.blk[g] = row[(t0 < last ? t0 : last) >> P.pshift];
-    }
-    return ids;
-}
-
-// Both chunks' block ids are in registers here: their scalar loads are issued together and
-// waited for once, instead of one round trip per id.
-// (The ids pass through the asm as in/out operands, so every use of them is ordered after it.)
-template <int NG>
-__device__ __forceinline__ void ids_ready(ChunkIds<NG>& a, ChunkIds<NG>& b)
-{
-    static_assert(NG == 2 || NG == 4, "two or four groups per chunk");
-    if constexpr (NG == 2) {
-        asm volatile("" : "+s"(a.blk[0]), "+s"(a.blk[1]), "+s"(b.blk[0]), "+s"(b.blk[1]));
-    } else {
-        asm volatile("" : "+s"(a.blk[0]), "+s"(a.blk[1]), "+s"(a.blk[2]), "+s"(a.blk[3]),
-                          "+s"(b.blk[0]), "+s"(b.blk[1]), "+s"(b.blk[2]), "+s"(b.blk[3]));
-    }
-}
-
-// Keeps the compiler from moving loads issued before it past it (into the branch that uses
-// them), which would undo the software pipeline.
-__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
-
-// Per-lane byte offsets of the chunk loads within one 16-token group (32-bit: the host rejects
-// slot strides that could overflow them).
-struct LaneOffsets {
-    uint32_t k;          // token lr, d = 16 lp
-    uint32_t v[4];       // token 4 lp + i, d = 8 lr
-};
-
-__device__ __forceinline__ LaneOffsets lane_offsets(const Params& P, int lr, int lp)
-{
-    LaneOffsets o;
-    o.k = (uint32_t)lr * (uint32_t)P.sk1 + 16u * (uint32_t)lp;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o.v[i] = (uint32_t)(4 * lp + i) * (uint32_t)P.sv1 + 8u * (uint32_t)lr;
-    return o;
-}
-
-// Request every K and V byte of the chunk starting at token c0 with the same instruction
-// sequence wherever the chunk lies, so the compiler's wait counts stay exact: the group holding hi
-// reads all 16 of its slots (inside its block; tokens >= hi are masked where used), and a group
-// past hi reads one line of the span's last group with every lane (no new traffic).  Group g's
-// base address is scalar (block id from `ids`), the per-lane part a 32-bit offset.  KF requests
-// the K bytes of every group before any V byte, so the S^T MFMAs and the softmax of a chunk can
-// start while its V bytes are still arriving; otherwise K and V alternate per group.
-template <int NG, bool KF>
-__device__ __forceinline__ void issue_chunk(ChunkRegs<NG>& c, const Params& P, const LaneOffsets& lo_,
-                                            const ChunkIds<NG>& ids, int kh, int c0, int hi, int last)
-{
-    auto slot_of = [&](int g) -> int64_t {
-        const int t0 = c0 + 16 * g;
-        return (int64_t)((t0 < last ? t0 : last) & (P.pblk - 1));
-    };
-    auto issue_k = [&](int g) {
-        const uint32_t m = c0 + 16 * g < hi ? ~0u : 0u;
-        const uint8_t* kb = P.k + (int64_t)ids.blk[g] * P.sk0 + slot_of(g) * P.sk1 + (int64_t)kh * P.sk2;
-        c.kr[g][0] = load_nt_16(kb + (lo_.k & m));
-        c.kr[g][1] = load_nt_16(kb + (lo_.k & m) + 64);
-    };
-    auto issue_v = [&](int g) {
-        const uint32_t m = c0 + 16 * g < hi ? ~0u : 0u;
-        const uint8_t* vb = P.v + (int64_t)ids.blk[g] * P.sv0 + slot_of(g) * P.sv1 + (int64_t)kh * P.sv2;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            c.vr[g >> 1][4 * (g & 1) + i] =
-                __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(vb + (lo_.v[i] & m)));
-    };
-    if constexpr (KF) {
-#pragma unroll
-        for (int g = 0; g < NG; ++g) issue_k(g);
-#pragma unroll
-        for (int g = 0; g < NG; ++g) issue_v(g);
-    } else {
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            issue_k(g);
-            issue_v(g);
-        }
-    }
-    issue_fence();
-}
-
-// S^T = K . Q^T, online softmax update, O^T += V^T . P^T for one chunk.
-template <int NG>
-__device__ __forceinline__ void consume_chunk(const ChunkRegs<NG>& c, WaveState& st, const u32x4_t (&qf)[4],
-                                              float qk_scale, int c0, int hi, int lp)
-{
-    // lane (h, p) gets S[token c0 + 16 g + 4 p + i][head h]
-    f32x4_t s[NG];
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mfma16x16x32_bf16(fp8x8_to_bf16x8(c.kr[g][0][0], c.kr[g][0][1]), as_bf16x8(qf[0]), acc);
-        acc = mfma16x16x32_bf16(fp8x8_to_bf16x8(c.kr[g][0][2], c.kr[g][0][3]), as_bf16x8(qf[1]), acc);
-        acc = mfma16x16x32_bf16(fp8x8_to_bf16x8(c.kr[g][1][0], c.kr[g][1][1]), as_bf16x8(qf[2]), acc);
-        acc = mfma16x16x32_bf16(fp8x8_to_bf16x8(c.kr[g][1][2], c.kr[g][1][3]), as_bf16x8(qf[3]), acc);
-        s[g] = acc;
-    }
-    float mc = neg_inf();
-    if (c0 + 16 * NG <= hi) {
-#pragma unroll
-        for (int g = 0; g < NG; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                s[g][i] *= qk_scale;
-                mc = fmaxf(mc, s[g][i]);
-            }
-    } else {
-#pragma unroll
-        for (int g = 0; g < NG; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int tok = c0 + 16 * g + 4 * lp + i;
-                const float x = tok < hi ? s[g][i] * qk_scale : neg_inf();
-                s[g][i] = x;
-                mc = fmaxf(mc, x);
-            }
-    }
-    mc = max_xor16_32(mc);
-    const float m_new = fmaxf(st.m_run, mc);
-    const float m_use = m_new == neg_inf() ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(st.m_run - m_use);
-    float psum = 0.f;
-#pragma unroll
-    for (int g = 0; g < NG; ++g)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float pv = __builtin_amdgcn_exp2f(s[g][i] - m_use);
-            s[g][i] = pv;
-            psum += pv;
-        }
-    st.l_run = st.l_run * alpha + psum;
-    st.m_run = m_new;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) st.o[n] *= alpha;
-#pragma unroll
-    for (int G = 0; G < NG / 2; ++G) {
-        u32x4_t pb;
-        pb[0] = pack_bf16x2(s[2 * G][0], s[2 * G][1]);
-        pb[1] = pack_bf16x2(s[2 * G][2], s[2 * G][3]);
-        pb[2] = pack_bf16x2(s[2 * G + 1][0], s[2 * G + 1][1]);
-        pb[3] = pack_bf16x2(s[2 * G + 1][2], s[2 * G + 1][3]);
-        // V bytes of tokens >= hi are stale cache slots (possibly NaN codes): zero them so that
-        // P = 0 contributes nothing.
-        u32x2_t vv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) vv[j] = c.vr[G][j];
-        if (c0 + 16 * NG > hi) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int tok = c0 + 32 * G + (j < 4 ? 4 * lp + j : 16 + 4 * lp + (j - 4));
-                if (tok >= hi) vv[j] = (u32x2_t){0u, 0u};
-            }
-        }
-        u32x4_t va[8];
-        v_fragments(vv, va);
-#pragma unroll
-        for (int n = 0; n < 8; ++n) st.o[n] = mfma16x16x32_bf16(as_bf16x8(va[n]), as_bf16x8(pb), st.o[n]);
-    }
 }
 
 // Final merge of up to SMAX split records in one round trip: every o value a thread needs (its
@@ -365,9 +165,10 @@ __device__ __forceinline__ void merge_all(const Params& P, const float* recs, in
 // preloading, so the hardware places them in SGPRs before the first instruction, and the sequence
 // length (the head of the dependent chain seq_lens -> block ids -> K/V) and the query row are
 // requested together with the rest of P instead of after it.
-template <int W, int NG, int DEPTH, bool KF>
-__global__ void __launch_bounds__(W * 64)
-decode_kernel(const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, Params P)
+// The kernel body, for e4m3 (B16 = false) or bf16 K/V caches.
+template <int W, int NG, int DEPTH, bool KF, bool B16>
+__device__ __forceinline__ void decode_body(const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl,
+                                            const Params& P)
 {
     // The two loads go out together with the loads of every argument the block-id, Q and K/V
     // requests need (the asm takes all of them, so one wait covers them all) rather than after
@@ -433,8 +234,9 @@ decode_kernel(const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ 
         qf[2] = load_16(qrow + 64 + 16 * lp);
         qf[3] = load_16(qrow + 64 + 16 * lp + 8);
     }
-    const float qk_scale = P.sm_scale * *(const_f32_t*)P.k_scale * kLog2e;
-    const float vs = *(const_f32_t*)P.v_scale;
+    // bf16 caches carry no scales (the reference ignores k_scale and v_scale for them).
+    const float qk_scale = B16 ? P.sm_scale * kLog2e : P.sm_scale * *(const_f32_t*)P.k_scale * kLog2e;
+    const float vs = B16 ? 1.f : *(const_f32_t*)P.v_scale;
 
     WaveState st;
     st.m_run = neg_inf();
@@ -443,15 +245,15 @@ decode_kernel(const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ 
     for (int n = 0; n < 8; ++n) st.o[n] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 
     if (c_first < hi) {
-        const LaneOffsets lofs = lane_offsets(P, lr, lp);
-        ChunkRegs<NG> ca;
-        [[maybe_unused]] ChunkRegs<NG> cb;
+        const LaneOffsets lofs = lane_offsets<B16>(P, lr, lp);
+        ChunkRegs<NG, B16> ca;
+        [[maybe_unused]] ChunkRegs<NG, B16> cb;
         int c0 = c_first;
         if constexpr (DEPTH == 1) {
             do {
                 const ChunkIds<NG> ia = load_chunk_ids<NG>(P, btrow, c0, last);
-                issue_chunk<NG, KF>(ca, P, lofs, ia, kh, c0, hi, last);
-                consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
+                issue_chunk<NG, KF, B16>(ca, P, lofs, ia, kh, c0, hi, last);
+                consume_chunk<NG, B16>(ca, st, qf, qk_scale, c0, hi - 1, c0 + CH > hi, hi, lp);
                 c0 += stride;
             } while (c0 < hi);
         } else {
@@ -461,15 +263,15 @@ decode_kernel(const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ 
             // reads one broadcast line per instruction and is not used.
             do {
                 ids_ready(ia, ib);
-                issue_chunk<NG, KF>(ca, P, lofs, ia, kh, c0, hi, last);
-                issue_chunk<NG, KF>(cb, P, lofs, ib, kh, c0 + stride, hi, last);
+                issue_chunk<NG, KF, B16>(ca, P, lofs, ia, kh, c0, hi, last);
+                issue_chunk<NG, KF, B16>(cb, P, lofs, ib, kh, c0 + stride, hi, last);
                 if (c0 + 2 * stride < hi) {            // the next pair's ids, a round trip ahead
                     ia = load_chunk_ids<NG>(P, btrow, c0 + 2 * stride, last);
                     ib = load_chunk_ids<NG>(P, btrow, c0 + 3 * stride, last);
                 }
-                consume_chunk<NG>(ca, st, qf, qk_scale, c0, hi, lp);
+                consume_chunk<NG, B16>(ca, st, qf, qk_scale, c0, hi - 1, c0 + CH > hi, hi, lp);
                 if (c0 + stride >= hi) break;
-                consume_chunk<NG>(cb, st, qf, qk_scale, c0 + stride, hi, lp);
+                consume_chunk<NG, B16>(cb, st, qf, qk_scale, c0 + stride, hi - 1, c0 + stride + CH > hi, hi, lp);
                 c0 += 2 * stride;
             } while (c0 < hi);
         }
@@ -627,6 +429,22 @@ decode_kernel(const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ 
         __hip_atomic_store(P.counters + ticket_slot(pair), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+template <int W, int NG, int DEPTH, bool KF>
+__global__ void __launch_bounds__(W * 64)
+decode_kernel(const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, Params P)
+{
+    decode_body<W, NG, DEPTH, KF, false>(seq_lens, qsl, P);
+}
+
+// bf16 K/V caches: the same kernel with twice the bytes per chunk and no widening (the reference's
+// K_FP8 = False branch, vllm-fp8kv/fp8kv_v3.py:44-45,61-66,110).
+template <int W, int NG, int DEPTH, bool KF>
+__global__ void __launch_bounds__(W * 64)
+decode_bf16kv_kernel(const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, Params P)
+{
+    decode_body<W, NG, DEPTH, KF, true>(seq_lens, qsl, P);
+}
+
 inline size_t counters_bytes() { return (size_t)kMaxPairs * sizeof(uint32_t); }
 
 inline size_t scratch_bytes(int ns, int hq, int hkv, int nsplit)
@@ -697,17 +515,18 @@ int launch_scratch_zero(void* p, size_t bytes, hipStream_t st)
 }
 
 // Checks the arguments and fills P (scratch pointers excluded); returns the scratch bytes the
-// call needs through `need`.
+// call needs through `need`.  Cache strides are in elements of elem_bytes bytes (1: e4m3, 2: bf16,
+// whose calls need no scales).
 int decode_setup(Params& P, const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
                  int64_t sk0, int64_t sk1, int64_t sk2, int64_t sv0, int64_t sv1, int64_t sv2, void* out,
                  int64_t out_row_stride, const int32_t* query_start_loc, const int32_t* seq_lens,
                  const int32_t* block_table, int64_t bt_stride, const float* k_scale, const float* v_scale,
                  float sm_scale, int num_seqs, int num_q_heads, int num_kv_heads, int head_size, int block_size,
-                 int num_splits, size_t& need)
+                 int num_splits, size_t& need, int elem_bytes = 1)
 {
-    if (!q || !k_cache || !v_cache || !out || !query_start_loc || !seq_lens || !block_table ||
-        !k_scale || !v_scale)
+    if (!q || !k_cache || !v_cache || !out || !query_start_loc || !seq_lens || !block_table)
         return FP8KV_ERR_ARG;
+    if (elem_bytes == 1 && (!k_scale || !v_scale)) return FP8KV_ERR_ARG;
     if (num_seqs < 1 || num_kv_heads < 1 || num_q_heads < 1 || block_size < 1 || num_splits < 1 ||
         num_splits > kMaxSplits || bt_stride < 0)
         return FP8KV_ERR_ARG;
@@ -717,11 +536,15 @@ int decode_setup(Params& P, const void* q, int64_t q_row_stride, const void* k_c
     const int gqa = num_q_heads / num_kv_heads;
     if (gqa > kMaxGqa) return FP8KV_ERR_SHAPE;
     if (block_size < 16 || (block_size & (block_size - 1)) != 0) return FP8KV_ERR_SHAPE;
-    // K rows are read with 16-byte loads and V rows with 8-byte loads; q with 16-byte loads.
-    if (!aligned(k_cache, 16) || !aligned(v_cache, 8) || !aligned(q, 16) || !aligned(out, 2))
+    // Strides in bytes from here on.  K rows are read with 16-byte loads and V rows with 8-byte
+    // (e4m3) or 16-byte (bf16) loads; q with 16-byte loads.
+    const int64_t vbytes = 8 * elem_bytes;
+    sk0 *= elem_bytes; sk1 *= elem_bytes; sk2 *= elem_bytes;
+    sv0 *= elem_bytes; sv1 *= elem_bytes; sv2 *= elem_bytes;
+    if (!aligned(k_cache, 16) || !aligned(v_cache, (size_t)vbytes) || !aligned(q, 16) || !aligned(out, 2))
         return FP8KV_ERR_ALIGN;
     if ((sk0 | sk1 | sk2) & 15) return FP8KV_ERR_ALIGN;
-    if ((sv0 | sv1 | sv2) & 7) return FP8KV_ERR_ALIGN;
+    if ((sv0 | sv1 | sv2) & (vbytes - 1)) return FP8KV_ERR_ALIGN;
     if (q_row_stride & 7) return FP8KV_ERR_ALIGN;
     // Per-lane offsets within a 16-token group are 32-bit.
     if (sk1 < 0 || sv1 < 0 || sk1 > ((int64_t)1 << 26) || sv1 > ((int64_t)1 << 26)) return FP8KV_ERR_SHAPE;
@@ -757,6 +580,15 @@ void use_scratch(Params& P, void* buf, size_t need)
     if (need == 0) return;
     P.counters = static_cast<uint32_t*>(buf);
     P.part = reinterpret_cast<float*>(static_cast<unsigned char*>(buf) + counters_bytes());
+}
+
+// bf16 caches: the default variant's shape.
+int decode_launch_bf16kv(const Params& P, int num_seqs, hipStream_t st)
+{
+    const dim3 grid((unsigned)P.nsplit, (unsigned)P.hkv, (unsigned)num_seqs);
+    begin_launch();
+    launch_kernel(decode_bf16kv_kernel<8, 2, 2, true>, grid, dim3(8 * 64), 0, st, P.seq_lens, P.qsl, P);
+    return finish_launch();
 }
 
 int decode_launch(const Params& P, int num_seqs, hipStream_t st)
@@ -896,6 +728,31 @@ extern "C" int fp8kv_decode_attn_noalloc(const void* q, int64_t q_row_stride,
     }
     use_scratch(P, ptr, need);
     return decode_launch(P, num_seqs, st);
+}
+
+extern "C" int fp8kv_decode_attn_bf16(const void* q, int64_t q_row_stride,
+                                      const void* k_cache, const void* v_cache,
+                                      int64_t sk0, int64_t sk1, int64_t sk2,
+                                      int64_t sv0, int64_t sv1, int64_t sv2,
+                                      void* out, int64_t out_row_stride,
+                                      const int32_t* query_start_loc, const int32_t* seq_lens,
+                                      const int32_t* block_table, int64_t bt_stride,
+                                      const float* k_scale, const float* v_scale, float sm_scale,
+                                      int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
+                                      int block_size, int num_splits, void* scratch_buf,
+                                      size_t scratch_bytes_given, void* stream)
+{
+    Params P;
+    size_t need = 0;
+    const int rc = decode_setup(P, q, q_row_stride, k_cache, v_cache, sk0, sk1, sk2, sv0, sv1, sv2, out,
+                                out_row_stride, query_start_loc, seq_lens, block_table, bt_stride, k_scale,
+                                v_scale, sm_scale, num_seqs, num_q_heads, num_kv_heads, head_size, block_size,
+                                num_splits, need, 2);
+    if (rc != FP8KV_OK) return rc;
+    if (need > 0 && (!scratch_buf || scratch_bytes_given < need || !aligned(scratch_buf, 256)))
+        return FP8KV_ERR_SCRATCH;
+    use_scratch(P, scratch_buf, need);
+    return decode_launch_bf16kv(P, num_seqs, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" void fp8kv_decode_tune(int variant, int target_wgs)

@@ -43,6 +43,15 @@ SIGNATURES: dict[str, tuple] = {
     "fp8kv_prefill_attn_varlen": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_i64] * 6
                                   + [_c_vp, _c_i64] + [_c_vp] * 3 + [_c_i64] + [_c_vp] * 2 + [_c_f]
                                   + [_c_i] * 6 + [_c_vp]),
+    # the same attention over bf16 K/V caches (csrc/decode_attn.hip, csrc/prefill_bf16kv.hip)
+    "fp8kv_decode_attn_bf16": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_i64] * 6 + [_c_vp, _c_i64]
+                               + [_c_vp] * 3 + [_c_i64] + [_c_vp] * 2 + [_c_f] + [_c_i] * 6
+                               + [_c_vp, _c_sz, _c_vp]),
+    "fp8kv_prefill_attn_bf16": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_i64] * 6 + [_c_vp, _c_i64]
+                                + [_c_vp, _c_i64] + [_c_vp] * 2 + [_c_f] + [_c_i] * 6 + [_c_vp]),
+    "fp8kv_prefill_attn_varlen_bf16": (_c_i, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_i64] * 6
+                                       + [_c_vp, _c_i64] + [_c_vp] * 3 + [_c_i64] + [_c_vp] * 2 + [_c_f]
+                                       + [_c_i] * 6 + [_c_vp]),
     # fp8 KV-cache write (csrc/cache_write.hip)
     "fp8kv_cache_write": (_c_i, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp] + [_c_i64] * 6
                           + [_c_vp] * 3 + [_c_i] * 4 + [_c_vp]),

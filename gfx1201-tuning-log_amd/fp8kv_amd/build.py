@@ -19,8 +19,8 @@ INCLUDE = os.path.join(REPO_ROOT, "include")
 LIB_NAME = "libfp8kv_amd.so"
 LIB_PATH = os.path.join(PKG_ROOT, LIB_NAME)
 
-SOURCES = ["h4mv.hip", "h4mv_repack.hip", "decode_attn.hip", "prefill_attn.hip", "cache_write.hip",
-           "epilogues.hip", "w4a8_gemm.hip", "lm_head.hip", "stream_read.hip"]
+SOURCES = ["h4mv.hip", "h4mv_repack.hip", "decode_attn.hip", "prefill_attn.hip", "prefill_bf16kv.hip",
+           "cache_write.hip", "epilogues.hip", "w4a8_gemm.hip", "lm_head.hip", "stream_read.hip"]
 
 # Packed-fp32 VALU forms are disabled for every HIP file built here (the compiler would otherwise
 # emit v_pk_{add,mul,fma}_f32 from ordinary float code).
@@ -40,6 +40,7 @@ FILE_FLAGS = {
     "w4a8_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "h4mv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
     "decode_attn.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+    "prefill_bf16kv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
 }
 
 

@@ -126,6 +126,10 @@ def decode_scratch_reset(scratch: torch.Tensor) -> None:
     _lib.check("fp8kv_decode_scratch_reset", st)
 
 
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
 def _scale_tensor(x, device) -> torch.Tensor:
     if torch.is_tensor(x):
         _require(x.dtype == torch.float32 and x.numel() >= 1 and x.device == device,
@@ -140,15 +144,30 @@ def _fp8_cache_check(c: torch.Tensor, name: str) -> None:
     _require(c.stride(3) == 1, f"{name} must be contiguous along head_size")
 
 
+def _kv_caches_bf16(k_cache: torch.Tensor, v_cache: torch.Tensor) -> bool:
+    """True for bf16 K/V caches (the reference's K_FP8 = False branch, scales ignored), False for
+    e4m3 ones (float8_e4m3fn or raw uint8); both caches must agree."""
+    if k_cache.dtype == torch.bfloat16 or v_cache.dtype == torch.bfloat16:
+        for c, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+            _require(c.is_cuda and c.dim() == 4 and c.dtype == torch.bfloat16 and c.stride(3) == 1,
+                     f"{n} must be a 4-D bf16 device tensor [NB, PBLK, HKV, D] contiguous along "
+                     "head_size (both caches bf16, or both e4m3)")
+        return True
+    _fp8_cache_check(k_cache, "k_cache")
+    _fp8_cache_check(v_cache, "v_cache")
+    return False
+
+
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                      out: torch.Tensor, query_start_loc: torch.Tensor, seq_lens: torch.Tensor,
                      block_table: torch.Tensor, k_scale, v_scale, sm_scale: float,
                      num_splits: int | None = None, max_seq_len: int | None = None,
                      scratch: torch.Tensor | None = None) -> torch.Tensor:
-    """Paged fp8 decode attention; writes ``out[query_start_loc[s]]`` for every sequence s.
+    """Paged decode attention; writes ``out[query_start_loc[s]]`` for every sequence s.
 
     Contract of vllm-fp8kv/fp8kv_v3.py:116-139 (q [T, HQ, D] bf16, caches [NB, PBLK, HKV, D] fp8
-    views with arbitrary block/slot/head strides, int32 metadata, device fp32 scales).
+    views with arbitrary block/slot/head strides, int32 metadata, device fp32 scales).  bf16
+    caches take the reference's K_FP8 = False branch (fp8kv_v3.py:135): the scales are ignored.
     ``num_splits`` defaults to the library's plan for ``max_seq_len`` (read from ``seq_lens`` when
     not given, which synchronises).  ``scratch`` defaults to a per-device cached buffer.
     """
@@ -157,8 +176,7 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     _require(out.dtype == torch.bfloat16 and out.dim() == 3 and out.stride(2) == 1
              and out.stride(1) == out.shape[2] and out.shape[1:] == q.shape[1:],
              "out must be bf16 [T, HQ, D] with contiguous heads")
-    _fp8_cache_check(k_cache, "k_cache")
-    _fp8_cache_check(v_cache, "v_cache")
+    bf16_kv = _kv_caches_bf16(k_cache, v_cache)
     for t, n in ((query_start_loc, "query_start_loc"), (seq_lens, "seq_lens"),
                  (block_table, "block_table")):
         _require(t.dtype == torch.int32 and t.is_cuda, f"{n} must be an int32 device tensor")
@@ -168,8 +186,8 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     HKV = k_cache.shape[2]
     PBLK = k_cache.shape[1]
     dev = q.device
-    ks = _scale_tensor(k_scale, dev)
-    vs = _scale_tensor(v_scale, dev)
+    ks = None if bf16_kv else _scale_tensor(k_scale, dev)
+    vs = None if bf16_kv else _scale_tensor(v_scale, dev)
     if num_splits is None:
         if max_seq_len is None:
             max_seq_len = int(seq_lens.max().item()) if NS > 0 else 0
@@ -182,15 +200,16 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                  f"scratch needs {need} bytes")
     sbytes = 0 if scratch is None else scratch.numel() * scratch.element_size()
     lib = _lib.load()
-    st = lib.fp8kv_decode_attn(
+    name = "fp8kv_decode_attn_bf16" if bf16_kv else "fp8kv_decode_attn"
+    st = getattr(lib, name)(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
         v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
         out.data_ptr(), out.stride(0), query_start_loc.data_ptr(), seq_lens.data_ptr(),
-        block_table.data_ptr(), block_table.stride(0), ks.data_ptr(), vs.data_ptr(),
+        block_table.data_ptr(), block_table.stride(0), _ptr(ks), _ptr(vs),
         float(sm_scale), NS, HQ, HKV, D, PBLK, int(num_splits),
         None if scratch is None else scratch.data_ptr(), sbytes, _stream_ptr(q))
-    _lib.check("fp8kv_decode_attn", st)
+    _lib.check(name, st)
     return out
 
 
@@ -202,10 +221,10 @@ def _prefill_common(q, k_cache, v_cache, out, block_table):
     _require(out.dtype == torch.bfloat16 and out.dim() == 3 and out.stride(2) == 1
              and out.stride(1) == out.shape[2] and out.shape[1:] == q.shape[1:],
              "out must be bf16 [T, HQ, D] with contiguous heads")
-    _fp8_cache_check(k_cache, "k_cache")
-    _fp8_cache_check(v_cache, "v_cache")
+    bf16_kv = _kv_caches_bf16(k_cache, v_cache)
     _require(block_table.dtype == torch.int32 and block_table.is_cuda and block_table.dim() == 2
              and block_table.stride(1) == 1, "block_table must be int32 [NS, max_blocks] on the device")
+    return bf16_kv
 
 
 def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -215,20 +234,22 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
 
     Contract of vllm-fp8kv/fp8kv_prefill.py:124-144 run(q, k_cache, v_cache, out, bt, kscale,
     vscale, sm_scale, q0, qlen): block-table row 0 holds the sequence, scales are device fp32.
+    bf16 caches take the reference's K_FP8 = False branch (fp8kv_prefill.py:143): no scales.
     """
-    _prefill_common(q, k_cache, v_cache, out, block_table)
+    bf16_kv = _prefill_common(q, k_cache, v_cache, out, block_table)
     _require(0 <= qlen <= q.shape[0] and qlen <= out.shape[0] and q0 >= 0, "bad q0 / qlen")
     dev = q.device
-    ks = _scale_tensor(k_scale, dev)
-    vs = _scale_tensor(v_scale, dev)
-    st = _lib.load().fp8kv_prefill_attn(
+    ks = None if bf16_kv else _scale_tensor(k_scale, dev)
+    vs = None if bf16_kv else _scale_tensor(v_scale, dev)
+    name = "fp8kv_prefill_attn_bf16" if bf16_kv else "fp8kv_prefill_attn"
+    st = getattr(_lib.load(), name)(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
         v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
         out.data_ptr(), out.stride(0), block_table.data_ptr(), block_table.stride(0),
-        ks.data_ptr(), vs.data_ptr(), float(sm_scale), q.shape[1], k_cache.shape[2], q.shape[2],
+        _ptr(ks), _ptr(vs), float(sm_scale), q.shape[1], k_cache.shape[2], q.shape[2],
         k_cache.shape[1], int(q0), int(qlen), _stream_ptr(q))
-    _lib.check("fp8kv_prefill_attn", st)
+    _lib.check(name, st)
     return out
 
 
@@ -242,7 +263,7 @@ def prefill_attention_varlen(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
     tokens (new ones included), so its q0 is seq_lens[s] - qlen_s; block_table row s maps it.
     ``max_query_len`` sizes the grid (read from ``cu_seqlens_q`` when not given, which syncs).
     """
-    _prefill_common(q, k_cache, v_cache, out, block_table)
+    bf16_kv = _prefill_common(q, k_cache, v_cache, out, block_table)
     for t, n in ((cu_seqlens_q, "cu_seqlens_q"), (seq_lens, "seq_lens")):
         _require(t.dtype == torch.int32 and t.is_cuda, f"{n} must be an int32 device tensor")
     NS = block_table.shape[0]
@@ -250,17 +271,18 @@ def prefill_attention_varlen(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
     if max_query_len is None:
         max_query_len = int((cu_seqlens_q[1:] - cu_seqlens_q[:-1]).max().item()) if NS else 0
     dev = q.device
-    ks = _scale_tensor(k_scale, dev)
-    vs = _scale_tensor(v_scale, dev)
-    st = _lib.load().fp8kv_prefill_attn_varlen(
+    ks = None if bf16_kv else _scale_tensor(k_scale, dev)
+    vs = None if bf16_kv else _scale_tensor(v_scale, dev)
+    name = "fp8kv_prefill_attn_varlen_bf16" if bf16_kv else "fp8kv_prefill_attn_varlen"
+    st = getattr(_lib.load(), name)(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
         v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
         out.data_ptr(), out.stride(0), cu_seqlens_q.data_ptr(), seq_lens.data_ptr(),
-        block_table.data_ptr(), block_table.stride(0), ks.data_ptr(), vs.data_ptr(),
+        block_table.data_ptr(), block_table.stride(0), _ptr(ks), _ptr(vs),
         float(sm_scale), NS, q.shape[1], k_cache.shape[2], q.shape[2], k_cache.shape[1],
         int(max_query_len), _stream_ptr(q))
-    _lib.check("fp8kv_prefill_attn_varlen", st)
+    _lib.check(name, st)
     return out
 
 

@@ -43,6 +43,18 @@ def _make_cache(nb: int, pblk: int, hkv: int, d: int, g: torch.Generator, layout
                 kv_gen: str = "amax"):
     k = torch.randn(nb, pblk, hkv, d, generator=g)
     v = torch.randn(nb, pblk, hkv, d, generator=g)
+    if kv_gen == "bf16":
+        # bf16 caches, stored as they are (the reference's K_FP8 = False branch: no scales)
+        kb, vb = k.to(torch.bfloat16), v.to(torch.bfloat16)
+        if layout == "standalone":
+            return kb, vb, None, 1.0, 1.0
+        if layout == "engine":
+            kv = torch.empty(nb, hkv, pblk, 2 * d, dtype=torch.bfloat16)
+            kv[..., :d] = kb.transpose(1, 2)
+            kv[..., d:] = vb.transpose(1, 2)
+            kc, vc = engine_views(kv, d)
+            return kc, vc, kv, 1.0, 1.0
+        raise ValueError(layout)
     if kv_gen == "amax":
         kq, ks = quantize_per_tensor(k)
         vq, vs = quantize_per_tensor(v)
@@ -82,9 +94,12 @@ def engine_pool_amax(nb: int, hkv: int, pblk: int, d: int, generator: torch.Gene
 
 
 def engine_views(kv_cache: torch.Tensor, head_size: int):
-    """The K and V fp8 views the attention hook builds (vllm-fp8kv/fp8kv_override.py:82-85)."""
+    """The K and V fp8 views the attention hook builds (vllm-fp8kv/fp8kv_override.py:82-85); a
+    bf16 pool gives bf16 views."""
     kc = kv_cache.transpose(1, 2)
     key_cache, value_cache = kc.split(head_size, dim=-1)
+    if kv_cache.dtype == torch.bfloat16:
+        return key_cache, value_cache
     return key_cache.view(torch.float8_e4m3fn), value_cache.view(torch.float8_e4m3fn)
 
 

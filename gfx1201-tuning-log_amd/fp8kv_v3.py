@@ -10,7 +10,8 @@ ignored (the HIP kernel's tiling is fixed).  ``nsplit`` is the number of context
 rounding; ``None`` lets the library plan it from the longest context).  ``scratch`` is a
 zero-initialised uint8 device buffer of at least ``fp8kv_amd.ops.decode_scratch_bytes`` bytes, or
 None for a per-device cached one (the reference's (o, m, l) float tuple is also accepted and
-replaced by the cached buffer, since the partial layout differs).
+replaced by the cached buffer, since the partial layout differs).  bf16 caches take the
+reference's K_FP8 = False branch (fp8kv_v3.py:135): ``fp8kv_decode_attn_bf16``, scales ignored.
 """
 from __future__ import annotations
 

@@ -202,6 +202,55 @@ int fp8kv_prefill_attn_varlen(const void* q, int64_t q_row_stride,
                               int block_size, int max_query_len, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * The same attention over bf16 K/V caches (the reference's K_FP8 = False branch): K and V are
+ * used as stored and the scales do not apply,
+ *
+ *   decode:  out[qsl[s], h, :] = bf16( softmax_t( q . K_t * sm_scale ) . V_t )
+ *   prefill: out[i, h, :]      = bf16( softmax_{t <= q0 + i}( q[i, h, :] . K_t * sm_scale ) . V_t )
+ *
+ * k_scale and v_scale are accepted for a signature identical to the e4m3 entry points and ignored
+ * (NULL allowed).  Cache strides are in bf16 elements (the caches' torch strides), each a multiple
+ * of 8, caches 16-byte aligned; slot strides at most 2^25 elements.  Everything else (layouts,
+ * geometry limits, scratch and its reset for decode, varlen metadata) as for the e4m3 entry points.
+ *
+ * Replace: vllm-fp8kv/fp8kv_v3.py:116-139 run() with a bf16 cache (K_FP8 = k_cache.dtype !=
+ * torch.bfloat16 at :135,139; the kernels' bf16 branches at :44-45,61-66,110) and
+ * vllm-fp8kv/fp8kv_prefill.py:124-144 run() with a bf16 cache (:143; kernel branches :57-60,
+ * 77-82,117).  The varlen entry point extends the latter as fp8kv_prefill_attn_varlen does. */
+int fp8kv_decode_attn_bf16(const void* q, int64_t q_row_stride,
+                           const void* k_cache, const void* v_cache,
+                           int64_t sk0, int64_t sk1, int64_t sk2,
+                           int64_t sv0, int64_t sv1, int64_t sv2,
+                           void* out, int64_t out_row_stride,
+                           const int32_t* query_start_loc, const int32_t* seq_lens,
+                           const int32_t* block_table, int64_t bt_stride,
+                           const float* k_scale, const float* v_scale, float sm_scale,
+                           int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
+                           int block_size, int num_splits, void* scratch, size_t scratch_bytes,
+                           void* stream);
+
+int fp8kv_prefill_attn_bf16(const void* q, int64_t q_row_stride,
+                            const void* k_cache, const void* v_cache,
+                            int64_t sk0, int64_t sk1, int64_t sk2,
+                            int64_t sv0, int64_t sv1, int64_t sv2,
+                            void* out, int64_t out_row_stride,
+                            const int32_t* block_table, int64_t bt_stride,
+                            const float* k_scale, const float* v_scale, float sm_scale,
+                            int num_q_heads, int num_kv_heads, int head_size, int block_size,
+                            int q0, int qlen, void* stream);
+
+int fp8kv_prefill_attn_varlen_bf16(const void* q, int64_t q_row_stride,
+                                   const void* k_cache, const void* v_cache,
+                                   int64_t sk0, int64_t sk1, int64_t sk2,
+                                   int64_t sv0, int64_t sv1, int64_t sv2,
+                                   void* out, int64_t out_row_stride,
+                                   const int32_t* cu_seqlens_q, const int32_t* seq_lens,
+                                   const int32_t* block_table, int64_t bt_stride,
+                                   const float* k_scale, const float* v_scale, float sm_scale,
+                                   int num_seqs, int num_q_heads, int num_kv_heads, int head_size,
+                                   int block_size, int max_query_len, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * fp8-e4m3 KV-cache write: quantise new K and V rows and scatter them into the paged cache.
  *
  *   k_cache[block, slot, h, d] = e4m3fn( float(key[i, h, d]) / k_scale )   (V likewise)

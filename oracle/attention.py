@@ -9,6 +9,8 @@ strides, so both the standalone ``[NB, PBLK, HKV, D]`` tensor and the engine's t
 K|V-interleaved view (vllm-fp8kv/fp8kv_override.py:82-85) are accepted as torch views.
 fp8 values are decoded with the e4m3fn table (exact), k_scale folds into the score scale and
 v_scale multiplies the output (fp8kv_v3.py:43-45,110-111; fp8kv_prefill.py:57-58,117-118).
+bf16 caches (the reference's K_FP8 = False branch, fp8kv_v3.py:44-45,61-66,110,135 and
+fp8kv_prefill.py:57-60,77-82,117,143) are used as stored and both scales are ignored.
 
   * ``decode_attention``  - fp8kv_v3.py:3-113 semantics; the reference's own oracle is
     fp8kv_v3.py:158-177 (also fp8kv_kernel.py:109-122, profiling/mb_stock.py:41-53).
@@ -27,7 +29,10 @@ v_scale * mean(V); torch's scaled_dot_product_attention (fp64, explicit causal m
 gathered dequantised cache; a brute-force pure-Python loop on a tiny case; the scale fold
 checked against pre-scaled K/V; block-table permutation invariance; decode == the last row of a
 prefill over the same context; varlen == independent per-sequence runs; planted mistakes
-(k_scale dropped, off-by-one causal mask, wrong GQA head mapping) failing those checks.
+(k_scale dropped, off-by-one causal mask, wrong GQA head mapping) failing those checks.  bf16
+caches: SDPA on the stored values with the scales left out, a bf16 cache holding an e4m3 cache's
+values times power-of-two scales reproducing the e4m3 path exactly, and a planted use of the
+scales failing the SDPA check.
 """
 from __future__ import annotations
 
@@ -48,14 +53,21 @@ def _as_u8(cache: torch.Tensor) -> torch.Tensor:
 
 def gather_kv(cache: torch.Tensor, bt_row: torch.Tensor, ctx: int, kh: int,
               dtype: torch.dtype = torch.float64) -> torch.Tensor:
-    """Dequantised (unscaled) [ctx, D] rows of kv head ``kh`` for tokens 0..ctx-1."""
-    c = _as_u8(cache)
-    pblk = c.shape[1]
+    """Dequantised (unscaled) [ctx, D] rows of kv head ``kh`` for tokens 0..ctx-1 (bf16 caches:
+    the stored values)."""
+    pblk = cache.shape[1]
     t = torch.arange(ctx)
     blk = bt_row.long()[t // pblk]
     slot = t % pblk
-    codes = c[blk, slot, kh, :]                                    # [ctx, D] uint8
+    if cache.dtype == torch.bfloat16:
+        return cache[blk, slot, kh, :].to(dtype)
+    codes = _as_u8(cache)[blk, slot, kh, :]                        # [ctx, D] uint8
     return _E4M3_T.to(dtype)[codes.long()]
+
+
+def _scales(cache: torch.Tensor, k_scale: float, v_scale: float) -> tuple[float, float]:
+    """The scales that apply: none for bf16 caches (fp8kv_v3.py:44-45,110; fp8kv_prefill.py:57-60,117)."""
+    return (1.0, 1.0) if cache.dtype == torch.bfloat16 else (k_scale, v_scale)
 
 
 def _attend(qh: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, v_scale: float,
@@ -78,6 +90,7 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     HQ, D = q.shape[1], q.shape[2]
     HKV = k_cache.shape[2]
     gqa = HQ // HKV
+    k_scale, v_scale = _scales(k_cache, k_scale, v_scale)
     out = torch.zeros(NS, HQ, D, dtype=dtype)
     for s in range(NS):
         ctx = int(seq_lens[s])
@@ -99,6 +112,7 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     HQ, D = q.shape[1], q.shape[2]
     HKV = k_cache.shape[2]
     gqa = HQ // HKV
+    k_scale, v_scale = _scales(k_cache, k_scale, v_scale)
     ctx = q0 + qlen
     pos = torch.arange(qlen) + q0
     out = torch.empty(qlen, HQ, D, dtype=dtype)

@@ -89,6 +89,21 @@ def test_decode_rejects_before_launch(lib, kw, code):
     assert lib.fp8kv_decode_attn(*_decode_args(**kw)) == code
 
 
+@pytest.mark.parametrize("kw,code", [
+    (dict(q=0), 1), (dict(hd=64), 2), (dict(hq=25), 2), (dict(pblk=8), 2),
+    (dict(k=A + 8), 3), (dict(v=A + 8), 3),                  # bf16 V rows are 16-byte loads
+    (dict(sk1=4 * 128 + 4), 3), (dict(sv2=4), 3),            # strides in elements, multiples of 8
+    (dict(sk1=1 << 26), 2),                                  # slot stride above 2^25 elements
+    (dict(ks=None, vs=None, nsplit=8), 5),                   # no scales needed: reaches the scratch check
+])
+def test_decode_bf16_rejects_before_launch(lib, kw, code):
+    assert lib.fp8kv_decode_attn_bf16(*_decode_args(**kw)) == code
+
+
+def test_decode_e4m3_needs_scales(lib):
+    assert lib.fp8kv_decode_attn(*_decode_args(ks=None)) == 1
+
+
 def test_decode_scratch_sizing(lib):
     assert lib.fp8kv_decode_scratch_bytes(8, 24, 4, 128, 1) == 0
     b = lib.fp8kv_decode_scratch_bytes(8, 24, 4, 128, 8)
@@ -170,6 +185,37 @@ def test_prefill_varlen_rejects_before_launch(lib, changes, code):
 
 def test_prefill_varlen_zero_query_is_a_no_op(lib):
     assert lib.fp8kv_prefill_attn_varlen(*PFV_OK) == 0
+
+
+# The bf16 entry points on the engine layout [NB, HKV, PBLK, 2D] of bf16 (strides in elements, the V
+# view 128 elements = 256 bytes in); qlen = 0 / max_query_len = 0 return before any launch.
+PFB_OK = [A, 24 * 128, A, A + 256, 16384, 256, 4096, 16384, 256, 4096, A, 24 * 128, A, 64, None, None,
+          0.088, 24, 4, 128, 16, 0, 0, None]
+
+
+@pytest.mark.parametrize("changes,code", [
+    ({0: None}, 1), ({12: None}, 1), ({21: -1}, 1), ({19: 64}, 2), ({17: 25}, 2), ({20: 8}, 2),
+    ({2: A + 8}, 3), ({3: A + 8}, 3), ({5: 260}, 3), ({8: 260}, 3), ({1: 24 * 128 + 4}, 3),
+    ({5: 1 << 26}, 2), ({5: -256}, 2),
+])
+def test_prefill_bf16_rejects_before_launch(lib, changes, code):
+    args = list(PFB_OK)
+    for k, v in changes.items():
+        args[k] = v
+    assert lib.fp8kv_prefill_attn_bf16(*args) == code
+
+
+def test_prefill_bf16_takes_no_scales(lib):
+    assert lib.fp8kv_prefill_attn_bf16(*PFB_OK) == 0
+
+
+def test_prefill_varlen_bf16_rejects_before_launch(lib):
+    base = PFB_OK[:12] + [A, A] + PFB_OK[12:14] + [None, None, 0.088, 2, 24, 4, 128, 16, 0, None]
+    assert lib.fp8kv_prefill_attn_varlen_bf16(*base) == 0
+    for idx, val, code in [(12, None, 1), (19, 0, 1), (24, -1, 1), (19, 65536, 2), (3, A + 8, 3)]:
+        args = list(base)
+        args[idx] = val
+        assert lib.fp8kv_prefill_attn_varlen_bf16(*args) == code, (idx, val)
 
 
 def test_prefill_accepts_largest_32_bit_block_offsets(lib):

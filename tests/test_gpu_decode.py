@@ -277,16 +277,65 @@ def test_merge_is_independent_of_the_merging_split():
         assert torch.equal(_run(c, num_splits=8), a)
 
 
-def test_bf16_caches_are_rejected_not_misread():
-    """The reference's run() also takes bf16 caches (K_FP8 = False, vllm-fp8kv/fp8kv_v3.py:61-66);
-    this build reads e4m3 bytes only and refuses them before launching anything."""
+# ---- bf16 caches (the reference's K_FP8 = False branch, vllm-fp8kv/fp8kv_v3.py:44-45,61-66,110,135):
+# fp8kv_decode_attn_bf16, values used as stored, scales ignored.
+
+@pytest.mark.parametrize("layout", ["standalone", "engine"])
+@pytest.mark.parametrize("num_splits", [None, 1, 3, 8, 33])
+def test_bf16_kv_batch(layout, num_splits):
+    """bf16 K/V, 8 sequences of mixed length (edge lengths included), both cache layouts; the scales
+    passed (0.5, 2.0) must play no part."""
+    c = workloads.decode_case([1, 15, 16, 17, 100, 511, 2048, 3001], pool_blocks=400, seed=21,
+                              layout=layout, kv_gen="bf16")
+    ref = attention.decode_attention(c["q"], c["k_cache"], c["v_cache"], c["qsl"], c["seq_lens"],
+                                     c["block_table"], 1.0, 1.0, c["sm_scale"])
+    got = _rows(c, _run(c, ks=0.5, vs=2.0, num_splits=num_splits))
+    torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (16, 4), (32, 8), (16, 1), (28, 4)])
+def test_bf16_kv_head_geometries(hq, hkv):
+    c = workloads.decode_case([700, 64, 2500], HQ=hq, HKV=hkv, pool_blocks=300, seed=hq + hkv,
+                              kv_gen="bf16")
+    torch.testing.assert_close(_rows(c, _run(c)), _oracle(c), rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("pblk", [32, 64])
+def test_bf16_kv_block_sizes(pblk):
+    c = workloads.decode_case([1000, 77], PBLK=pblk, seed=pblk, kv_gen="bf16", layout="engine")
+    torch.testing.assert_close(_rows(c, _run(c)), _oracle(c), rtol=RTOL, atol=ATOL)
+
+
+def test_bf16_kv_b8_4k_and_zero_context():
+    """b8@4k over a 5060-block bf16 pool, plus a batch whose first sequence has no context (zeros)."""
+    c = workloads.decode_case([4096] * 8, pool_blocks=5060, seed=22, layout="engine", kv_gen="bf16")
+    torch.testing.assert_close(_rows(c, _run(c)), _oracle(c), rtol=RTOL, atol=ATOL)
+    c = workloads.decode_case([0, 300], seed=23, kv_gen="bf16")
+    got = _rows(c, _run(c))
+    assert torch.count_nonzero(got[0]) == 0
+    torch.testing.assert_close(got, _oracle(c), rtol=RTOL, atol=ATOL)
+
+
+def test_bf16_kv_through_the_reference_run():
+    """fp8kv_v3.run (the reference's signature) takes bf16 caches as the reference does."""
     import fp8kv_v3
-    c = workloads.decode_case([64, 100], seed=20)
+    c = workloads.decode_case([64, 100], seed=20, kv_gen="bf16")
     d = workloads.to_device(c, DEV)
-    kb = d["k_cache"].view(torch.uint8).to(torch.bfloat16)
-    vb = d["v_cache"].view(torch.uint8).to(torch.bfloat16)
     out = torch.full_like(d["q"], 5.0)
-    with pytest.raises(ValueError, match="float8_e4m3fn"):
-        fp8kv_v3.run(d["q"], kb, vb, out, d["qsl"], d["seq_lens"], d["block_table"], 1.0, 1.0, c["sm_scale"])
+    fp8kv_v3.run(d["q"], d["k_cache"], d["v_cache"], out, d["qsl"], d["seq_lens"], d["block_table"],
+                 0.3, 7.0, c["sm_scale"])
+    torch.cuda.synchronize()
+    torch.testing.assert_close(_rows(c, out), _oracle(c), rtol=RTOL, atol=ATOL)
+
+
+def test_mixed_cache_dtypes_are_rejected():
+    """K bf16 with V e4m3 (or the reverse) is refused before anything is launched."""
+    c = workloads.decode_case([64], seed=24)
+    d = workloads.to_device(c, DEV)
+    kb = d["k_cache"].to(torch.bfloat16)
+    out = torch.full_like(d["q"], 5.0)
+    with pytest.raises(ValueError, match="both caches bf16"):
+        ops.decode_attention(d["q"], kb, d["v_cache"], out, d["qsl"], d["seq_lens"], d["block_table"],
+                             1.0, 1.0, c["sm_scale"])
     torch.cuda.synchronize()
     assert torch.all(out == 5.0)

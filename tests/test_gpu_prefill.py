@@ -116,8 +116,10 @@ def test_rows_beyond_qlen_untouched_and_deterministic():
 
 # --- varlen -------------------------------------------------------------------------------------
 
-def _check_varlen(qlens, q0s, seed, HQ=24, HKV=4, layout="standalone", dtype=torch.float64):
-    c = workloads.prefill_case(qlens, q0s, HQ=HQ, HKV=HKV, seed=seed, layout=layout)
+def _check_varlen(qlens, q0s, seed, HQ=24, HKV=4, layout="standalone", dtype=torch.float64,
+                  kv_gen="amax", PBLK=16):
+    c = workloads.prefill_case(qlens, q0s, HQ=HQ, HKV=HKV, seed=seed, layout=layout, kv_gen=kv_gen,
+                               PBLK=PBLK)
     d = workloads.to_device(c, DEV)
     out = torch.full_like(d["q"], 7.0)
     ops.prefill_attention_varlen(d["q"], d["k_cache"], d["v_cache"], out, d["cu_seqlens_q"],
@@ -274,3 +276,57 @@ def test_cascade_shared_prefix_batch(layout):
                                              c["seq_lens"], c["block_table"], c["k_scale"], c["v_scale"],
                                              c["sm_scale"])
     torch.testing.assert_close(out.cpu().to(torch.float64), ref.to(torch.float64), rtol=RTOL, atol=ATOL)
+
+
+# ---- bf16 caches (the reference's K_FP8 = False branch, vllm-fp8kv/fp8kv_prefill.py:57-60,77-82,
+# 117,143): fp8kv_prefill_attn_bf16 / _varlen_bf16, values used as stored, scales ignored.
+
+@pytest.mark.parametrize("hq,hkv", [(24, 4), (32, 8)])
+@pytest.mark.parametrize("qlen,q0", [(2048, 0), (850, 2048), (256, 3840), (512, 0)])
+def test_bf16_kv_reference_cases(hq, hkv, qlen, q0):
+    """The reference's four prefill cases (prefill_test.py:95-98) over bf16 caches; the scales
+    passed (0.5, 2.0) must play no part."""
+    c = workloads.prefill_case([qlen], [q0], HQ=hq, HKV=hkv, seed=qlen + q0 + 5, kv_gen="bf16")
+    got = _run_single(c, q0, qlen, ks=0.5, vs=2.0)[:qlen].to(torch.float64)
+    ref = _oracle_single(c, q0, qlen, 1.0, 1.0).to(torch.float64)
+    torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("gqa", [1, 2, 3, 4, 6, 7, 8, 12, 16])
+def test_bf16_kv_every_gqa(gqa):
+    """Up to 8 query heads per workgroup, two head groups above 8; a tail block and odd lengths."""
+    _check_single(161, 45, HQ=4 * gqa, HKV=4, seed=gqa + 90, kv_gen="bf16")
+    _check_single(33, 0, HQ=2 * gqa, HKV=2, seed=gqa + 91, kv_gen="bf16", layout="engine")
+
+
+@pytest.mark.parametrize("qlen,q0", [(1, 0), (1, 700), (16, 0), (17, 15), (300, 1)])
+def test_bf16_kv_edge_lengths(qlen, q0):
+    _check_single(qlen, q0, seed=qlen * 7 + q0, kv_gen="bf16")
+
+
+@pytest.mark.parametrize("PBLK", [32, 64, 128])
+def test_bf16_kv_block_sizes(PBLK):
+    _check_single(700, 600, seed=PBLK + 3, PBLK=PBLK, layout="engine", kv_gen="bf16")
+
+
+def test_bf16_kv_varlen():
+    _check_varlen([5, 100, 33, 512, 1], [0, 7, 1000, 3, 250], seed=93, kv_gen="bf16")
+    _check_varlen([512] * 4, [0] * 4, seed=94, layout="engine", kv_gen="bf16", PBLK=32)
+
+
+def test_bf16_kv_config3_full_size():
+    """configs[3] over bf16 caches: 2048 new tokens after 2048 cached, 24/4 heads."""
+    _check_single(2048, 2048, seed=95, layout="engine", kv_gen="bf16")
+
+
+def test_bf16_kv_through_the_reference_run():
+    """fp8kv_prefill.run (the reference's signature) takes bf16 caches as the reference does."""
+    import fp8kv_prefill
+    c = workloads.prefill_case([200], [100], seed=96, kv_gen="bf16")
+    d = workloads.to_device(c, DEV)
+    out = torch.full_like(d["q"], 7.0)
+    fp8kv_prefill.run(d["q"], d["k_cache"], d["v_cache"], out, d["block_table"], 0.3, 5.0,
+                      c["sm_scale"], 100, 200)
+    torch.cuda.synchronize()
+    ref = _oracle_single(c, 100, 200).to(torch.float64)
+    torch.testing.assert_close(out.cpu().to(torch.float64), ref, rtol=RTOL, atol=ATOL)

@@ -323,6 +323,64 @@ def test_prefill_matches_sdpa_and_row0():
         assert torch.equal(out[0, h], c["v_cache"][blk, 0, h // 3].to(torch.float64) * 2.0)
 
 
+# ---- bf16 caches: the reference's K_FP8 = False branch (vllm-fp8kv/fp8kv_v3.py:44-45,61-66,110;
+# fp8kv_prefill.py:57-60,77-82,117): values used as stored, k_scale and v_scale ignored.
+
+def _bf16_case(layout="standalone", ctx=(37, 5, 20), seed=4):
+    from fp8kv_amd import workloads
+    return workloads.decode_case(ctx, HQ=6, HKV=2, D=16, PBLK=4, pool_blocks=24, seed=seed,
+                                 layout=layout, kv_gen="bf16")
+
+
+@pytest.mark.parametrize("layout", ["standalone", "engine"])
+def test_bf16_decode_matches_sdpa_without_scales(layout):
+    c = _bf16_case(layout)
+    assert c["k_cache"].dtype == torch.bfloat16
+    out = attention.decode_attention(c["q"], c["k_cache"], c["v_cache"], c["qsl"], c["seq_lens"],
+                                     c["block_table"], 0.5, 2.0, c["sm_scale"])   # scales ignored
+    for s in range(3):
+        ctx = int(c["seq_lens"][s])
+        ref = _sdpa_reference(c["q"][s:s + 1], c["k_cache"], c["v_cache"], c["block_table"][s],
+                              1.0, 1.0, c["sm_scale"], ctx - 1, 1)
+        torch.testing.assert_close(out[s], ref[0], rtol=1e-12, atol=1e-12)
+
+
+def test_bf16_prefill_matches_sdpa_without_scales():
+    from fp8kv_amd import workloads
+    c = workloads.prefill_case([19], [7], HQ=6, HKV=2, D=16, PBLK=4, pool_blocks=8, seed=5, kv_gen="bf16")
+    out = attention.prefill_attention(c["q"], c["k_cache"], c["v_cache"], c["block_table"][0],
+                                      0.25, 3.0, c["sm_scale"], 7, 19)
+    ref = _sdpa_reference(c["q"], c["k_cache"], c["v_cache"], c["block_table"][0], 1.0, 1.0,
+                          c["sm_scale"], 7, 19)
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_bf16_cache_of_scaled_e4m3_values_equals_the_e4m3_path():
+    """A bf16 cache holding an e4m3 cache's values times power-of-two scales (exact in bf16) gives
+    what the e4m3 path gives with those scales; the bf16 call's own scales play no part."""
+    c = _small_case(seed=6)
+    ks, vs = 0.5, 4.0
+    k16 = (c["k_cache"].to(torch.float64) * ks).to(torch.bfloat16)
+    v16 = (c["v_cache"].to(torch.float64) * vs).to(torch.bfloat16)
+    assert torch.equal(k16.to(torch.float64), c["k_cache"].to(torch.float64) * ks)
+    a = attention.decode_attention(c["q"], c["k_cache"], c["v_cache"], c["qsl"], c["seq_lens"],
+                                   c["block_table"], ks, vs, c["sm_scale"])
+    b = attention.decode_attention(c["q"], k16, v16, c["qsl"], c["seq_lens"], c["block_table"],
+                                   123.0, 0.01, c["sm_scale"])
+    torch.testing.assert_close(a, b, rtol=1e-13, atol=0)
+
+
+def test_bf16_planted_scale_use_fails_the_pin(monkeypatch):
+    """An oracle that applied the scales to bf16 caches fails the SDPA pin above."""
+    monkeypatch.setattr(attention, "_scales", lambda cache, ks, vs: (ks, vs))
+    c = _bf16_case()
+    out = attention.decode_attention(c["q"], c["k_cache"], c["v_cache"], c["qsl"], c["seq_lens"],
+                                     c["block_table"], 0.5, 2.0, c["sm_scale"])
+    ref = _sdpa_reference(c["q"][0:1], c["k_cache"], c["v_cache"], c["block_table"][0], 1.0, 1.0,
+                          c["sm_scale"], int(c["seq_lens"][0]) - 1, 1)
+    assert not torch.allclose(out[0], ref[0], rtol=1e-6, atol=1e-6)
+
+
 def test_prefill_continuation_matches_sdpa():
     from fp8kv_amd import workloads
     c = workloads.prefill_case([11], [13], HQ=6, HKV=2, D=16, PBLK=4, pool_blocks=8, seed=4,
