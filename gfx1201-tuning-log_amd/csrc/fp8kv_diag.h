@@ -38,6 +38,10 @@ void fp8kv_decode_tune(int variant, int target_wgs);
  * token blocks (r, n16 - 1 - r) at any grid size, or -1 for the per-GQA default. */
 void fp8kv_prefill_tune(int shape);
 
+/* bf16-KV prefill: query heads per wave (1 or 2); any other value restores the default (two where
+ * GQA > 1, else one). */
+void fp8kv_prefill_bf16_tune(int heads_per_wave);
+
 /* Planner query of the prefill attention launch (host only, no GPU call): the plan the entry
  * points would launch for this shape under the current tuning hook.  ctx_hint is the longest
  * context (q0 + qlen) for fp8kv_prefill_attn and max_query_len for the varlen entry point.

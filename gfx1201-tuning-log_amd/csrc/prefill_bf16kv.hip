@@ -6,10 +6,11 @@
 // gfx950 design (the engine's caches are fp8, so this path serves callers of the reference's
 // run() with bf16 caches; it uses the decode kernel's register-direct chunk loads rather than the
 // fp8 prefill kernels' LDS tile rings):
-//   * one workgroup per (16-token block, kv head, group of up to 8 query heads, sequence); wave w
-//     owns head 8 y + w of its block, i.e. one row-set of 16 queries, and streams every key the
-//     block sees (q0 + 16 b + 16, capped at the context) through kv_chunk: 32-key chunks straight
-//     into MFMA fragments, two chunks in flight, the next pair's block ids a round trip ahead;
+//   * one workgroup per (16-token block, kv head, group of up to 16 query heads, sequence); each
+//     wave owns two query heads of its block (one for MHA), i.e. two row-sets of 16 queries that
+//     share every K/V load, and streams every key the block sees (q0 + 16 b + 16, capped at the
+//     context) through kv_chunk: 32-key chunks straight into MFMA fragments, the next chunk's
+//     block ids a round trip ahead;
 //   * S^T = K . Q^T and O^T = V^T . P^T on v_mfma_f32_16x16x32_bf16 with the query token in
 //     lane % 16 (the rescale is lane-local); the causal mask applies only to chunks that reach
 //     past the block's first query position;
@@ -17,6 +18,7 @@
 //     waits for another: there is no LDS and no barrier.
 #include "fp8kv_common.h"
 #include "fp8kv_status.h"
+#include "fp8kv_diag.h"
 #include "attn_common.h"
 #include "kv_chunk.h"
 
@@ -27,7 +29,7 @@ using namespace kv_chunk;
 
 constexpr int kD = 128;
 constexpr int kMaxGqa = 16;
-constexpr int kHeadsPerWG = 8;
+constexpr int kWavesPerWG = 8;
 constexpr int kNG = 2;                         // 16-token groups per chunk
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -47,7 +49,8 @@ struct Params {
     int q0_host, qlen_host;
 };
 
-__global__ void __launch_bounds__(kHeadsPerWG * 64)
+template <int RS>
+__global__ void __launch_bounds__(kWavesPerWG * 64)
 prefill_bf16kv_kernel(Params P)
 {
     constexpr int CH = 16 * kNG;
@@ -58,8 +61,10 @@ prefill_bf16kv_kernel(Params P)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15;
     const int lp = lane >> 4;
-    const int g = blockIdx.y * kHeadsPerWG + wave;                 // query head within the kv head
-    if (g >= P.gqa) return;                                        // no barriers: waves are independent
+    // query heads (within the kv head) g0 .. g0 + RS - 1 of this wave; past gqa: head g0 again,
+    // computed and not stored
+    const int g0 = (blockIdx.y * kWavesPerWG + wave) * RS;
+    if (g0 >= P.gqa) return;                                       // no barriers: waves are independent
 
     int q_begin, qlen, q0;
     if (P.cu_q) {
@@ -82,57 +87,64 @@ prefill_bf16kv_kernel(Params P)
 
     // Q^T fragments of this lane's query row (rows past qlen read the last row again; their
     // results are not stored): d = 16 lp + 0..15 and 64 + 16 lp + 0..15.
-    u32x4_t qf[4];
-    {
+    u32x4_t qf[RS][4];
+    WaveState st[RS];
+#pragma unroll
+    for (int j = 0; j < RS; ++j) {
+        const int g = g0 + j < P.gqa ? g0 + j : g0;
         const __bf16* qrow = P.q + (int64_t)(q_begin + (tok_ok ? tok : qlen - 1)) * P.q_stride +
                              (int64_t)(kh * P.gqa + g) * kD;
-        qf[0] = load_16(qrow + 16 * lp);
-        qf[1] = load_16(qrow + 16 * lp + 8);
-        qf[2] = load_16(qrow + 64 + 16 * lp);
-        qf[3] = load_16(qrow + 64 + 16 * lp + 8);
+        qf[j][0] = load_16(qrow + 16 * lp);
+        qf[j][1] = load_16(qrow + 16 * lp + 8);
+        qf[j][2] = load_16(qrow + 64 + 16 * lp);
+        qf[j][3] = load_16(qrow + 64 + 16 * lp + 8);
+        st[j].m_run = neg_inf();
+        st[j].l_run = 0.f;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) st[j].o[n] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     }
     const float qk_scale = P.sm_scale * kLog2e;
-
-    WaveState st;
-    st.m_run = neg_inf();
-    st.l_run = 0.f;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) st.o[n] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 
     const int32_t* btrow = P.bt + (int64_t)seq * P.bt_stride;
     const int last = (k_hi - 1) & ~15;
     const LaneOffsets lofs = lane_offsets<true>(P, lr, lp);
+    // One chunk in flight; the next chunk's block ids go out before this chunk is consumed.  (Two
+    // chunks in flight measured slower: 408 against 377 us at configs[3] with one head per wave,
+    // and two heads per wave then spill.)
     ChunkIds<kNG> ia = load_chunk_ids<kNG>(P, btrow, 0, last);
     ChunkIds<kNG> ib = load_chunk_ids<kNG>(P, btrow, CH, last);
-    ChunkRegs<kNG, true> ca, cb;
+    ChunkRegs<kNG, true> ca;
     int c0 = 0;
     do {
         ids_ready(ia, ib);
         issue_chunk<kNG, true, true>(ca, P, lofs, ia, kh, c0, k_hi, last);
-        issue_chunk<kNG, true, true>(cb, P, lofs, ib, kh, c0 + CH, k_hi, last);
-        if (c0 + 2 * CH < k_hi) {                  // the next pair's ids, a round trip ahead
-            ia = load_chunk_ids<kNG>(P, btrow, c0 + 2 * CH, last);
-            ib = load_chunk_ids<kNG>(P, btrow, c0 + 3 * CH, last);
-        }
-        consume_chunk<kNG, true>(ca, st, qf, qk_scale, c0, qpos, c0 + CH - 1 > qpos0, k_hi, lp);
-        if (c0 + CH >= k_hi) break;
-        consume_chunk<kNG, true>(cb, st, qf, qk_scale, c0 + CH, qpos, c0 + 2 * CH - 1 > qpos0, k_hi, lp);
-        c0 += 2 * CH;
+        ia = ib;
+        if (c0 + 2 * CH < k_hi) ib = load_chunk_ids<kNG>(P, btrow, c0 + 2 * CH, last);
+#pragma unroll
+        for (int j = 0; j < RS; ++j)
+            consume_chunk<kNG, true>(ca, st[j], qf[j], qk_scale, c0, qpos, c0 + CH - 1 > qpos0, k_hi, lp);
+        c0 += CH;
     } while (c0 < k_hi);
 
     // o[n][i] is this lane's query at d = 32 lp + 8 i + n: one 16-byte store per i.
-    const float l = sum_xor16_32(st.l_run);
-    if (!tok_ok) return;
-    const float f = l > 0.f ? 1.f / l : 0.f;
-    __bf16* orow = P.out + (int64_t)(q_begin + tok) * P.o_stride + (int64_t)(kh * P.gqa + g) * kD + 32 * lp;
+    float l[RS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        u32x4_t w;
-        w[0] = pack_bf16x2(st.o[0][i] * f, st.o[1][i] * f);
-        w[1] = pack_bf16x2(st.o[2][i] * f, st.o[3][i] * f);
-        w[2] = pack_bf16x2(st.o[4][i] * f, st.o[5][i] * f);
-        w[3] = pack_bf16x2(st.o[6][i] * f, st.o[7][i] * f);
-        *reinterpret_cast<u32x4_t*>(orow + 8 * i) = w;
+    for (int j = 0; j < RS; ++j) l[j] = sum_xor16_32(st[j].l_run);
+    if (!tok_ok) return;
+#pragma unroll
+    for (int j = 0; j < RS; ++j) {
+        if (g0 + j >= P.gqa) break;
+        const float f = l[j] > 0.f ? 1.f / l[j] : 0.f;
+        __bf16* orow = P.out + (int64_t)(q_begin + tok) * P.o_stride + (int64_t)(kh * P.gqa + g0 + j) * kD + 32 * lp;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            u32x4_t w;
+            w[0] = pack_bf16x2(st[j].o[0][i] * f, st[j].o[1][i] * f);
+            w[1] = pack_bf16x2(st[j].o[2][i] * f, st[j].o[3][i] * f);
+            w[2] = pack_bf16x2(st[j].o[4][i] * f, st[j].o[5][i] * f);
+            w[3] = pack_bf16x2(st[j].o[6][i] * f, st[j].o[7][i] * f);
+            *reinterpret_cast<u32x4_t*>(orow + 8 * i) = w;
+        }
     }
 }
 
@@ -178,14 +190,24 @@ int setup(Params& P, const void* q, int64_t q_row_stride, const void* k_cache, c
     return FP8KV_OK;
 }
 
+// Heads per wave: two wherever GQA > 1, so both row-sets use one set of K/V loads (configs[3]:
+// 222 against 377 us with one head per wave; 1024 over 1024: 98.7 against 122.6 us); one for MHA.
+int g_rs_override = 0;
+
 int launch(Params& P, int num_seqs, int max_query_len, hipStream_t stream)
 {
     P.n16_grid = (max_query_len + 15) / 16;
-    const int groups = (P.gqa + kHeadsPerWG - 1) / kHeadsPerWG;
-    const int waves = P.gqa < kHeadsPerWG ? P.gqa : kHeadsPerWG;
+    const int rs = g_rs_override ? g_rs_override : (P.gqa > 1 ? 2 : 1);
+    const int wave_heads = kWavesPerWG * rs;
+    const int groups = (P.gqa + wave_heads - 1) / wave_heads;
+    const int waves_needed = (P.gqa + rs - 1) / rs;
+    const int waves = waves_needed < kWavesPerWG ? waves_needed : kWavesPerWG;
     const dim3 grid((unsigned)(P.n16_grid * P.hkv), (unsigned)groups, (unsigned)num_seqs);
     begin_launch();
-    launch_kernel(prefill_bf16kv_kernel, grid, dim3(64 * waves), 0, stream, P);
+    if (rs == 2)
+        launch_kernel(prefill_bf16kv_kernel<2>, grid, dim3(64 * waves), 0, stream, P);
+    else
+        launch_kernel(prefill_bf16kv_kernel<1>, grid, dim3(64 * waves), 0, stream, P);
     return finish_launch();
 }
 
@@ -246,4 +268,10 @@ extern "C" int fp8kv_prefill_attn_varlen_bf16(const void* q, int64_t q_row_strid
     P.cu_q = cu_seqlens_q;
     P.seq_lens = seq_lens;
     return launch(P, num_seqs, max_query_len, reinterpret_cast<hipStream_t>(stream));
+}
+
+// Sweeps and tests: query heads per wave (1 or 2); any other value restores the default.
+extern "C" void fp8kv_prefill_bf16_tune(int heads_per_wave)
+{
+    g_rs_override = (heads_per_wave == 1 || heads_per_wave == 2) ? heads_per_wave : 0;
 }

@@ -299,6 +299,17 @@ def test_bf16_kv_every_gqa(gqa):
     _check_single(33, 0, HQ=2 * gqa, HKV=2, seed=gqa + 91, kv_gen="bf16", layout="engine")
 
 
+@pytest.mark.parametrize("gqa", [3, 6, 16])
+def test_bf16_kv_one_head_per_wave(gqa):
+    """The one-head-per-wave kernel (the MHA default) forced at GQA > 1."""
+    lib = _lib.load()
+    try:
+        lib.fp8kv_prefill_bf16_tune(1)
+        _check_single(161, 45, HQ=4 * gqa, HKV=4, seed=gqa + 97, kv_gen="bf16")
+    finally:
+        lib.fp8kv_prefill_bf16_tune(0)
+
+
 @pytest.mark.parametrize("qlen,q0", [(1, 0), (1, 700), (16, 0), (17, 15), (300, 1)])
 def test_bf16_kv_edge_lengths(qlen, q0):
     _check_single(qlen, q0, seed=qlen * 7 + q0, kv_gen="bf16")
