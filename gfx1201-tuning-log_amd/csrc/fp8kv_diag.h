@@ -6,8 +6,8 @@
 extern "C" {
 #endif
 
-/* Enumerate every global and LDS address the MXFP4 matvec's LDS kernel (K-slice or streaming,
- * whichever the planner picks) would touch for (N, K, M) and check it against the operand sizes
+/* Enumerate every global and LDS address the MXFP4 matvec's LDS kernel (M = 1, K-slice or
+ * streaming, whichever the planner picks) would touch for (N, K, M) and check it against the operand sizes
  * and the LDS allocation.
  * 0 = all in bounds, 1 = the shape uses the register-path kernel instead, >= 2 = violation id. */
 int fp8kv_h4mv_audit(int N, int K, int M);
@@ -25,6 +25,13 @@ void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode);
  * workgroups = workgroup count the planner aims for (0: default).  Affects later launches and
  * audits. */
 void fp8kv_h4mv_kslice_tune(int mode, int depth, int order, int workgroups);
+
+/* Tuning hook for the matvec's M = 1 kernel (e2m1 codes on the block-scaled MFMA, activations as
+ * e4m3 hi + lo): mode 0 = used at M = 1 when N / 16 >= 1024 tiles (the default), 1 = whenever the
+ * shape allows it (M = 1, K % 512 == 0), 2 = never; depth = LDS ring slots per wave (3; any other
+ * value: 2, the default); workgroups = workgroup count the planner aims for (0: default 256).
+ * Affects later launches and audits. */
+void fp8kv_h4mv_m1_tune(int mode, int depth, int workgroups);
 
 /* Tuning hook for sweeps of the decode attention launch: kernel variant index (0..6; any other
  * value, e.g. -1, selects the default, variant 4: 8 waves, chunks of 2 groups of 16 keys, 2 chunks

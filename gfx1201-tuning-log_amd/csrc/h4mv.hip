@@ -647,6 +647,237 @@ h4mv_kslice_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// M = 1 kernel: the codes go to the block-scaled MFMA as stored, the activation row as e4m3 hi + lo.
+//
+// At M = 1 the bf16 path widens every code to bf16 (64 v_cvt_scalef32_pk_bf16_fp4 per lane and
+// 512-k step) for 16x16x32 MFMAs of which one column is used; measured with the copies alone
+// (the same bytes, addresses and waits, no arithmetic), that work costs about 1.5 us of a cfg1
+// launch.  Here A of v_mfma_scale_f32_16x16x128_f8f6f4 is the e2m1 codes straight from the ring
+// (cbsz 4) with the rows' e8m0 group scales as the MFMA's A scales, and B is the activation row
+// in two e4m3 columns: per block of 32 k, x * 2^e = hi + lo, where 2^e puts the block's largest
+// |x| in [128, 256), hi is x * 2^e rounded to 4 significant bits and lo the remainder, and 2^-e
+// is the block's B scale.  The remainder of a bf16 value is exact in e4m3 whenever |x| >= 2^-9
+// of its block's largest (below that lo keeps what the e4m3 subnormals hold), so column 0 plus
+// column 1 of the product is sum_k w_k x_k up to the accumulation order: the bf16 path's result.
+//   * a workgroup of TW waves owns the tiles b + w G (wave w, G workgroups), one wave per tile
+//     over all of K, each streaming 4 KB code steps through its own DEPTH-slot ring after a
+//     one-time copy of its scale slice (the streaming kernel's copy addresses and LDS placement);
+//   * the workgroup converts the activation row once: the row is copied into LDS first (ahead of
+//     the rings and the scale slices, and as copies, not register loads, which would make the
+//     compiler wait for every copy in flight before using them); once each wave has its own row
+//     pieces (a wait that leaves its ring and scale copies in flight), one barrier, then thread t
+//     converts 8 bf16 (a quarter of a 32-k block; a block's quarters sit in four consecutive
+//     lanes, which take their common maximum with two DPP steps) and writes its 8 hi and 8 lo
+//     bytes and the block's scale byte, while the first code steps are in flight; a second
+//     barrier publishes them.  A wave without a tile copies its workgroup's first tile (its reads
+//     meet wave 0's in L2), so every wave issues the same copies and all waits are exact; it
+//     leaves after the second barrier;
+//   * non-finite activations: NaN stays NaN through e4m3; a block holding an infinity gets the
+//     NaN scale byte 0xFF, so every output is NaN (the reference gives +-inf or NaN there);
+//   * step s: four MFMAs of 128 k.  Lane (n, j) = (lane % 16, lane / 16) supplies A row n's
+//     group 4u + j (16 bytes from the ring, its scale byte shifted to the bottom), B column n's
+//     k 16j .. 16j + 15 and 64 + 16j .. + 15 (hi for even n, lo for odd n: columns >= 2 repeat
+//     them and are never stored) and the B scale of block j, four MFMAs' scales in one dword
+//     picked with op_sel;
+//   * lane (c, q) ends with rows 4q .. 4q + 3 of column c; one DPP exchange adds column 1 to
+//     column 0 and store_tile writes them (with the SiLU-and-mul stage for h4mv_silu_mul).
+// ---------------------------------------------------------------------------------------------
+constexpr int kM1MaxWaves = 16;
+constexpr int kM1Workgroups = 512;             // two workgroups per CU when their LDS allows it
+constexpr int kM1MinTiles = 1024;              // default: when the tiles alone fill the GPU
+constexpr int kM1MaxSteps = 64;                // K <= 32768
+constexpr int kM1MaxScaleCopies = kM1MaxSteps / 4;   // 16 nsteps / 64 copies of the scale slice
+
+// LDS bytes of the activation row: hi [K], lo [K], scale bytes [K / 32] (rounded to 16).
+__host__ __device__ inline int m1_x_bytes(int K) { return 2 * K + (((K >> 5) + 15) & ~15); }
+// Scale area of a wave: 16 rows x nsteps x 16 B, rounded up to whole 64-lane copies (1 KB).
+__host__ __device__ inline int m1_scale_bytes(int nsteps) { return 16 * ((16 * nsteps + 63) & ~63); }
+__host__ __device__ inline int m1_wave_bytes(int depth, int nsteps)
+{
+    return depth * kStepCodeBytes + m1_scale_bytes(nsteps);
+}
+// LDS byte of block b's B scale: the 16 blocks of a step are stored so that dword j holds blocks
+// j, 4 + j, 8 + j, 12 + j (byte u = block 4u + j, the scale lane j supplies to MFMA u).
+__host__ __device__ inline int m1_xe_pos(int b)
+{
+    const int c = b & 15;
+    return (b & ~15) + 4 * (c & 3) + (c >> 2);
+}
+// s_waitcnt vmcnt(n) for 0 <= n <= A.
+template <int A>
+__device__ __forceinline__ void m1_wait_n(int n)
+{
+    if constexpr (A == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (n >= A) wait_vmcnt<A>();
+        else m1_wait_n<A - 1>(n);
+    }
+}
+
+// s_waitcnt vmcnt(4 ahead) for 0 <= ahead <= A (four code copies per step).
+template <int A>
+__device__ __forceinline__ void m1_wait(int ahead)
+{
+    if constexpr (A == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (ahead >= A) wait_vmcnt<4 * A>();
+        else m1_wait<A - 1>(ahead);
+    }
+}
+
+typedef int m1_v8i __attribute__((ext_vector_type(8)));
+
+template <int U>
+__device__ __forceinline__ f32x4_t m1_mfma(const u32x4_t& w, const m1_v8i& b, uint32_t sa, uint32_t sb, f32x4_t acc)
+{
+    const m1_v8i a = {(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc, 4, 0, 0, (int)sa, U, (int)sb);
+}
+
+__device__ __forceinline__ float m1_quad_max(float v)
+{
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));   // quad_perm 1,0,3,2
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true))); // quad_perm 2,3,0,1
+}
+
+template <int DEPTH, typename OutT, int EPI>
+__global__ void __launch_bounds__(64 * kM1MaxWaves)
+h4mv_m1_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
+               const __bf16* __restrict__ X, OutT* __restrict__ Out, int N, int K)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    const int T = (N + kRowsPerWG - 1) / kRowsPerWG;
+    const int nsteps = K >> 9;
+
+    unsigned char* xh = smem;                                   // hi bytes, k order
+    unsigned char* xl = smem + K;                               // lo bytes
+    unsigned char* xe = smem + 2 * K;                           // B scale bytes (m1_xe_pos)
+    unsigned char* xs = smem + m1_x_bytes(K);                   // the bf16 row as loaded
+    unsigned char* ring = xs + 2 * K + wave * m1_wave_bytes(DEPTH, nsteps);
+    unsigned char* sarea = ring + DEPTH * kStepCodeBytes;
+
+    const int tile_w = blockIdx.x + wave * gridDim.x;
+    const bool has_tile = tile_w < T;                           // wave-uniform
+    const int tile = has_tile ? tile_w : blockIdx.x;
+    const int n0 = tile * kRowsPerWG;
+
+    // ---- the activation row, the scale slice, then the ring: all copies straight to LDS --------
+    // (register loads of the row would make the compiler wait for every copy before using them)
+    const int np = K >> 3;                                      // 16-byte pieces of the row
+    for (int p0 = wave * 64; p0 < np; p0 += nwaves * 64)
+        if (p0 + lane < np) dma16_to_lds(X + 8 * (p0 + lane), xs + 16 * p0);
+    uint32_t woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) woff[i] = stream_w_lane_off(n0, N, K, lane, i);
+    const uint8_t* wtile = W + (size_t)n0 * (size_t)(K >> 1);
+    auto issue = [&](int s, unsigned char* slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(wtile + (size_t)s * (kStepGroups * 16) + woff[i]),
+                                             (lds_void_t*)(slot + i * 1024), 16, 0, kDmaAux);
+    };
+    // step 0, the scale slice, then the rest of the ring: the first barrier waits for the row
+    // only, and step 0's wait covers the scales.  Every slot is filled (a slice shorter than the
+    // ring fetches its last step again into slots it never reads) and every scale copy is issued
+    // by all lanes, so the copy counts are exact.
+    issue(0, ring);
+    const int nseg = 16 * nsteps;
+    for (int t0 = 0; t0 < nseg; t0 += 64) {
+        const int t = min(t0 + lane, nseg - 1);
+        dma16_to_lds(St + stream_s_seg_off(n0, N, K, nsteps, 0, t), sarea + t0 * 16);
+    }
+#pragma unroll
+    for (int s = 1; s < DEPTH; ++s) issue(min(s, nsteps - 1), ring + s * kStepCodeBytes);
+    m1_wait_n<4 * DEPTH + kM1MaxScaleCopies>(4 * DEPTH + (nseg + 63) / 64);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");    // every wave's row pieces landed
+
+    // ---- activation row -> e4m3 hi / lo and block scales ----------------------------------------
+    for (int g0 = 0; g0 < np; g0 += nwaves * 64) {
+        const int gr = g0 + (int)threadIdx.x;
+        const int g = gr < np ? gr : np - 4 + (gr & 3);         // a quad past the end redoes the last block
+        const u32x4_t xw = *reinterpret_cast<const u32x4_t*>(xs + 16 * g);
+        float v[8];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            v[2 * c] = __uint_as_float(xw[c] << 16);
+            v[2 * c + 1] = __uint_as_float(xw[c] & 0xFFFF0000u);
+        }
+        float amax = 0.f;                          // fmaxf drops NaN: NaN values stay out of the max
+#pragma unroll
+        for (int c = 0; c < 8; ++c) amax = fmaxf(amax, fabsf(v[c]));
+        amax = m1_quad_max(amax);
+        const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xFFu;
+        int be = 261 - (int)eb;                    // biased exponent of 2^e = 2^(7 - floor(log2 amax))
+        be = be < 1 ? 1 : (be > 253 ? 253 : be);
+        const float scale = __uint_as_float((uint32_t)be << 23);
+        uint32_t hw[2], lw[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float x[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[c] = v[4 * h + c] * scale;
+            uint32_t a = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+            a = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], (int)a, true);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, true);
+            uint32_t b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0] - h01[0], x[1] - h01[1], 0, false);
+            b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2] - h23[0], x[3] - h23[1], (int)b, true);
+            hw[h] = a;
+            lw[h] = b;
+        }
+        *reinterpret_cast<u32x2_t*>(xh + 8 * g) = (u32x2_t){hw[0], hw[1]};
+        *reinterpret_cast<u32x2_t*>(xl + 8 * g) = (u32x2_t){lw[0], lw[1]};
+        xe[m1_xe_pos(g >> 2)] = (unsigned char)(eb == 255u ? 255 : 254 - be);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (!has_tile) {
+        wait_vmcnt<0>();                           // its copies land before the wave leaves
+        return;
+    }
+
+    // ---- stream ------------------------------------------------------------------------------
+    int rdoff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rdoff[u] = stream_w_read_off(r, q, u);
+    const unsigned char* xcol = ((r & 1) ? xl : xh) + 16 * q;
+    f32x4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < nsteps; ++s) {
+        unsigned char* sl = ring + (s % DEPTH) * kStepCodeBytes;
+        m1_wait<DEPTH - 1>(min(nsteps - 1 - s, DEPTH - 1));
+        const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(sarea + (r * nsteps + s) * 16);
+        u32x4_t wv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wv[u] = *reinterpret_cast<const u32x4_t*>(sl + rdoff[u]);
+        m1_v8i b[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(xcol + 512 * s + 128 * u);
+            const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(xcol + 512 * s + 128 * u + 64);
+            b[u] = (m1_v8i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+        const uint32_t sb = *reinterpret_cast<const uint32_t*>(xe + 16 * s + 4 * q);
+        __builtin_amdgcn_s_waitcnt(0xC07F);                 // lgkmcnt(0): the slot is free again
+        if (s + DEPTH < nsteps) issue(s + DEPTH, sl);
+        c0 = m1_mfma<0>(wv[0], b[0], sv[0] >> (8 * q), sb, c0);
+        c1 = m1_mfma<1>(wv[1], b[1], sv[1] >> (8 * q), sb, c1);
+        c0 = m1_mfma<2>(wv[2], b[2], sv[2] >> (8 * q), sb, c0);
+        c1 = m1_mfma<3>(wv[3], b[3], sv[3] >> (8 * q), sb, c1);
+    }
+    f32x4_t acc = c0 + c1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)                                 // column 0 (hi) + column 1 (lo)
+        acc[i] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc[i]), 0xB1, 0xF, 0xF, true));
+    store_tile<OutT, EPI>(acc, Out, tile, N, 1, r, q);
+}
+
 // Waves per tile: enough tiles x waves to cover the GPU, at most 16 per workgroup and at most one
 // per step.
 inline int stream_waves(int N, int K, int target_waves, int rt)
@@ -864,6 +1095,62 @@ void launch_kslice(const KsPlan& p, const void* W, const void* St, const void* X
 #undef FP8KV_KS
 }
 
+// M = 1 planner (tunables: fp8kv_h4mv_m1_tune).  mode 0: used for M = 1 when the tiles alone fill
+// the GPU (>= kM1MinTiles); 1: whenever the shape allows it; 2: never.
+int g_m1_mode = 0;
+int g_m1_depth = 0;
+int g_m1_wgs = 0;               // workgroups the planner aims for (0: kM1Workgroups)
+
+struct M1Plan {
+    int tw, grid, depth;
+    size_t lds;
+};
+
+inline bool m1_plan(int N, int K, int M, M1Plan& p)
+{
+    if (g_m1_mode == 2 || M != 1 || (K & 511) != 0 || (K >> 9) > kM1MaxSteps) return false;
+    const int T = (N + kRowsPerWG - 1) / kRowsPerWG;
+    if (g_m1_mode == 0 && T < kM1MinTiles) return false;
+    const int nsteps = K >> 9;
+    // Default: the fewest tiles per workgroup that still run every workgroup in one round, at two
+    // workgroups per CU (one per CU when two do not fit the LDS).  Measured (one process, tiles
+    // per workgroup 3..10): cfg1 4 tiles 11.30 us against 11.42 at 7 and 12.1-14.0 elsewhere,
+    // gate/up 5 tiles 12.89 us against 13.40 at 10 and 13.6-17.0 elsewhere; a grid that needs a
+    // second round of workgroups costs 1.5-3 us.
+    auto plan_for = [&](int wgs) {
+        const int G = std::min(T, wgs);
+        p.tw = std::min((T + G - 1) / G, kM1MaxWaves);
+        p.grid = (T + p.tw - 1) / p.tw;
+        p.lds = (size_t)m1_x_bytes(K) + 2 * (size_t)K + (size_t)p.tw * m1_wave_bytes(p.depth, nsteps);
+    };
+    for (p.depth = g_m1_depth == 3 ? 3 : 2; p.depth >= 2; --p.depth) {
+        if (g_m1_wgs > 0) {
+            plan_for(g_m1_wgs);
+            if (p.lds <= kLdsPerCU) return true;
+            continue;
+        }
+        plan_for(kM1Workgroups);
+        if (2 * p.lds <= kLdsPerCU) return true;
+        plan_for(kM1Workgroups / 2);
+        if (p.lds <= kLdsPerCU) return true;
+    }
+    return false;
+}
+
+template <typename OutT, int EPI = 0>
+void launch_m1(const M1Plan& p, const void* W, const void* St, const void* Xb, void* Out, int N, int K,
+               hipStream_t s)
+{
+    const dim3 grid((unsigned)p.grid), block(64 * p.tw);
+#define FP8KV_M1(D) \
+    launch_kernel(h4mv_m1_kernel<D, OutT, EPI>, grid, block, (uint32_t)p.lds, s, \
+                  static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
+                  static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K)
+    if (p.depth == 3) FP8KV_M1(3);
+    else FP8KV_M1(2);
+#undef FP8KV_M1
+}
+
 template <typename OutT>
 int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N, int K, int M,
                 void* stream)
@@ -874,9 +1161,12 @@ int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N,
     if (!aligned(W, 16) || !aligned(Xb, 16) || !aligned(Out, sizeof(OutT))) return FP8KV_ERR_ALIGN;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
+    M1Plan mp;
     KsPlan kp;
     StreamPlan p;
-    if (aligned(St, 4) && kslice_plan(N, K, M, kp)) {
+    if (aligned(St, 4) && m1_plan(N, K, M, mp)) {
+        launch_m1<OutT>(mp, W, St, Xb, Out, N, K, s);
+    } else if (aligned(St, 4) && kslice_plan(N, K, M, kp)) {
         launch_kslice<OutT>(kp, W, St, Xb, Out, N, K, M, s);
     } else if (aligned(St, 4) && stream_plan(N, K, M, p)) {
         launch_stream_m<OutT>(p, W, St, Xb, Out, N, K, M, s);
@@ -900,6 +1190,13 @@ extern "C" int h4mv_silu_mul(const void* W, const void* St, const void* Xb, void
     if (M > 8 || (K & 511) != 0 || (N & 15) != 0) return FP8KV_ERR_SHAPE;
     if (!aligned(W, 16) || !aligned(Xb, 16) || !aligned(Out, 8) || !aligned(St, 4)) return FP8KV_ERR_ALIGN;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    M1Plan mp;
+    if (m1_plan(N, K, M, mp)) {
+        begin_launch();
+        if (mode == 0) launch_m1<__bf16, 1>(mp, W, St, Xb, Out, N, K, s);
+        else launch_m1<__bf16, 2>(mp, W, St, Xb, Out, N, K, s);
+        return finish_launch();
+    }
     KsPlan kp;
     if (kslice_plan(N, K, M, kp)) {
         begin_launch();
@@ -1048,12 +1345,94 @@ int audit_kslice(int N, int K, int M, const KsPlan& p)
     return 0;
 }
 
+// Audit of the M = 1 kernel (same return convention as audit_stream): tile coverage, every
+// activation / code / scale byte read, every LDS byte written or read, the activation groups of
+// each block held by one quad of lanes.
+int audit_m1(int N, int K, const M1Plan& p)
+{
+    const int T = (N + kRowsPerWG - 1) / kRowsPerWG, G = p.grid, tw = p.tw, depth = p.depth;
+    if ((K & 511) || tw < 1 || tw > kM1MaxWaves || G < 1 || (long)G * tw < T || depth < 2 || depth > 3) return 2;
+    const int nsteps = K >> 9, nthreads = 64 * tw, np = K >> 3;
+    const size_t xb = (size_t)m1_x_bytes(K), xs = xb, wb = (size_t)m1_wave_bytes(depth, nsteps);
+    if (xb + 2 * (size_t)K + (size_t)tw * wb != p.lds || p.lds > kLdsPerCU) return 3;
+    const size_t wbytes = (size_t)N * (size_t)(K >> 1), sbytes = (size_t)N * (size_t)(K >> 5);
+    const size_t xbytes = (size_t)K * 2;
+    // the row's copies: every piece once, inside the operand and the staging area
+    std::vector<unsigned char> pseen((size_t)np, 0);
+    for (int w = 0; w < tw; ++w)
+        for (int p0 = w * 64; p0 < np; p0 += tw * 64)
+            for (int lane = 0; lane < 64 && p0 + lane < np; ++lane) {
+                const int pc = p0 + lane;
+                if (16 * (size_t)pc + 16 > xbytes || xs + 16 * (size_t)p0 + 16 * lane + 16 > xs + xbytes) return 4;
+                if (pseen[(size_t)pc]) return 4;
+                pseen[(size_t)pc] = 1;
+            }
+    for (size_t i = 0; i < pseen.size(); ++i)
+        if (!pseen[i]) return 4;
+    // conversion: staging reads and hi / lo / scale writes in range, the four groups of a block
+    // in one quad of lanes, every group converted
+    std::vector<unsigned char> gseen((size_t)np, 0);
+    for (int g0 = 0; g0 < np; g0 += nthreads)
+        for (int t = 0; t < nthreads; ++t) {
+            const int gr = g0 + t, g = gr < np ? gr : np - 4 + (gr & 3);
+            const int gq = g0 + (t & ~3), gq0 = gq < np ? gq : np - 4;
+            if ((g & ~3) != gq0 || (g & 3) != (t & 3)) return 5;
+            if (16 * (size_t)g + 16 > xbytes || 8 * (size_t)g + 8 > (size_t)K) return 5;
+            if (2 * (size_t)K + (size_t)m1_xe_pos(g >> 2) + 1 > xb) return 5;
+            gseen[(size_t)g] = 1;
+        }
+    for (size_t g = 0; g < gseen.size(); ++g)
+        if (!gseen[g]) return 5;
+    std::vector<unsigned char> seen((size_t)T, 0);
+    for (int b = 0; b < G; ++b)
+        for (int w = 0; w < tw; ++w) {
+            const int tw_tile = b + w * G;
+            const bool has = tw_tile < T;
+            if (has) {
+                if (seen[(size_t)tw_tile]) return 6;
+                seen[(size_t)tw_tile] = 1;
+            }
+            const int n0 = (has ? tw_tile : b) * kRowsPerWG;
+            const size_t ring = xs + 2 * (size_t)K + (size_t)w * wb, sarea = ring + (size_t)depth * kStepCodeBytes;
+            if (ring + wb > p.lds) return 7;
+            for (int lane = 0; lane < 64; ++lane) {
+                for (int t0 = 0; t0 < 16 * nsteps; t0 += 64) {        // scale slice copies
+                    const int t = std::min(t0 + lane, 16 * nsteps - 1);
+                    if (stream_s_seg_off(n0, N, K, nsteps, 0, t) + 16 > sbytes) return 8;
+                    if (sarea + 16 * (size_t)(t0 + lane) + 16 > ring + wb) return 8;
+                }
+                for (int s = 0; s < nsteps; ++s)                       // code copies
+                    for (int i = 0; i < 4; ++i) {
+                        const size_t g = (size_t)n0 * (K >> 1) + (size_t)s * 256 + stream_w_lane_off(n0, N, K, lane, i);
+                        if (g + 16 > wbytes) return 9;
+                        if ((size_t)(s % depth) * kStepCodeBytes + i * 1024 + 16 * lane + 16 > (size_t)depth * kStepCodeBytes) return 9;
+                    }
+                const int r = lane & 15, q = lane >> 4;
+                for (int s = 0; s < nsteps; ++s) {                     // fragment reads
+                    if ((size_t)((r * nsteps + s) * 16 + 16) > (size_t)m1_scale_bytes(nsteps)) return 10;
+                    for (int u = 0; u < 4; ++u) {
+                        if (stream_w_read_off(r, q, u) + 16 > kStepCodeBytes) return 11;
+                        const size_t k = (size_t)512 * s + 128 * u + 16 * q;
+                        if ((r & 1 ? (size_t)K : 0) + k + 64 + 16 > (size_t)2 * K) return 12;
+                        if (k + 64 + 16 > (size_t)K) return 12;
+                    }
+                    if (2 * (size_t)K + 16 * (size_t)s + 4 * q + 4 > xb) return 13;
+                }
+            }
+        }
+    for (int t = 0; t < T; ++t)
+        if (!seen[(size_t)t]) return 6;
+    return 0;
+}
+
 }}  // namespace fp8kv::h4mv_detail
 
 extern "C" int fp8kv_h4mv_audit(int N, int K, int M)
 {
     using namespace fp8kv::h4mv_detail;
     if (N < 1 || K < 32 || M < 1 || M > 16 || (K & 31)) return 2;
+    M1Plan mp;
+    if (m1_plan(N, K, M, mp)) return audit_m1(N, K, mp);
     KsPlan kp;
     if (kslice_plan(N, K, M, kp)) return audit_kslice(N, K, M, kp);
     StreamPlan p;
@@ -1067,6 +1446,13 @@ extern "C" void fp8kv_h4mv_kslice_tune(int mode, int depth, int order, int workg
     fp8kv::h4mv_detail::g_kslice_depth = depth;
     fp8kv::h4mv_detail::g_kslice_order = (order == 1 || order == 2) ? order : 0;
     fp8kv::h4mv_detail::g_kslice_wgs = workgroups > 0 ? workgroups : 0;
+}
+
+extern "C" void fp8kv_h4mv_m1_tune(int mode, int depth, int workgroups)
+{
+    fp8kv::h4mv_detail::g_m1_mode = (mode == 1 || mode == 2) ? mode : 0;
+    fp8kv::h4mv_detail::g_m1_depth = depth;
+    fp8kv::h4mv_detail::g_m1_wgs = workgroups > 0 ? workgroups : 0;
 }
 
 extern "C" void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode)

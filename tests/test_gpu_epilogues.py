@@ -120,6 +120,27 @@ def test_fused_silu_epilogue_kslice(mode, depth):
         lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("depth", [2, 3])
+def test_fused_silu_epilogue_m1(mode, depth):
+    """The fused epilogue on the M = 1 kernel forced through its tuning hook equals the two-step
+    path on the same kernel (one tile, several tiles per workgroup, cfg1's shape)."""
+    from fp8kv_amd import _lib
+    lib = _lib.load()
+    try:
+        lib.fp8kv_h4mv_m1_tune(1, depth, 0)
+        for N, K in ((16, 512), (8224, 2048), (28672, 4096)):
+            c = workloads.w4_case(N, K, 1, seed=N + depth)
+            W, St, X = c["W"].to(DEV), c["St"].to(DEV), c["X"].to(DEV)
+            wi, si = ops.interleave_gate_up(W, St)
+            fused = ops.h4mv_silu_mul(X, wi, si, mode=mode)
+            two = ops.silu_mul(ops.h4mv(X, W, St), mode=mode)
+            torch.cuda.synchronize()
+            assert torch.equal(fused, two), (N, K)
+    finally:
+        lib.fp8kv_h4mv_m1_tune(0, 0, 0)
+
+
 def test_fused_silu_epilogue_vs_oracle():
     N, K, M = 1024, 2048, 4
     c = workloads.w4_case(N, K, M, seed=11)

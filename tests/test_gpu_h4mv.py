@@ -233,10 +233,12 @@ def test_kslice_variants(depth, N, K, order):
     lib = _lib.load()
     try:
         lib.fp8kv_h4mv_kslice_tune(1, depth, order, 0)
+        lib.fp8kv_h4mv_m1_tune(2, 0, 0)                 # M = 1 on the K-slice kernel too
         for M in (1, 3, 8):
             _check(workloads.w4_case(N=N, K=K, M=M, seed=N + K + M + depth))
     finally:
         lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+        lib.fp8kv_h4mv_m1_tune(0, 0, 0)
 
 
 def test_kslice_and_streaming_kernels_agree():
@@ -250,4 +252,137 @@ def test_kslice_and_streaming_kernels_agree():
         b = _run(case, out_dtype=torch.float32)
     finally:
         lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+    assert np.abs(a - b).max() <= 1e-5 * np.abs(a).max()
+
+
+# --- M = 1 kernel: e2m1 codes on the block-scaled MFMA, the activation row as e4m3 hi + lo -------
+
+class _M1:
+    """The M = 1 kernel forced (mode 1) or switched off (mode 2) for the duration of a block."""
+
+    def __init__(self, mode=1, depth=0, wgs=0):
+        self.args = (mode, depth, wgs)
+
+    def __enter__(self):
+        _lib.load().fp8kv_h4mv_m1_tune(*self.args)
+
+    def __exit__(self, *exc):
+        _lib.load().fp8kv_h4mv_m1_tune(0, 0, 0)
+
+
+@pytest.mark.parametrize("wgs", [0, 5, 150])
+@pytest.mark.parametrize("depth", [2, 3])
+@pytest.mark.parametrize("N,K", [(1, 512), (272, 1024), (250, 1536), (4096, 3584), (3584, 18944),
+                                 (28672, 4096), (37888, 3584)])
+def test_m1_kernel_variants(depth, wgs, N, K):
+    """Both ring depths and three workgroup targets (256; 5, which gives several tiles per
+    workgroup and waves without a tile; 150): one K step, ragged N, K = 18944, cfg1, gate/up,
+    bf16 and fp32 outputs against the oracle."""
+    with _M1(1, depth, wgs):
+        _check(workloads.w4_case(N=N, K=K, M=1, seed=N + K + depth + wgs))
+
+
+def test_m1_one_hot_probes_across_groups_and_rows():
+    """Distinct code per row and scale per (row, group): every k of a 512-k step, exact."""
+    N, K = 37, 512
+    rng = np.random.default_rng(5)
+    St = rng.integers(120, 135, (N, K // 32), dtype=np.uint8)
+    from oracle.formats import pack_e2m1
+    with _M1():
+        for k in [0, 1, 15, 16, 31, 32, 63, 64, 127, 128, 200, 255, 256, 480, 511]:
+            codes = np.zeros((N, K), dtype=np.uint8)
+            codes[:, k] = rng.integers(1, 16, N).astype(np.uint8)
+            X = np.zeros((1, K), dtype=np.float32)
+            X[0, k] = -1.5
+            case = {"W": torch.from_numpy(pack_e2m1(codes)), "St": torch.from_numpy(St),
+                    "X": torch.from_numpy(X).to(torch.bfloat16)}
+            assert np.array_equal(_run(case), _oracle(case)), f"k={k}"
+
+
+def test_m1_integer_full_row_exact():
+    g = torch.Generator().manual_seed(0)
+    N, K = 8, 4096
+    case = {"W": torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, generator=g),
+            "St": torch.full((N, K // 32), 127, dtype=torch.uint8),
+            "X": (torch.arange(K) % 7 - 3).to(torch.bfloat16)[None, :]}
+    with _M1():
+        y = _run(case, out_dtype=torch.float32)
+    assert np.array_equal(y, _oracle(case).astype(np.float32))
+
+
+def test_m1_every_bf16_value_splits_exactly():
+    """Each block holds its largest value and values 2^0 .. 2^-15 below it with random 8-bit
+    mantissas: hi + lo is exact for all values >= 2^-9 of the block's largest, and the rest are
+    below the bar; one-hot rows of W pick single k, so each output is one product."""
+    K = 512
+    N = 64
+    rng = np.random.default_rng(8)
+    x = np.zeros(K, dtype=np.float32)
+    for b in range(K // 32):
+        top = 2.0 ** rng.integers(-100, 100)
+        mant = 1 + rng.integers(0, 128, 32) / 128.0
+        sgn = rng.choice([-1.0, 1.0], 32)
+        x[32 * b: 32 * b + 32] = sgn * mant * top * 2.0 ** -np.minimum(np.arange(32), 9)
+        x[32 * b] = top * 1.9921875
+    codes = np.zeros((N, K), dtype=np.uint8)
+    ks = rng.choice(K, N, replace=False)
+    codes[np.arange(N), ks] = 2                                   # e2m1 1.0
+    from oracle.formats import pack_e2m1
+    case = {"W": torch.from_numpy(pack_e2m1(codes)), "St": torch.full((N, K // 32), 127, dtype=torch.uint8),
+            "X": torch.from_numpy(x[None, :]).to(torch.bfloat16)}
+    with _M1():
+        y = _run(case, out_dtype=torch.float32)
+    ref = _oracle(case)
+    assert np.array_equal(y, ref.astype(np.float32))
+
+
+def test_m1_activation_dynamic_range():
+    """Blocks scaled by 2^-60 .. 2^60 and values spread inside each block."""
+    case = workloads.w4_case(N=2048, K=4096, M=1, seed=12)
+    g = torch.Generator().manual_seed(3)
+    x = case["X"].float()
+    x = x * (2.0 ** torch.randint(-60, 61, (1, 128), generator=g).float()).repeat_interleave(32, dim=1)
+    case["X"] = x.to(torch.bfloat16)
+    with _M1():
+        _check(case)
+
+
+def test_m1_scale_bytes_zero_255_and_wide():
+    base = workloads.w4_case(N=96, K=512, M=1, seed=9)
+    St = base["St"].clone()
+    St[:16] = 0                        # 2^-127: negligible rows
+    St[16:32] = 60                     # 2^-67
+    St[32:64] = 150                    # 2^23
+    St[70, 3] = 255                    # NaN
+    case = dict(base, St=St)
+    with _M1():
+        y = _run(case, out_dtype=torch.float32)
+    ref = _oracle(case)
+    assert np.all(np.abs(y[:, :16]) < 1e-30)
+    for a, b in ((16, 32), (32, 64)):
+        assert matvec.rel_to_max_error(y[:, a:b], ref[:, a:b]) < TOL
+    assert np.isnan(y[0, 70]) and np.isfinite(np.delete(y[0], 70)).all()
+
+
+def test_m1_zero_nan_and_inf_activations():
+    """A zero row gives zeros; NaN anywhere gives NaN everywhere (as the reference); an infinity
+    gives NaN everywhere (the reference gives +-inf or NaN)."""
+    case = workloads.w4_case(N=64, K=1024, M=1, seed=4)
+    with _M1():
+        z = _run(dict(case, X=torch.zeros_like(case["X"])), out_dtype=torch.float32)
+        assert np.array_equal(z, np.zeros_like(z))
+        for bad in (float("nan"), float("inf"), float("-inf")):
+            x = case["X"].clone()
+            x[0, 700] = bad
+            y = _run(dict(case, X=x), out_dtype=torch.float32)
+            assert np.isnan(y).all(), bad
+
+
+def test_m1_and_streaming_kernels_agree():
+    """cfg1 M = 1 on the M = 1 kernel (the default) and on the streaming kernel: within the fp32
+    rounding of their accumulation orders."""
+    case = workloads.w4_case(N=28672, K=4096, M=1, seed=7)
+    a = _run(case, out_dtype=torch.float32)
+    with _M1(2):
+        b = _run(case, out_dtype=torch.float32)
     assert np.abs(a - b).max() <= 1e-5 * np.abs(a).max()

@@ -70,3 +70,23 @@ def test_h4mv_kslice_in_bounds(lib, depth, order, wgs):
                 assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
     finally:
         lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+
+
+@pytest.mark.parametrize("wgs", [0, 7, 300])
+@pytest.mark.parametrize("depth", [2, 3])
+def test_h4mv_m1_in_bounds(lib, depth, wgs):
+    """The M = 1 kernel forced on every shape it accepts: model shapes, ragged N (the last tile's
+    rows clamped), K from one step up, fewer or more workgroups than CUs (1..16 tiles per
+    workgroup, waves without a tile): every tile covered once, the activation row copied and
+    converted once, a block's four groups in one quad of lanes."""
+    rng = random.Random(depth + wgs)
+    try:
+        lib.fp8kv_h4mv_m1_tune(1, depth, wgs)
+        shapes = list(CFG4_SHAPES) + [(1, 512), (15, 512), (17, 1024), (4097, 2048),
+                                      (16 * 4096 + 3, 4096), (250, 1536)]
+        for _ in range(30):
+            shapes.append((rng.randrange(1, 20000), 512 * rng.randrange(1, 25)))
+        for N, K in shapes:
+            assert lib.fp8kv_h4mv_audit(N, K, 1) == 0, (N, K)
+    finally:
+        lib.fp8kv_h4mv_m1_tune(0, 0, 0)
