@@ -32,9 +32,11 @@ def _capture(fn):
     return graph
 
 
-@pytest.mark.parametrize("N,K,M", [(28672, 4096, 1), (37888, 3584, 8), (4096, 3584, 8), (3584, 18944, 8)])
+@pytest.mark.parametrize("N,K,M", [(28672, 4096, 1), (37888, 3584, 1), (37888, 3584, 8), (4096, 3584, 8),
+                                   (3584, 18944, 8), (4096, 3584, 1)])
 def test_matvec_replay(N, K, M):
-    """Streaming kernel (M = 1, and the small-N shapes) and K-slice kernel (gate/up, M = 8)."""
+    """M = 1 kernel (cfg1 and gate/up at M = 1), K-slice kernel (gate/up, M = 8) and streaming
+    kernel (the small-N shapes)."""
     c = workloads.w4_case(N=N, K=K, M=M, seed=N + M)
     X, W, St = c["X"].to(DEV), c["W"].to(DEV), c["St"].to(DEV)
     Y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
@@ -46,8 +48,10 @@ def test_matvec_replay(N, K, M):
         assert torch.equal(Y, ops.h4mv(X, W, St)), f"replay {it}"
 
 
-def test_fused_silu_replay():
-    N, K, M = 37888, 3584, 8
+@pytest.mark.parametrize("M", [8, 1])
+def test_fused_silu_replay(M):
+    """The fused gate/up + SiLU-and-mul matvec on the K-slice kernel (M = 8) and the M = 1 kernel."""
+    N, K = 37888, 3584
     c = workloads.w4_case(N=N, K=K, M=M, seed=3)
     wi, si = ops.interleave_gate_up(c["W"].to(DEV), c["St"].to(DEV))
     X = c["X"].to(DEV)
