@@ -273,11 +273,11 @@ class _M1:
 @pytest.mark.parametrize("wgs", [0, 5, 150])
 @pytest.mark.parametrize("depth", [2, 3])
 @pytest.mark.parametrize("N,K", [(1, 512), (272, 1024), (250, 1536), (4096, 3584), (3584, 18944),
-                                 (28672, 4096), (37888, 3584)])
+                                 (28672, 4096), (37888, 3584), (100, 32768)])
 def test_m1_kernel_variants(depth, wgs, N, K):
-    """Both ring depths and three workgroup targets (256; 5, which gives several tiles per
-    workgroup and waves without a tile; 150): one K step, ragged N, K = 18944, cfg1, gate/up,
-    bf16 and fp32 outputs against the oracle."""
+    """Both ring depths and three workgroup targets (the default; 5, which gives several tiles per
+    workgroup and waves without a tile; 150): one K step, ragged N, K = 18944, the 64-step
+    maximum, cfg1, gate/up, bf16 and fp32 outputs against the oracle."""
     with _M1(1, depth, wgs):
         _check(workloads.w4_case(N=N, K=K, M=1, seed=N + K + depth + wgs))
 

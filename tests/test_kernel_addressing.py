@@ -83,7 +83,7 @@ def test_h4mv_m1_in_bounds(lib, depth, wgs):
     try:
         lib.fp8kv_h4mv_m1_tune(1, depth, wgs)
         shapes = list(CFG4_SHAPES) + [(1, 512), (15, 512), (17, 1024), (4097, 2048),
-                                      (16 * 4096 + 3, 4096), (250, 1536)]
+                                      (16 * 4096 + 3, 4096), (250, 1536), (33, 32768), (1000, 32768)]
         for _ in range(30):
             shapes.append((rng.randrange(1, 20000), 512 * rng.randrange(1, 25)))
         for N, K in shapes:
