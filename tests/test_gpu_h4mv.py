@@ -111,6 +111,24 @@ def test_shapes(N, K, M):
     _check(case)
 
 
+@pytest.mark.parametrize("m1_mode", [0, 1])
+def test_random_shapes_every_plan(m1_mode):
+    """Seeded random shapes across every planner branch (M = 1 kernel forced or default, K-slice,
+    streaming with one or two row tiles, register kernel for K % 512 != 0 or M > 8): N from 1 to
+    40000, K a multiple of 32 up to 8192, M from 1 to 16."""
+    rng = np.random.default_rng(77 + m1_mode)
+    lib = _lib.load()
+    try:
+        lib.fp8kv_h4mv_m1_tune(m1_mode, 0, 0)
+        for i in range(24):
+            N = int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 4096)), int(rng.integers(4096, 40000))]))
+            K = 32 * int(rng.integers(1, 257)) if i % 3 else 512 * int(rng.integers(1, 17))
+            M = int(rng.choice([1, 1, 2, 3, int(rng.integers(4, 9)), int(rng.integers(9, 17))]))
+            _check(workloads.w4_case(N=N, K=K, M=M, seed=1000 + i))
+    finally:
+        lib.fp8kv_h4mv_m1_tune(0, 0, 0)
+
+
 def test_wide_scale_range():
     """Scale bytes far from 127 on both sides; each band is checked against its own maximum."""
     case = workloads.w4_case(N=96, K=256, M=2, seed=9)
