@@ -19,7 +19,7 @@ int fp8kv_h4mv_audit(int N, int K, int M);
 void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode);
 
 /* Tuning hook for the matvec's K-slice kernel: mode 0 = used from M = 3 on when every CU gets at
- * least two 16-row tiles (the default), 1 = whenever the shape allows it (N % 16 == 0, K % 512 == 0,
+ * least two 16-row tiles (the default), 1 = whenever the shape allows it (N >= 16, K % 512 == 0,
  * K <= 4096, M <= 8), 2 = never; depth = LDS ring slots per wave (3; any other value: 2, the default);
  * order = tile order (1: each workgroup a contiguous range, 2: interleaved; 0: default);
  * workgroups = workgroup count the planner aims for (0: default).  Affects later launches and

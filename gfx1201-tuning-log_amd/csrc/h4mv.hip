@@ -499,6 +499,27 @@ constexpr int kKsSlotBytes = kStepCodeBytes + 256;
 constexpr int kKsTmax = 16;                    // tiles per workgroup (register tiles)
 constexpr int kKsMinM = 3;                     // default: K-slice kernel from this M on
 
+// Tiles of N rows, and the first row of tile t.  When N % 16 != 0 the last tile is moved back to
+// rows N - 16 .. N - 1 (N >= 16), so its copies read whole rows of the operand with the full
+// tiles' per-lane offsets; it stores only its rows from 16 t on (the others belong to the tile
+// before it).
+__host__ __device__ inline int ks_tiles(int N) { return (N + 15) >> 4; }
+__host__ __device__ inline int ks_row0(int t, int N) { return 16 * t < N - 16 ? 16 * t : N - 16; }
+
+// Output rows n0 + 4 q .. n0 + 4 q + 3 of lane (r, q)'s accumulator, those in [lo, N) only.
+template <typename OutT>
+__device__ __forceinline__ void store_rows(const f32x4_t& acc, OutT* __restrict__ Out, int n0, int lo, int N,
+                                           int M, int r, int q)
+{
+    if (r >= M) return;
+    OutT* orow = Out + (size_t)r * (size_t)N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 4 * q + i;
+        if (n >= lo && n < N) orow[n] = (OutT)acc[i];
+    }
+}
+
 // Scale copy of a tile-step: lane l fetches bytes 4 (l % 4) .. +3 of row l / 4's 16 scale bytes
 // of the step; offset from the tile's first scale byte of the step.
 __host__ __device__ inline uint32_t ks_s_lane_off(int K, int lane)
@@ -549,7 +570,7 @@ h4mv_kslice_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
     const int r = lane & 15;
     const int q = lane >> 4;
     int t0, nt, tstride;
-    ks_tiles_of(blockIdx.x, N >> 4, gridDim.x, interleaved != 0, t0, nt, tstride);
+    ks_tiles_of(blockIdx.x, ks_tiles(N), gridDim.x, interleaved != 0, t0, nt, tstride);
     const int G = K >> 5;
     const int gs = wave * kStepGroups;                  // first scale group of this wave's step
 
@@ -558,17 +579,16 @@ h4mv_kslice_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
 #pragma unroll
     for (int i = 0; i < 4; ++i) woff[i] = stream_w_lane_off(0, kRowsPerWG, K, lane, i);
     const uint32_t soff = ks_s_lane_off(K, lane);
-    const uint8_t* wstep = W + (size_t)t0 * kRowsPerWG * (size_t)(K >> 1) + (size_t)gs * 16;
-    const uint8_t* sstep = St + (size_t)t0 * kRowsPerWG * (size_t)G + gs;
-    const size_t wtile = (size_t)tstride * kRowsPerWG * (size_t)(K >> 1);
-    const size_t stile = (size_t)tstride * kRowsPerWG * (size_t)G;
+    const uint8_t* wstep = W + (size_t)gs * 16;
+    const uint8_t* sstep = St + gs;
     auto issue = [&](int i, unsigned char* slot) {
-        const uint8_t* w = wstep + (size_t)i * wtile;
+        const int n0 = ks_row0(t0 + i * tstride, N);
+        const uint8_t* w = wstep + (size_t)n0 * (size_t)(K >> 1);
 #pragma unroll
         for (int c = 0; c < 4; ++c)
             __builtin_amdgcn_global_load_lds((const void*)(w + woff[c]), (lds_void_t*)(slot + c * 1024),
                                              16, 0, kDmaAux);
-        __builtin_amdgcn_global_load_lds((const void*)(sstep + (size_t)i * stile + soff),
+        __builtin_amdgcn_global_load_lds((const void*)(sstep + (size_t)n0 * (size_t)G + soff),
                                          (lds_void_t*)(slot + kStepCodeBytes), 4, 0, 0);
     };
     // Tile 0's copies go out first, then the activation loads, then the rest of the ring, filled
@@ -643,7 +663,14 @@ h4mv_kslice_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
     for (int i = wave; i < nt; i += nwaves) {
         f32x4_t a = red[(i * nwaves) * 64 + lane];
         for (int w = 1; w < nwaves; ++w) a += red[(i * nwaves + w) * 64 + lane];
-        store_tile<OutT, EPI>(a, Out, t0 + i * tstride, N, M, r, q);
+        const int t = t0 + i * tstride;
+        if constexpr (EPI == 0) {
+            if (16 * t > N - 16) {                      // partial last tile: rows N - 16 .. N - 1
+                store_rows(a, Out, N - 16, 16 * t, N, M, r, q);
+                continue;
+            }
+        }
+        store_tile<OutT, EPI>(a, Out, t, N, M, r, q);
     }
 }
 
@@ -1059,10 +1086,10 @@ struct KsPlan {
 inline bool kslice_plan(int N, int K, int M, KsPlan& p)
 {
     if (g_kslice_mode == 2) return false;
-    if ((K & 511) != 0 || (N & 15) != 0 || M > 8) return false;
+    if ((K & 511) != 0 || N < 16 || M > 8) return false;
     const int steps = K >> 9;
     if (steps > kKsMaxWaves) return false;
-    const int T = N >> 4;
+    const int T = ks_tiles(N);
     if (g_kslice_mode == 0 && (T < 2 * kKsWorkgroups || M < kKsMinM)) return false;
     p.nw = steps;
     p.depth = g_kslice_depth == 3 ? 3 : 2;
@@ -1072,7 +1099,14 @@ inline bool kslice_plan(int N, int K, int M, KsPlan& p)
     const int cap = std::min(kKsTmax, (int)((kLdsPerCU - ring_bytes) / ((size_t)p.nw * 1024)));
     if (cap < 1) return false;
     int G = std::min(T, g_kslice_wgs > 0 ? g_kslice_wgs : kKsWorkgroups);
-    if ((T + G - 1) / G > cap) G = (T + cap - 1) / cap;
+    if ((T + G - 1) / G > cap) {
+        // More tiles than one round of workgroups holds.  Default: whole rounds of kKsWorkgroups,
+        // the fewest that keep every workgroup within cap tiles (a short last round runs the GPU
+        // part-empty: lm_head N = 128167, K = 3584, M = 8: 56.7 us at 573 workgroups, 14 tiles
+        // each, against 51.4 us at 768, 10-11 tiles each).
+        if (g_kslice_wgs > 0) G = (T + cap - 1) / cap;
+        else G = std::min(T, kKsWorkgroups * ((T + kKsWorkgroups * cap - 1) / (kKsWorkgroups * cap)));
+    }
     p.grid = G;
     p.nt_max = (T + G - 1) / G;
     const size_t ring = (size_t)p.nw * p.depth * kKsSlotBytes;
@@ -1292,14 +1326,14 @@ int audit_stream(int N, int K, int M, const StreamPlan& p)
 // code / scale / activation byte read, every LDS byte written or read.
 int audit_kslice(int N, int K, int M, const KsPlan& p)
 {
-    const int T = N >> 4, G = p.grid, nw = p.nw, depth = p.depth;
-    if ((N & 15) || (K & 511) || nw != (K >> 9) || nw > kKsMaxWaves || G < 1 || G > T) return 2;
+    const int T = ks_tiles(N), G = p.grid, nw = p.nw, depth = p.depth;
+    if (N < 16 || (K & 511) || nw != (K >> 9) || nw > kKsMaxWaves || G < 1 || G > T) return 2;
     if (depth < 2 || depth > 3 || p.lds > kLdsPerCU) return 3;
     if ((size_t)nw * depth * kKsSlotBytes + (size_t)p.nt_max * nw * 1024 > p.lds) return 3;
     const size_t wbytes = (size_t)N * (size_t)(K >> 1), sbytes = (size_t)N * (size_t)(K >> 5);
     const size_t xbytes = (size_t)M * (size_t)K * 2;
     const size_t slot = kKsSlotBytes;
-    std::vector<unsigned char> seen((size_t)T, 0);
+    std::vector<unsigned char> seen((size_t)T, 0), stored((size_t)N, 0);
     for (int b = 0; b < G; ++b) {
         int t0, nt, tstride;
         ks_tiles_of(b, T, G, p.interleaved != 0, t0, nt, tstride);
@@ -1308,6 +1342,12 @@ int audit_kslice(int N, int K, int M, const KsPlan& p)
             const long t = (long)t0 + (long)i * tstride;
             if (t < 0 || t >= T || seen[(size_t)t]) return 4;
             seen[(size_t)t] = 1;
+            // output rows the tile stores: 16 t .. min(row0 + 16, N) - 1 (store_tile / store_rows)
+            const int hi = std::min(ks_row0((int)t, N) + kRowsPerWG, N);
+            for (int n = 16 * (int)t; n < hi; ++n) {
+                if (stored[(size_t)n]) return 15;
+                stored[(size_t)n] = 1;
+            }
         }
         for (int w = 0; w < nw; ++w) {
             const int gs = w * kStepGroups;
@@ -1321,13 +1361,16 @@ int audit_kslice(int N, int K, int M, const KsPlan& p)
                             if ((size_t)r * K * 2 + (size_t)gs * 64 + stream_x_frag_off(q, u, j) + 16 > xbytes) return 6;
                 for (int i = 0; i < nt; ++i) {
                     const size_t sl = ring + (size_t)(i % depth) * slot;
-                    const size_t tile = (size_t)t0 + (size_t)i * tstride;
-                    const size_t wt = tile * kRowsPerWG * (K >> 1) + (size_t)gs * 16;
+                    const int tile = t0 + i * tstride;
+                    const size_t n0 = (size_t)ks_row0(tile, N);
+                    if (n0 + kRowsPerWG > (size_t)N) return 7;
+                    if (16 * tile < N - 16 ? n0 != (size_t)(16 * tile) : n0 + kRowsPerWG != (size_t)N) return 7;
+                    const size_t wt = n0 * (K >> 1) + (size_t)gs * 16;
                     for (int c = 0; c < 4; ++c) {
                         if (wt + stream_w_lane_off(0, kRowsPerWG, K, lane, c) + 16 > wbytes) return 7;
                         if (c * 1024 + 16 * lane + 16 > kStepCodeBytes) return 8;
                     }
-                    const size_t st = tile * kRowsPerWG * (K >> 5) + gs;
+                    const size_t st = n0 * (K >> 5) + gs;
                     if (st + ks_s_lane_off(K, lane) + 4 > sbytes) return 9;
                     if (kStepCodeBytes + 4 * lane + 4 > (int)slot) return 10;
                     if (kStepCodeBytes + 16 * r + 16 > (int)slot) return 11;
@@ -1342,6 +1385,8 @@ int audit_kslice(int N, int K, int M, const KsPlan& p)
     }
     for (int t = 0; t < T; ++t)
         if (!seen[(size_t)t]) return 4;
+    for (int n = 0; n < N; ++n)
+        if (!stored[(size_t)n]) return 15;
     return 0;
 }
 

@@ -242,12 +242,13 @@ def test_row_tile_variants(rt, N, K, x_mode):
 @pytest.mark.parametrize("order", [1, 2])
 @pytest.mark.parametrize("depth", [2, 3])
 @pytest.mark.parametrize("N,K", [(16, 512), (4096, 3584), (4112, 1024), (8208, 2048), (28672, 4096),
-                                 (65536, 512), (66048, 512)])
+                                 (65536, 512), (66048, 512), (17, 512), (4097, 1024), (40003, 3584)])
 def test_kslice_variants(depth, N, K, order):
     """The K-slice kernel forced through its tuning hook at every ring depth and both tile
     orders: one tile per workgroup (fewer tiles than ring slots), uneven tile counts (T = 257,
-    513), seven tiles (cfg1), the sixteen-tile maximum and more workgroups than CUs (T = 4128),
-    at M = 1, 3, 8 with bf16 and fp32 outputs."""
+    513), seven tiles (cfg1), the sixteen-tile maximum, more workgroups than CUs (T = 4128) and
+    partial last tiles (N % 16 != 0: the last tile reads rows N - 16 .. N - 1 and stores the
+    rows past the tile before it), at M = 1, 3, 8 with bf16 and fp32 outputs."""
     lib = _lib.load()
     try:
         lib.fp8kv_h4mv_kslice_tune(1, depth, order, 0)

@@ -57,14 +57,19 @@ def test_h4mv_stream_in_bounds_every_row_tile_count(lib, rt, x_mode):
 def test_h4mv_kslice_in_bounds(lib, depth, order, wgs):
     """The K-slice kernel forced on every shape it accepts, both tile orders and two workgroup
     targets: model shapes, tile counts per workgroup from 1 to 16, more workgroups than CUs,
-    random shapes; every tile is covered exactly once."""
+    partial last tiles, random shapes; every tile is covered exactly once and every output row
+    stored exactly once."""
     rng = random.Random(depth)
     try:
         lib.fp8kv_h4mv_kslice_tune(1, depth, order, wgs)
         shapes = [(N, K) for N, K in CFG4_SHAPES if K <= 4096]
         shapes += [(16, 512), (4112, 1024), (8208, 2048), (65536, 512), (66048, 512)]
+        # partial last tiles (N % 16 != 0): the lm_head vocabulary, the smallest N, random N
+        shapes += [(128167, 3584), (17, 512), (31, 1024), (4097, 1024), (40003, 3584)]
         for _ in range(60):
             shapes.append((16 * rng.randrange(1, 5000), 512 * rng.randrange(1, 9)))
+        for _ in range(30):
+            shapes.append((rng.randrange(16, 80000), 512 * rng.randrange(1, 9)))
         for N, K in shapes:
             for M in (1, 3, 8):
                 assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
