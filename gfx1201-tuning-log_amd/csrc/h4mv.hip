@@ -674,6 +674,128 @@ h4mv_kslice_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
     }
 }
 
+// Batched form of the K-slice kernel for shapes with more tiles than one round of workgroups
+// holds at kKsTmax (plain output only).  The waves' partial tiles are added every B tiles instead
+// of once at the end: after the B-th tile an LDS-only barrier (the ring's copies stay in flight),
+// each wave adds the partials of some of the batch's tiles into the workgroup's output area in
+// LDS (1 KB per tile), and a second barrier frees the partial area for the next batch.  The
+// global stores all wait for the end, as in h4mv_kslice_kernel: a store issued between ring
+// copies would enter the in-order vmcnt count and make the next waits drain the ring.  LDS:
+// rings, then B x nwaves partial tiles, then nt_max output tiles.
+template <int DEPTH, int B, typename OutT>
+__global__ void __launch_bounds__(64 * kKsMaxWaves)
+h4mv_kslice_batched_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
+                           const __bf16* __restrict__ X, OutT* __restrict__ Out, int N, int K, int M,
+                           int interleaved)
+{
+    static_assert(DEPTH * 5 < 64, "vmcnt holds at most 63");
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;                 // == K / 512
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    int t0, nt, tstride;
+    ks_tiles_of(blockIdx.x, ks_tiles(N), gridDim.x, interleaved != 0, t0, nt, tstride);
+    const int G = K >> 5;
+    const int gs = wave * kStepGroups;
+
+    unsigned char* ring = smem + (size_t)wave * DEPTH * kKsSlotBytes;
+    uint32_t woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) woff[i] = stream_w_lane_off(0, kRowsPerWG, K, lane, i);
+    const uint32_t soff = ks_s_lane_off(K, lane);
+    const uint8_t* wstep = W + (size_t)gs * 16;
+    const uint8_t* sstep = St + gs;
+    auto issue = [&](int i, unsigned char* slot) {
+        const int n0 = ks_row0(t0 + i * tstride, N);
+        const uint8_t* w = wstep + (size_t)n0 * (size_t)(K >> 1);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            __builtin_amdgcn_global_load_lds((const void*)(w + woff[c]), (lds_void_t*)(slot + c * 1024),
+                                             16, 0, kDmaAux);
+        __builtin_amdgcn_global_load_lds((const void*)(sstep + (size_t)n0 * (size_t)G + soff),
+                                         (lds_void_t*)(slot + kStepCodeBytes), 4, 0, 0);
+    };
+    // tile 0's copies, the activation loads, then the rest of the ring (as in h4mv_kslice_kernel)
+    u32x4_t xv[4][4];
+    issue(0, ring);
+    if (r < M) {
+        const unsigned char* xrow = reinterpret_cast<const unsigned char*>(X) +
+                                    (size_t)r * (size_t)K * 2 + (size_t)gs * 64;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xv[u][j] = load_16(xrow + stream_x_frag_off(q, u, j));
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) asm volatile("" : "=v"(xv[u][j]));
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 1; i < DEPTH; ++i) issue(min(i, nt - 1), ring + i * kKsSlotBytes);
+    wait_vmcnt<5 * (DEPTH - 1)>();
+
+    int rdoff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rdoff[u] = stream_w_read_off(r, q, u);
+
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(smem + (size_t)nwaves * DEPTH * kKsSlotBytes);   // [B][nwaves][64]
+    f32x4_t* outb = red + (size_t)B * nwaves * 64;                                             // [nt][64]
+    for (int b0 = 0; b0 < nt; b0 += B) {
+        f32x4_t acc[B];
+#pragma unroll
+        for (int ii = 0; ii < B; ++ii) {
+            const int i = b0 + ii;
+            if (i < nt) {
+                unsigned char* sl = ring + (i % DEPTH) * kKsSlotBytes;
+                ks_wait<DEPTH - 1>(min(nt - 1 - i, DEPTH - 1));
+                const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(sl + kStepCodeBytes + 16 * r);
+                u32x4_t wv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) wv[u] = *reinterpret_cast<const u32x4_t*>(sl + rdoff[u]);
+                __builtin_amdgcn_s_waitcnt(0xC07F);             // lgkmcnt(0): the slot is free again
+                if (i + DEPTH < nt) issue(i + DEPTH, sl);
+                f32x4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float sc = e8m0_to_f32((sv[u] >> (8 * q)) & 0xFFu);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const bf16x8_t a = fp4x8_to_bf16x8(wv[u][j], sc);
+                        if (u & 1) c1 = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), c1);
+                        else       c0 = mfma16x16x32_bf16(a, as_bf16x8(xv[u][j]), c0);
+                    }
+                }
+                acc[ii] = c0 + c1;
+                if (ii > 0) red[((ii - 1) * nwaves + wave) * 64 + lane] = acc[ii - 1];
+            }
+        }
+        const int nb = min(B, nt - b0);
+#pragma unroll
+        for (int ii = 0; ii < B; ++ii)
+            if (ii == nb - 1) red[(ii * nwaves + wave) * 64 + lane] = acc[ii];
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        for (int ii = wave; ii < nb; ii += nwaves) {
+            f32x4_t a = red[(ii * nwaves) * 64 + lane];
+            for (int w = 1; w < nwaves; ++w) a += red[(ii * nwaves + w) * 64 + lane];
+            outb[(b0 + ii) * 64 + lane] = a;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+
+    // every copy has landed (the last tile's wait was vmcnt(0)); the output tiles are in LDS
+    for (int i = wave; i < nt; i += nwaves) {
+        const f32x4_t a = outb[i * 64 + lane];
+        const int t = t0 + i * tstride;
+        if (16 * t > N - 16) store_rows(a, Out, N - 16, 16 * t, N, M, r, q);
+        else store_tile<OutT, 0>(a, Out, t, N, M, r, q);
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // M = 1 kernel: the codes go to the block-scaled MFMA as stored, the activation row as e4m3 hi + lo.
 //
@@ -1078,13 +1200,18 @@ int g_kslice_depth = 0;
 int g_kslice_order = 0;         // 0: default, 1: contiguous, 2: interleaved
 int g_kslice_wgs = 0;           // workgroups the planner aims for (0: kKsWorkgroups)
 
+constexpr int kKsBatch = 8;                    // tiles per partial-tile batch (batched kernel)
+
 struct KsPlan {
     int nw, depth, grid, nt_max, interleaved;
+    int batched;                                // h4mv_kslice_batched_kernel
     size_t lds;
 };
 
-inline bool kslice_plan(int N, int K, int M, KsPlan& p)
+// allow_batched: the caller can launch the batched kernel (plain output).
+inline bool kslice_plan(int N, int K, int M, KsPlan& p, bool allow_batched = false)
 {
+    p.batched = 0;
     if (g_kslice_mode == 2) return false;
     if ((K & 511) != 0 || N < 16 || M > 8) return false;
     const int steps = K >> 9;
@@ -1099,6 +1226,19 @@ inline bool kslice_plan(int N, int K, int M, KsPlan& p)
     const int cap = std::min(kKsTmax, (int)((kLdsPerCU - ring_bytes) / ((size_t)p.nw * 1024)));
     if (cap < 1) return false;
     int G = std::min(T, g_kslice_wgs > 0 ? g_kslice_wgs : kKsWorkgroups);
+    if ((T + G - 1) / G > cap && allow_batched && g_kslice_wgs == 0) {
+        // More tiles than one round holds at cap: one round of the batched kernel when its rings,
+        // one batch of partial tiles and the output tiles fit the LDS.
+        const int nt = (T + G - 1) / G;
+        const size_t lds = ring_bytes + (size_t)kKsBatch * p.nw * 1024 + (size_t)nt * 1024;
+        if (lds <= kLdsPerCU) {
+            p.batched = 1;
+            p.grid = G;
+            p.nt_max = nt;
+            p.lds = lds;
+            return true;
+        }
+    }
     if ((T + G - 1) / G > cap) {
         // More tiles than one round of workgroups holds.  Default: whole rounds of kKsWorkgroups,
         // the fewest that keep every workgroup within cap tiles (a short last round runs the GPU
@@ -1120,6 +1260,18 @@ void launch_kslice(const KsPlan& p, const void* W, const void* St, const void* X
                    int N, int K, int M, hipStream_t s)
 {
     const dim3 grid((unsigned)p.grid), block(64 * p.nw);
+    if constexpr (EPI == 0) {
+        if (p.batched) {
+#define FP8KV_KSB(D) \
+    launch_kernel(h4mv_kslice_batched_kernel<D, kKsBatch, OutT>, grid, block, (uint32_t)p.lds, s, \
+                  static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
+                  static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M, p.interleaved)
+            if (p.depth == 3) FP8KV_KSB(3);
+            else FP8KV_KSB(2);
+#undef FP8KV_KSB
+            return;
+        }
+    }
 #define FP8KV_KS(D) \
     launch_kernel(h4mv_kslice_kernel<D, kKsTmax, OutT, EPI>, grid, block, (uint32_t)p.lds, s, \
                   static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
@@ -1200,7 +1352,7 @@ int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N,
     StreamPlan p;
     if (aligned(St, 4) && m1_plan(N, K, M, mp)) {
         launch_m1<OutT>(mp, W, St, Xb, Out, N, K, s);
-    } else if (aligned(St, 4) && kslice_plan(N, K, M, kp)) {
+    } else if (aligned(St, 4) && kslice_plan(N, K, M, kp, true)) {
         launch_kslice<OutT>(kp, W, St, Xb, Out, N, K, M, s);
     } else if (aligned(St, 4) && stream_plan(N, K, M, p)) {
         launch_stream_m<OutT>(p, W, St, Xb, Out, N, K, M, s);
@@ -1329,7 +1481,12 @@ int audit_kslice(int N, int K, int M, const KsPlan& p)
     const int T = ks_tiles(N), G = p.grid, nw = p.nw, depth = p.depth;
     if (N < 16 || (K & 511) || nw != (K >> 9) || nw > kKsMaxWaves || G < 1 || G > T) return 2;
     if (depth < 2 || depth > 3 || p.lds > kLdsPerCU) return 3;
-    if ((size_t)nw * depth * kKsSlotBytes + (size_t)p.nt_max * nw * 1024 > p.lds) return 3;
+    if (p.batched) {
+        if ((size_t)nw * depth * kKsSlotBytes + (size_t)kKsBatch * nw * 1024 + (size_t)p.nt_max * 1024 > p.lds)
+            return 3;
+    } else if ((size_t)nw * depth * kKsSlotBytes + (size_t)p.nt_max * nw * 1024 > p.lds) {
+        return 3;
+    }
     const size_t wbytes = (size_t)N * (size_t)(K >> 1), sbytes = (size_t)N * (size_t)(K >> 5);
     const size_t xbytes = (size_t)M * (size_t)K * 2;
     const size_t slot = kKsSlotBytes;
@@ -1337,7 +1494,7 @@ int audit_kslice(int N, int K, int M, const KsPlan& p)
     for (int b = 0; b < G; ++b) {
         int t0, nt, tstride;
         ks_tiles_of(b, T, G, p.interleaved != 0, t0, nt, tstride);
-        if (nt < 1 || nt > kKsTmax || nt > p.nt_max) return 4;
+        if (nt < 1 || (!p.batched && nt > kKsTmax) || nt > p.nt_max) return 4;
         for (int i = 0; i < nt; ++i) {                    // every tile exactly once
             const long t = (long)t0 + (long)i * tstride;
             if (t < 0 || t >= T || seen[(size_t)t]) return 4;
@@ -1378,7 +1535,14 @@ int audit_kslice(int N, int K, int M, const KsPlan& p)
                         if (stream_w_read_off(r, q, u) + 16 > kStepCodeBytes) return 12;
                     if (sl + slot > p.lds) return 13;
                     const size_t rings = (size_t)nw * depth * slot;
-                    if (rings + (((size_t)i * nw + w) * 64 + lane) * 16 + 16 > p.lds) return 14;
+                    if (p.batched) {
+                        // partial tile (i mod B, w), then output tile i (batched kernel)
+                        const size_t redb = (size_t)kKsBatch * nw * 1024;
+                        if ((((size_t)(i % kKsBatch) * nw + w) * 64 + lane) * 16 + 16 > redb) return 14;
+                        if (rings + redb + ((size_t)i * 64 + lane) * 16 + 16 > p.lds) return 14;
+                    } else if (rings + (((size_t)i * nw + w) * 64 + lane) * 16 + 16 > p.lds) {
+                        return 14;
+                    }
                 }
             }
         }
@@ -1479,7 +1643,7 @@ extern "C" int fp8kv_h4mv_audit(int N, int K, int M)
     M1Plan mp;
     if (m1_plan(N, K, M, mp)) return audit_m1(N, K, mp);
     KsPlan kp;
-    if (kslice_plan(N, K, M, kp)) return audit_kslice(N, K, M, kp);
+    if (kslice_plan(N, K, M, kp, true)) return audit_kslice(N, K, M, kp);
     StreamPlan p;
     if (!stream_plan(N, K, M, p)) return 1;
     return audit_stream(N, K, M, p);

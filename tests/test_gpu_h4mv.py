@@ -260,6 +260,26 @@ def test_kslice_variants(depth, N, K, order):
         lib.fp8kv_h4mv_m1_tune(0, 0, 0)
 
 
+@pytest.mark.parametrize("N,K,oracle", [(70000, 4096, True), (128167, 3584, False)])
+def test_kslice_batched_and_rounds_agree(N, K, oracle):
+    """More tiles than one round of 256 workgroups holds: the batched kernel (one round, partial
+    tiles added every 8 tiles) and the plain K-slice kernel over whole rounds (forced with a
+    workgroup target) add the same partials in the same order, so they agree bit for bit; the
+    batched result also meets the oracle bar (the lm_head shape's oracle check is in
+    test_gpu_lm_head.py)."""
+    case = workloads.w4_case(N=N, K=K, M=8, seed=N + 11)
+    a = _run(case, out_dtype=torch.float32)
+    lib = _lib.load()
+    try:
+        lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 768)
+        b = _run(case, out_dtype=torch.float32)
+    finally:
+        lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+    assert np.array_equal(a, b)
+    if oracle:
+        _check(case)
+
+
 def test_kslice_and_streaming_kernels_agree():
     """Both LDS kernels on the same cfg1 inputs (K-slice by default, streaming forced): within
     the fp32 rounding of their different accumulation orders."""
