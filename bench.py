@@ -41,7 +41,7 @@ ROTATE_BYTES = 1 << 30         # >= 4x the 256 MB MALL
 # HBM bytes per launch of each leg's kernel, from two rocprofv3 --pmc runs of this script
 # (FETCH_SIZE, then WRITE_SIZE, scaled by what they read for a 256 MiB copy; commands and tables in
 # profiles/*.md).  They are properties of the kernels as built when profiled, not measured here.
-MEASURED_TRAFFIC = {"w4_gemv_M1": 62581074, "decode_b8_4k": 35962052, "prefill_cfg3": 33882803}
+MEASURED_TRAFFIC = {"w4_gemv_M1": 62581458, "decode_b8_4k": 35964036, "prefill_cfg3": 33883059}
 METRIC = "µs/layer + achieved HBM GB/s (%roofline): decode attn b8@4k, W4 GEMV M=1"
 
 
