@@ -33,10 +33,11 @@ def _capture(fn):
 
 
 @pytest.mark.parametrize("N,K,M", [(28672, 4096, 1), (37888, 3584, 1), (37888, 3584, 8), (4096, 3584, 8),
-                                   (3584, 18944, 8), (4096, 3584, 1), (40003, 3584, 8)])
+                                   (3584, 18944, 8), (4096, 3584, 1), (40003, 3584, 8), (70000, 4096, 8)])
 def test_matvec_replay(N, K, M):
     """M = 1 kernel (cfg1 and gate/up at M = 1), K-slice kernel (gate/up, M = 8; a partial last
-    tile at N = 40003) and streaming kernel (the small-N shapes)."""
+    tile at N = 40003), its batched form (N = 70000: more tiles than one round of the plain
+    kernel holds) and streaming kernel (the small-N shapes)."""
     c = workloads.w4_case(N=N, K=K, M=M, seed=N + M)
     X, W, St = c["X"].to(DEV), c["W"].to(DEV), c["St"].to(DEV)
     Y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
