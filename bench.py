@@ -56,10 +56,12 @@ def decode_bytes(ctx, HQ: int, HKV: int, D: int, PBLK: int) -> int:
             + sum(math.ceil(c / PBLK) for c in ctx) * 4)
 
 
-def time_launches(launch, n_sets: int, steps: int, warmup: int, arm: bool = True):
+def time_launches(launch, n_sets: int, steps: int, warmup: int, arm=True):
     """Run ``launch(i % n_sets)`` warmup + steps times.
 
-    Returns (wall ms per step over the timed region, list of per-launch kernel ms).  With
+    Returns (wall ms per step over the timed region, list of per-launch kernel ms).  ``arm`` True
+    arms the library's timing hook before each timed launch; a callable is called as
+    ``arm(start_event, stop_event)`` instead (a launch that takes its events itself); with
     ``arm=False`` (a launch that is not this library's) each launch is bracketed by two events
     recorded on the stream instead, which adds the marker overhead to its duration."""
     import torch
@@ -79,7 +81,10 @@ def time_launches(launch, n_sets: int, steps: int, warmup: int, arm: bool = True
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record()
     for i in range(steps):
-        if arm:
+        if callable(arm):
+            arm(st[i].cuda_event, en[i].cuda_event)
+            launch(i % n_sets)
+        elif arm:
             lib.fp8kv_time_next_launch(st[i].cuda_event, en[i].cuda_event)
             launch(i % n_sets)
         else:
@@ -541,13 +546,19 @@ def bench_stream_read(nbytes: int, steps: int, warmup: int):
     n_sets = max(4, -(-2 * (256 << 20) // nbytes) + 1)
     bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(n_sets)]
     sink = torch.empty(4096, dtype=torch.int32, device=dev)
-    lib = _lib.load()
+    lib = _lib.load_measure()
+    events = [None, None]
+
+    def arm(a, b):
+        events[:] = [a, b]
 
     def launch(i):
         _lib.check("fp8kv_stream_read", lib.fp8kv_stream_read(bufs[i].data_ptr(), nbytes, sink.data_ptr(),
-                                                                torch.cuda.current_stream().cuda_stream))
+                                                                torch.cuda.current_stream().cuda_stream,
+                                                                events[0], events[1]))
+        events[:] = [None, None]
 
-    wall, per = time_launches(launch, n_sets, steps, warmup)
+    wall, per = time_launches(launch, n_sets, steps, warmup, arm=arm)
     del bufs
     torch.cuda.empty_cache()
     r = _summary(wall, per, nbytes)

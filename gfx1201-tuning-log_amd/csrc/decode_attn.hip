@@ -467,8 +467,8 @@ constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
 // Launch tunables (host state; fp8kv_decode_tune changes them for sweeps).
 constexpr int kDefaultVariant = 4;
-int g_variant = kDefaultVariant;
-int g_target_wgs = 256;
+thread_local int g_variant = kDefaultVariant;
+thread_local int g_target_wgs = 256;
 
 // Splits per (sequence, kv head): enough workgroups to reach g_target_wgs (one per CU: at the
 // kernel's register use only one 8-wave workgroup fits on a CU, so a larger grid runs in two

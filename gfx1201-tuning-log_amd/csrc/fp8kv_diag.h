@@ -1,5 +1,16 @@
 /* Diagnostics exported by libfp8kv_amd.so for the tests and the benchmark (not part of the drop-in ABI in
- * include/fp8kv_amd.h): host-only audits and tuning hooks, and one measurement kernel. */
+ * include/fp8kv_amd.h): host-only audits, tuning hooks and the launch-timing hook.  Every tuning hook
+ * and the timing hook set state of the calling host thread only (thread_local): "later launches"
+ * below means later launches from that thread, and a sweep on one thread never changes the kernels
+ * another thread launches.
+ *
+ * The benchmark's read-only reference launch lives in a library of its own, libfp8kv_measure.so
+ * (csrc/stream_read.hip), which the product library does not contain:
+ *   int fp8kv_stream_read(const void* src, size_t bytes, void* sink, void* stream,
+ *                         void* start_event, void* stop_event);
+ * reads `bytes` (a multiple of 16, at most 16 GiB) from the 16-byte aligned `src` once, with 16-byte
+ * non-temporal loads all in flight at once, writes one dword per workgroup to `sink` (4096 dwords
+ * suffice) and stamps the two hipEvent_t (either may be NULL) at the dispatch's start and end. */
 #ifndef FP8KV_DIAG_H
 #define FP8KV_DIAG_H
 #ifdef __cplusplus
@@ -70,12 +81,6 @@ void fp8kv_gemm_tune(int variant, int order);
  * hipExtLaunchKernel.  hipEventElapsedTime between them is then the kernel's execution time.
  * The events are used once; a rejected call leaves them armed for the next launch. */
 void fp8kv_time_next_launch(void* start_event, void* stop_event);
-
-/* Measurement kernel: reads `bytes` (a multiple of 16, at most 16 GiB) from the 16-byte aligned
- * `src` once, with 16-byte non-temporal loads all in flight at once, and writes one dword per
- * workgroup to `sink` (4096 dwords suffice; so the loads are not dead).  The benchmark's reference for what one read-only launch of a given size reaches
- * on the box. */
-int fp8kv_stream_read(const void* src, size_t bytes, void* sink, void* stream);
 
 #ifdef __cplusplus
 }

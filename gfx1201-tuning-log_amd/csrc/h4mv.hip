@@ -1081,10 +1081,10 @@ constexpr size_t kLdsPerCU = 160 * 1024;
 // Tunables (host state; fp8kv_h4mv_tune changes them for sweeps).  0 = the measured defaults:
 // one wave per tile when there are >= 1024 tiles, otherwise a K split aiming at 4096 waves, and
 // a two-slot ring (deeper rings measured slower at every cfg1/cfg4 shape).
-int g_target_waves = 0;
-int g_depth_override = 0;
-int g_rt_override = 0;
-int g_xg_override = 0;          // 1: activation copies through LDS, 2: direct activation loads
+thread_local int g_target_waves = 0;
+thread_local int g_depth_override = 0;
+thread_local int g_rt_override = 0;
+thread_local int g_xg_override = 0;          // 1: activation copies through LDS, 2: direct activation loads
 
 inline int stream_mmax(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
@@ -1195,10 +1195,10 @@ void launch_stream_m(const StreamPlan& p, const void* W, const void* St, const v
 
 // K-slice planner (tunables: fp8kv_h4mv_kslice_tune).  mode 0: used from M = kKsMinM on when
 // every CU gets at least two tiles; 1: whenever the shape allows it; 2: never.
-int g_kslice_mode = 0;
-int g_kslice_depth = 0;
-int g_kslice_order = 0;         // 0: default, 1: contiguous, 2: interleaved
-int g_kslice_wgs = 0;           // workgroups the planner aims for (0: kKsWorkgroups)
+thread_local int g_kslice_mode = 0;
+thread_local int g_kslice_depth = 0;
+thread_local int g_kslice_order = 0;         // 0: default, 1: contiguous, 2: interleaved
+thread_local int g_kslice_wgs = 0;           // workgroups the planner aims for (0: kKsWorkgroups)
 
 constexpr int kKsBatch = 8;                    // tiles per partial-tile batch (batched kernel)
 
@@ -1283,9 +1283,9 @@ void launch_kslice(const KsPlan& p, const void* W, const void* St, const void* X
 
 // M = 1 planner (tunables: fp8kv_h4mv_m1_tune).  mode 0: used for M = 1 when the tiles alone fill
 // the GPU (>= kM1MinTiles); 1: whenever the shape allows it; 2: never.
-int g_m1_mode = 0;
-int g_m1_depth = 0;
-int g_m1_wgs = 0;               // workgroups the planner aims for (0: kM1Workgroups)
+thread_local int g_m1_mode = 0;
+thread_local int g_m1_depth = 0;
+thread_local int g_m1_wgs = 0;               // workgroups the planner aims for (0: kM1Workgroups)
 
 struct M1Plan {
     int tw, grid, depth;

@@ -852,7 +852,7 @@ constexpr SplitShape kSplitShapes[] = {{3, 2}, {3, 4}, {2, 2}, {2, 4}, {2, 8}};
 constexpr int kNumSplitShapes = sizeof(kSplitShapes) / sizeof(kSplitShapes[0]);
 // -1: choose by GQA; kNumShapes + s: key-split shape s; kNumShapes + kNumSplitShapes + s: the
 // same with paired token blocks whatever the grid size.
-int g_shape = -1;
+thread_local int g_shape = -1;
 
 inline int split_shape_for(int gqa)
 {

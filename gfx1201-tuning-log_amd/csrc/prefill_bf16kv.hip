@@ -192,7 +192,7 @@ int setup(Params& P, const void* q, int64_t q_row_stride, const void* k_cache, c
 
 // Heads per wave: two wherever GQA > 1, so both row-sets use one set of K/V loads (configs[3]:
 // 222 against 377 us with one head per wave; 1024 over 1024: 98.7 against 122.6 us); one for MHA.
-int g_rs_override = 0;
+thread_local int g_rs_override = 0;
 
 int launch(Params& P, int num_seqs, int max_query_len, hipStream_t stream)
 {

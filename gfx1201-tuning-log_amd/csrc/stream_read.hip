@@ -1,4 +1,5 @@
-// Measurement helper (not part of the drop-in ABI): one launch that reads a buffer once.
+// Measurement helper (not part of the drop-in ABI, and built into its own library,
+// libfp8kv_measure.so, which only the benchmark loads): one launch that reads a buffer once.
 //
 // The benchmark times it beside the HBM-bound kernels at their own byte counts, so their roofline
 // fractions can be read against what a single read-only launch of the same size reaches on the
@@ -8,7 +9,6 @@
 // and 64 MB, 512-2048 workgroups were fastest, 1024 x 256 within 1%).
 #include "fp8kv_common.h"
 #include "fp8kv_status.h"
-#include "fp8kv_diag.h"
 
 namespace fp8kv {
 namespace stream_detail {
@@ -42,11 +42,12 @@ __global__ void __launch_bounds__(kThreads) stream_read_kernel(const u32x4_t* __
 }  // namespace stream_detail
 }  // namespace fp8kv
 
-extern "C" int fp8kv_stream_read(const void* src, size_t bytes, void* sink, void* stream)
+extern "C" int fp8kv_stream_read(const void* src, size_t bytes, void* sink, void* stream, void* start_event,
+                                 void* stop_event)
 {
-    using namespace fp8kv;
     using namespace fp8kv::stream_detail;
-    if (!src || !sink || bytes < 16 || (bytes & 15) || !aligned(src, 16) || !aligned(sink, 4)) return FP8KV_ERR_ARG;
+    if (!src || !sink || bytes < 16 || (bytes & 15) || !fp8kv::aligned(src, 16) || !fp8kv::aligned(sink, 4))
+        return FP8KV_ERR_ARG;
     // 1024 workgroups while that keeps 16 or fewer loads per thread (the probe's best shape for 32
     // and 64 MB), more beyond; sizes past kMaxBlocks * 256 * 16 vectors (16 GiB) are refused.
     const size_t n16 = bytes / 16;
@@ -54,8 +55,11 @@ extern "C" int fp8kv_stream_read(const void* src, size_t bytes, void* sink, void
     if (blocks < 1024) blocks = 1024;
     if (blocks > kMaxBlocks) return FP8KV_ERR_SHAPE;
     const int per = (int)((n16 + blocks * kThreads - 1) / (blocks * kThreads));
-    begin_launch();
-    launch_kernel(stream_read_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, reinterpret_cast<hipStream_t>(stream),
-                  static_cast<const u32x4_t*>(src), n16, per, static_cast<uint32_t*>(sink));
-    return finish_launch();
+    (void)hipGetLastError();
+    // hipExtLaunchKernel stamps the events (either may be NULL) at the dispatch's own start and end
+    hipExtLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
+                          reinterpret_cast<hipStream_t>(stream), static_cast<hipEvent_t>(start_event),
+                          static_cast<hipEvent_t>(stop_event), 0, static_cast<const u32x4_t*>(src), n16,
+                          per, static_cast<uint32_t*>(sink));
+    return hipGetLastError() == hipSuccess ? FP8KV_OK : FP8KV_ERR_LAUNCH;
 }

@@ -50,7 +50,7 @@ constexpr int kXcds = 8;
 // least 256 tiles or K >= 8192, else variant 5 (measured at the configs[4] linears, M = 2048:
 // gate/up 1.41 -> 1.66 PFLOP/s and down 1.41 -> 1.47 with variant 6, o 1.27 -> 1.22).
 constexpr int kDefaultVariant = -1;
-int g_gemm_variant = kDefaultVariant;
+thread_local int g_gemm_variant = kDefaultVariant;
 
 inline int default_variant(int N, int K, int M)
 {
@@ -61,7 +61,7 @@ inline int default_variant(int N, int K, int M)
 inline int pick_variant(int N, int K, int M) { return g_gemm_variant >= 0 ? g_gemm_variant : default_variant(N, K, M); }
 // 0: XCD split by the traffic model of pick_split (default); 1: XCDs split the weight blocks
 // only; 2: XCDs split the token blocks as far as their count allows.
-int g_gemm_order = 0;
+thread_local int g_gemm_order = 0;
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 

@@ -9,7 +9,7 @@ import ctypes
 import os
 import threading
 
-from .build import LIB_PATH
+from .build import LIB_PATH, MEASURE_LIB_PATH
 
 _c_vp = ctypes.c_void_p
 _c_i = ctypes.c_int
@@ -82,11 +82,16 @@ SIGNATURES: dict[str, tuple] = {
     "fp8kv_prefill_plan": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_vp]),
     "fp8kv_gemm_tune": (None, [_c_i, _c_i]),
     "fp8kv_time_next_launch": (None, [_c_vp, _c_vp]),
-    "fp8kv_stream_read": (_c_i, [_c_vp, _c_sz, _c_vp, _c_vp]),
+}
+
+# libfp8kv_measure.so: the benchmark's read-only reference launch (csrc/stream_read.hip).
+MEASURE_SIGNATURES: dict[str, tuple] = {
+    "fp8kv_stream_read": (_c_i, [_c_vp, _c_sz, _c_vp, _c_vp, _c_vp, _c_vp]),
 }
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_measure: ctypes.CDLL | None = None
 
 
 class Fp8kvError(RuntimeError):
@@ -125,6 +130,23 @@ def load() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = lib
         return lib
+
+
+def load_measure() -> ctypes.CDLL:
+    """Load (once) the benchmark's measurement library (fp8kv_stream_read); not part of the path."""
+    global _measure
+    load()
+    with _lock:
+        if _measure is None:
+            if not os.path.exists(MEASURE_LIB_PATH):
+                raise FileNotFoundError(f"{MEASURE_LIB_PATH} is missing: build it with fp8kv_amd.build.build()")
+            lib = ctypes.CDLL(MEASURE_LIB_PATH)
+            for name, (res, args) in MEASURE_SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _measure = lib
+        return _measure
 
 
 def check(fn_name: str, status: int) -> None:

@@ -507,13 +507,40 @@ def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor,
 # ------------------------------------------------------------------------------ lm_head, top-k, rerank
 
 _topk_ws: dict = {}
+# Workspaces replaced by a larger one stay alive for the life of the process, as the decode
+# scratch does: a graph captured while one was current replays its logits and candidates into it.
+_topk_ws_retired: list = []
+
+
+def topk_workspace(nbytes: int, device, allow_alloc: bool = True) -> torch.Tensor | None:
+    """The per-device cached lm_head workspace, grown to at least ``nbytes``.  A replaced buffer
+    is kept alive; with ``allow_alloc=False`` (graph capture) a too-small cache returns None.
+    Every call on a device shares this buffer, so calls that overlap on different streams race:
+    pass an explicit workspace per stream instead."""
+    dev = torch.device(device)
+    idx = dev.index
+    if idx is None:
+        idx = torch.cuda.current_device() if dev.type == "cuda" else 0
+    key = (dev.type, idx)
+    buf = _topk_ws.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if not allow_alloc:
+            return None
+        if buf is not None:
+            _topk_ws_retired.append(buf)
+        buf = torch.empty(max(nbytes, 2 * buf.numel() if buf is not None else nbytes), dtype=torch.uint8,
+                          device=dev)
+        _topk_ws[key] = buf
+    return buf
 
 
 def lm_head_topk(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor, k: int,
                  workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """(values fp32 [M, k], indices int32 [M, k]) of the k largest logits x . dequant(W)^T per row,
     in rank order (value descending, NaN first, ties by lower index).  h4mv_topk; the workspace
-    defaults to a per-device cached buffer."""
+    defaults to the per-device cached buffer of ``topk_workspace``, which calls on one device
+    share (calls overlapping on different streams must pass their own).  During graph capture
+    the cache is not grown: capture a call whose workspace is already large enough, or pass one."""
     _require(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(),
              "x must be a contiguous 2-D bf16 device tensor")
     M, K = x.shape
@@ -526,11 +553,9 @@ def lm_head_topk(x: torch.Tensor, weight: torch.Tensor, scales_nk: torch.Tensor,
     need = int(lib.h4mv_topk_workspace_bytes(N, M, int(k)))
     _require(need > 0, f"k={k} outside [1, 64]")
     if workspace is None:
-        key = (x.device.index if x.device.index is not None else torch.cuda.current_device())
-        workspace = _topk_ws.get(key)
-        if workspace is None or workspace.numel() < need:
-            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-            _topk_ws[key] = workspace
+        workspace = topk_workspace(need, x.device, allow_alloc=not torch.cuda.is_current_stream_capturing())
+        _require(workspace is not None,
+                 f"lm_head_topk during graph capture needs {need} workspace bytes: pass a workspace")
     vals = torch.empty((M, k), dtype=torch.float32, device=x.device)
     idx = torch.empty((M, k), dtype=torch.int32, device=x.device)
     st = lib.h4mv_topk(weight.data_ptr(), scales_nk.data_ptr(), x.data_ptr(), N, K, M, int(k),

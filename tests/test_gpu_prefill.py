@@ -245,6 +245,72 @@ def test_every_split_shape(split, paired):
         lib.fp8kv_prefill_tune(-1)
 
 
+def _plan(lib, hq, hkv, num_seqs, max_query_len, ctx_hint):
+    import ctypes
+    out = (ctypes.c_int * 8)()
+    assert lib.fp8kv_prefill_plan(hq, hkv, num_seqs, max_query_len, ctx_hint, ctypes.addressof(out)) == 0
+    return dict(zip(("split", "shape", "nb", "paired", "ntb", "grid_x", "grid_z", "threads"), list(out)))
+
+
+@pytest.mark.parametrize("case", ["configs3_paired", "1k_over_1k_single", "forced_paired_gqa6",
+                                  "forced_paired_gqa4", "varlen_paired"])
+def test_split_kernel_repeats_bitwise(case):
+    """The key-split kernel is deterministic: its partial states merge in LDS in a fixed order and
+    every copy is waited for by count, so repeated calls on the same inputs give the same bits.
+    Ten calls each on the configs[3] plan (256 workgroups of two paired token blocks), the
+    single-block plan (1024 over 1024), the paired plan forced onto a smaller grid at GQA 6 and
+    4, and the paired varlen plan; the first call is also checked against the oracle."""
+    lib = _lib.load()
+    tune = -1
+    if case == "configs3_paired":
+        qlens, q0s, hq, layout = [2048], [2048], 24, "engine"
+    elif case == "1k_over_1k_single":
+        qlens, q0s, hq, layout = [1024], [1024], 24, "engine"
+    elif case == "forced_paired_gqa6":
+        qlens, q0s, hq, layout, tune = [600], [700], 24, "standalone", SPLIT_PAIRED + 0
+    elif case == "forced_paired_gqa4":
+        qlens, q0s, hq, layout, tune = [600], [700], 16, "standalone", SPLIT_PAIRED + 2
+    else:
+        qlens, q0s, hq, layout = [1100, 1030, 300], [0, 40, 900], 24, "engine"
+    c = workloads.prefill_case(qlens, q0s, HQ=hq, HKV=4, seed=len(case) + 400, layout=layout)
+    d = workloads.to_device(c, DEV)
+    ks = torch.tensor([c["k_scale"]], device=DEV)
+    vs = torch.tensor([c["v_scale"]], device=DEV)
+    varlen = len(qlens) > 1
+    try:
+        lib.fp8kv_prefill_tune(tune)
+        if varlen:
+            p = _plan(lib, hq, 4, len(qlens), max(qlens), max(qlens))
+        else:
+            p = _plan(lib, hq, 4, 1, qlens[0], q0s[0] + qlens[0])
+        assert p["split"] == 1, p                       # the key-split kernel serves every case
+        assert p["paired"] == (case != "1k_over_1k_single"), p
+        outs = []
+        for _ in range(10):
+            out = torch.zeros_like(d["q"])
+            if varlen:
+                ops.prefill_attention_varlen(d["q"], d["k_cache"], d["v_cache"], out, d["cu_seqlens_q"],
+                                             d["seq_lens"], d["block_table"], ks, vs, c["sm_scale"])
+            else:
+                ops.prefill_attention(d["q"], d["k_cache"], d["v_cache"], out, d["block_table"], ks, vs,
+                                      c["sm_scale"], q0s[0], qlens[0])
+            outs.append(out)
+        torch.cuda.synchronize()
+    finally:
+        lib.fp8kv_prefill_tune(-1)
+    for i, o in enumerate(outs[1:], 1):
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16)), f"call {i} differs"
+    if varlen:
+        ref = attention.varlen_prefill_attention(c["q"], c["k_cache"], c["v_cache"], c["cu_seqlens_q"],
+                                                 c["seq_lens"], c["block_table"], c["k_scale"],
+                                                 c["v_scale"], c["sm_scale"], dtype=torch.float32)
+        got = outs[0].cpu()
+    else:
+        ref = _oracle_single(c, q0s[0], qlens[0], dtype=torch.float32)
+        got = outs[0].cpu()[:qlens[0]]
+    torch.testing.assert_close(got.to(torch.float64), ref.to(torch.float64), rtol=RTOL, atol=ATOL)
+
+
 @pytest.mark.parametrize("gqa", SPLIT_GQA)
 def test_split_paired_default_plan(gqa):
     """Grids above one round of 256 workgroups take paired token blocks on the default plan:

@@ -642,3 +642,20 @@ def test_hipw4_gemm_gate_rejections(monkeypatch, case):
     elif case == "fp32":
         x = x.float()
     assert not h.gemm_path_ok(x, w, s, 4, torch)
+
+
+def test_topk_workspace_never_frees_a_replaced_buffer(monkeypatch):
+    """lm_head_topk's cached workspace: a larger request replaces it but keeps the old buffer
+    alive (a captured graph replays into it), and no buffer is allocated when allocation is off."""
+    from fp8kv_amd import ops
+    monkeypatch.setattr(ops, "_topk_ws", {})
+    monkeypatch.setattr(ops, "_topk_ws_retired", [])
+    assert ops.topk_workspace(1000, "cpu", allow_alloc=False) is None
+    a = ops.topk_workspace(1000, "cpu")
+    assert a.numel() == 1000
+    assert ops.topk_workspace(600, "cpu") is a
+    assert ops.topk_workspace(5000, "cpu", allow_alloc=False) is None
+    b = ops.topk_workspace(1500, "cpu")
+    assert b is not a and b.numel() >= 2000
+    assert ops._topk_ws_retired == [a]
+    assert ops.topk_workspace(1800, "cpu", allow_alloc=False) is b
