@@ -623,9 +623,11 @@ constexpr int kMaxDevices = 64;
 std::mutex g_noalloc_mu;
 void* g_noalloc_ptr[kMaxDevices] = {};
 
-// The device address of `scratch` on the current device.  The first call on a device resolves it
-// and zeroes its ticket region with a kernel on `st` (the records need no initial state).
-int noalloc_scratch(hipStream_t st, void** out)
+// The device address of `scratch` on the current device, resolved by the first call on that
+// device.  Nothing is launched for it: the array is zero when the code object is loaded (it has no
+// initializer), and every completed decode call leaves its tickets at zero again, so a first call
+// captured into a graph records no extra node (the records need no initial state).
+int noalloc_scratch(void** out)
 {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -642,8 +644,6 @@ int noalloc_scratch(hipStream_t st, void** out)
             g_last_hip_error = (int)e;
             return FP8KV_ERR_LAUNCH;
         }
-        const int rc = launch_scratch_zero(ptr, counters_bytes(), st);
-        if (rc != FP8KV_OK) return rc;
         g_noalloc_ptr[dev] = ptr;
     }
     *out = g_noalloc_ptr[dev];
@@ -723,7 +723,7 @@ extern "C" int fp8kv_decode_attn_noalloc(const void* q, int64_t q_row_stride,
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     void* ptr = nullptr;
     if (need > 0) {
-        rc = noalloc_scratch(st, &ptr);
+        rc = noalloc_scratch(&ptr);
         if (rc != FP8KV_OK) return rc;
     }
     use_scratch(P, ptr, need);

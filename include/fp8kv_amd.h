@@ -50,6 +50,11 @@ const char* fp8kv_last_hip_error_string(void);
  * Same symbol, same signature, same argument meaning.  Differences: M up to 16 (the reference runs
  * M > 8 silently as M = 8), bf16 rounding is nearest-even (the reference rounds half up), and a
  * rejected call launches nothing and records its status for fp8kv_last_status().
+ * Non-finite activations depend on M: NaN in X gives NaN outputs at every M (as the reference).
+ * An infinity in X gives +-inf (NaN where its weight is zero) for M >= 2, as the reference does,
+ * but NaN in every output of the row at M = 1 on shapes of at least 1024 row tiles with
+ * K % 512 == 0 (there the row is split into e4m3 parts, which have no infinity, and its 32-k
+ * block takes the NaN scale).
  */
 void h4mv_launch(const void* W, const void* St, const void* Xb, void* Out,
                  int N, int K, int M, void* stream);
@@ -121,8 +126,9 @@ int fp8kv_decode_attn(const void* q, int64_t q_row_stride,
  * or freed.  Same arguments, semantics and results as fp8kv_decode_attn (bit for bit) except that
  * a call needing more than 8 MiB of scratch (fp8kv_decode_scratch_bytes) returns
  * FP8KV_ERR_SCRATCH and launches nothing; every split count the library plans fits at any GQA.
- * The first call on a device also launches a small kernel on `stream` that zeroes the array's
- * ticket region (if that call is captured, the kernel is part of the graph).  Every call on one
+ * The array is zero when the library is loaded and every completed call leaves its tickets at
+ * zero, so no call launches anything besides the decode kernel (a captured first call records no
+ * extra node).  Every call on one
  * GPU shares that GPU's array: calls that overlap in time on one GPU (different streams, or
  * graphs replayed concurrently) race and must be serialised by the caller. */
 int fp8kv_decode_attn_noalloc(const void* q, int64_t q_row_stride,

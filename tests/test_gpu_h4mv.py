@@ -280,6 +280,22 @@ def test_kslice_batched_and_rounds_agree(N, K, oracle):
         _check(case)
 
 
+@pytest.mark.parametrize("order", [1, 2])
+@pytest.mark.parametrize("depth", [2, 3])
+@pytest.mark.parametrize("N,K", [(70003, 2048), (70000, 4096)])
+def test_kslice_batched_variants(N, K, depth, order):
+    """The batched K-slice kernel (more tiles than one round of 256 workgroups holds) at several
+    waves per workgroup (K = 2048: 4 waves, 4096: 8), with a partial last tile (N = 70003), at
+    both ring depths and both tile orders, M = 3 and 8, against the oracle."""
+    lib = _lib.load()
+    try:
+        lib.fp8kv_h4mv_kslice_tune(0, depth, order, 0)
+        for M in (3, 8):
+            _check(workloads.w4_case(N=N, K=K, M=M, seed=N + K + M + depth + 10 * order))
+    finally:
+        lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+
+
 def test_kslice_and_streaming_kernels_agree():
     """Both LDS kernels on the same cfg1 inputs (K-slice by default, streaming forced): within
     the fp32 rounding of their different accumulation orders."""
@@ -405,8 +421,11 @@ def test_m1_scale_bytes_zero_255_and_wide():
 
 def test_m1_zero_nan_and_inf_activations():
     """A zero row gives zeros; NaN anywhere gives NaN everywhere (as the reference); an infinity
-    gives NaN everywhere (the reference gives +-inf or NaN)."""
+    gives NaN everywhere on the M = 1 kernel, while the same row at M = 2 (bf16 kernels) gives
+    +-inf with the sign of its weight and NaN where that weight is zero, as the reference does:
+    the M-dependence documented at h4mv_launch."""
     case = workloads.w4_case(N=64, K=1024, M=1, seed=4)
+    case2 = workloads.w4_case(N=64, K=1024, M=2, seed=4)
     with _M1():
         z = _run(dict(case, X=torch.zeros_like(case["X"])), out_dtype=torch.float32)
         assert np.array_equal(z, np.zeros_like(z))
@@ -415,6 +434,17 @@ def test_m1_zero_nan_and_inf_activations():
             x[0, 700] = bad
             y = _run(dict(case, X=x), out_dtype=torch.float32)
             assert np.isnan(y).all(), bad
+            x2 = torch.stack([x[0], case2["X"][1]])
+            y2 = _run(dict(case, X=x2), out_dtype=torch.float32)
+            if bad != bad:
+                assert np.isnan(y2[0]).all()
+            else:
+                ref = _oracle(dict(case, X=x2))
+                # the oracle's fp64 product: +-inf by the weight's sign, NaN where it is zero
+                assert np.array_equal(np.isnan(y2[0]), np.isnan(ref[0]))
+                fin = ~np.isnan(ref[0])
+                assert np.array_equal(y2[0][fin], ref[0][fin]) and np.isinf(y2[0][fin]).all()
+            assert np.isfinite(y2[1]).all()
 
 
 def test_m1_and_streaming_kernels_agree():

@@ -66,6 +66,8 @@ def test_h4mv_kslice_in_bounds(lib, depth, order, wgs):
         shapes += [(16, 512), (4112, 1024), (8208, 2048), (65536, 512), (66048, 512)]
         # partial last tiles (N % 16 != 0): the lm_head vocabulary, the smallest N, random N
         shapes += [(128167, 3584), (17, 512), (31, 1024), (4097, 1024), (40003, 3584)]
+        # the batched form (more tiles than one round holds) with a partial last tile
+        shapes += [(70003, 2048), (70003, 4096), (70000, 4096)]
         for _ in range(60):
             shapes.append((16 * rng.randrange(1, 5000), 512 * rng.randrange(1, 9)))
         for _ in range(30):

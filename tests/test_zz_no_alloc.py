@@ -82,3 +82,40 @@ def test_noalloc_rejects_scratch_beyond_its_array():
     assert st == 5 and torch.all(out == 5.0)
     # a split count that fits on the same batch still works right after the refusal
     _check(c, 2)
+
+
+def test_noalloc_graph_replays():
+    """The no-allocation call captured in a HIP graph: every replay, with new query values copied
+    into the captured input between replays (and eager calls of the other entry point in
+    between), equals an eager fp8kv_decode_attn call on the same inputs bit for bit."""
+    lib = _lib.load()
+    c = workloads.decode_case([1500, 4096, 77, 2048], pool_blocks=2000, seed=34, layout="engine")
+    d = workloads.to_device(c, DEV)
+    NS, HQ, HKV = 4, d["q"].shape[1], d["k_cache"].shape[2]
+    nsplit = ops.decode_num_splits(NS, HKV, 4096)
+    out = torch.zeros_like(d["q"])
+    args = _args(d, c, out, nsplit)
+    keep = d["_keep"]                   # the captured call's scale tensors stay alive
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            assert lib.fp8kv_decode_attn_noalloc(*args, s.cuda_stream) == 0
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    need = ops.decode_scratch_bytes(NS, HQ, HKV, nsplit)
+    scratch = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(35)
+    for rep in range(4):
+        d["q"].copy_(torch.randn(d["q"].shape, device=DEV, generator=gen).to(torch.bfloat16))
+        out.fill_(5.0)
+        g.replay()
+        torch.cuda.synchronize()
+        ref_out = torch.full_like(d["q"], 7.0)
+        st = lib.fp8kv_decode_attn(*_args(d, c, ref_out, nsplit), scratch.data_ptr(), need,
+                                   torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert st == 0
+        assert torch.equal(out, ref_out), f"replay {rep}"
+    del g, keep
