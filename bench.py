@@ -40,8 +40,21 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0 # MI355X dense bf16 MFMA
 ROTATE_BYTES = 1 << 30         # >= 4x the 256 MB MALL
 # HBM bytes per launch of each leg's kernel, from two rocprofv3 --pmc runs of this script
 # (FETCH_SIZE, then WRITE_SIZE, scaled by what they read for a 256 MiB copy; commands and tables in
-# profiles/*.md).  They are properties of the kernels as built when profiled, not measured here.
+# the profile named beside each).  Static: properties of the kernels as built when profiled, not
+# measured by this run (counters need the profiler).
 MEASURED_TRAFFIC = {"w4_gemv_M1": 62581458, "decode_b8_4k": 35964036, "prefill_cfg3": 33883059}
+TRAFFIC_SOURCE = {
+    "w4_gemv_M1": "static: profiles/h4mv_m1_kslice_kernels_cfg1.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
+    "decode_b8_4k": "static: profiles/decode_kernel_b8_4k.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
+    "prefill_cfg3": "static: profiles/prefill_kernel_cfg3.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
+}
+# The clocks behind the roofline fractions: "frac" divides by each kernel's own duration from
+# dispatch-stamped HIP events (hipExtLaunchKernel) on the launches issued one by one; "frac_graph"
+# by the wall time per launch of the same launches replayed from one HIP graph (launch gaps
+# included, the clock of "value").  A rocprofv3 kernel trace of the same launches reads 0.3-0.8 us
+# longer than the events (its figures and this run's event figures sit side by side in profiles/).
+CLOCKS = ("frac: bytes / mean kernel duration from dispatch-stamped HIP events; frac_graph: bytes / "
+          "wall time per launch under HIP-graph replay (the clock of value)")
 METRIC = "µs/layer + achieved HBM GB/s (%roofline): decode attn b8@4k, W4 GEMV M=1"
 
 
@@ -131,6 +144,7 @@ def time_graph(launch, n_sets: int, steps: int, warmup: int, reps: int = 5) -> f
 def _with_graph(r: dict, graph_ms: float, nbytes: int) -> dict:
     r["us_graph"] = round(graph_ms * 1e3, 3)
     r["GBps_graph"] = round(nbytes / (graph_ms * 1e-3) / 1e9, 1)
+    r["frac_graph"] = round(nbytes / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     return r
 
 
@@ -846,7 +860,10 @@ def main():
                    "rotation_sets": head["rotation_sets"]},
         "roofline": {"bound": "hbm", "achieved": head["GBps_kernel"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": head["frac_kernel"],
-                     "traffic": MEASURED_TRAFFIC["w4_gemv_M1" if m1 is not None else "decode_b8_4k"]},
+                     "us_kernel": head["us_kernel"], "us_graph": head["us_graph"],
+                     "frac_graph": head["frac_graph"], "clocks": CLOCKS,
+                     "traffic": MEASURED_TRAFFIC["w4_gemv_M1" if m1 is not None else "decode_b8_4k"],
+                     "traffic_source": TRAFFIC_SOURCE["w4_gemv_M1" if m1 is not None else "decode_b8_4k"]},
         "cpu_baseline": cpu,
         "cpu_legs": extra_cpu,
         "legs": legs,
@@ -867,13 +884,16 @@ def main():
         pf = legs["prefill_cfg3"]
         line["roofline_prefill_cfg3"] = {"bound": "mfma", "achieved": pf["TFLOPs_kernel"],
                                          "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                         "frac": pf["frac_kernel"],
-                                         "traffic": MEASURED_TRAFFIC["prefill_cfg3"]}
+                                         "frac": pf["frac_kernel"], "us_kernel": pf["us_kernel"],
+                                         "traffic": MEASURED_TRAFFIC["prefill_cfg3"],
+                                         "traffic_source": TRAFFIC_SOURCE["prefill_cfg3"]}
     if dec is not None:
         line["roofline_decode_b8_4k"] = {"bound": "hbm", "achieved": dec["GBps_kernel"],
                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                          "frac": dec["frac_kernel"], "us_per_layer": dec["us_kernel"],
-                                         "traffic": MEASURED_TRAFFIC["decode_b8_4k"]}
+                                         "us_graph": dec["us_graph"], "frac_graph": dec["frac_graph"],
+                                         "traffic": MEASURED_TRAFFIC["decode_b8_4k"],
+                                         "traffic_source": TRAFFIC_SOURCE["decode_b8_4k"]}
         if ref_dec is not None:
             line["roofline_decode_b8_4k"]["read_reference_GBps"] = ref_dec["GBps_kernel"]
             line["roofline_decode_b8_4k"]["frac_of_read_reference"] = round(dec["GBps_kernel"] / ref_dec["GBps_kernel"], 4)
