@@ -194,6 +194,14 @@ constexpr int kStepGroups = 16;
 constexpr int kStepCodeBytes = 16 * 256;
 constexpr int kXgLoads = 16;                 // XG: activation fragment loads per step and lane
 constexpr int kDmaAux = 2;                    // streaming cache policy for the code copies
+// Copies read once per launch take the streaming policy too: lines left in L2 by ordinary loads
+// add to the gap between consecutive launches (measured under graph replay: the M = 1 kernel's
+// 3.7 MB of scale slices, copied with the default policy, cost it 0.2-0.3 us per launch there).
+// Not for the K-slice kernels' scale copies: their waves share each scale line through L2 (with
+// the streaming policy cfg1 M = 4 / 8 went 12.6 -> 13.7 / 13.0 -> 14.4 us).
+__device__ __forceinline__ void dma16_to_lds_stream(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 16, 0, kDmaAux);
+}
 
 // LDS layout of one wave (bytes), shared by kernel, planner and audit.
 struct WaveLds {
@@ -364,7 +372,7 @@ h4mv_stream_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St
         for (int t0 = 0; t0 < 16 * RT * per; t0 += 64) {
             const int t = t0 + lane;
             if (t < 16 * RT * per && (t % per) < nsteps)
-                dma16_to_lds(St + stream_s_seg_off(n0, N, K, per, step0, t), sarea + t0 * 16);
+                dma16_to_lds_stream(St + stream_s_seg_off(n0, N, K, per, step0, t), sarea + t0 * 16);
         }
     }
     // ---- fill the ring ------------------------------------------------------------------------
@@ -941,7 +949,7 @@ h4mv_m1_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
     const int nseg = 16 * nsteps;
     for (int t0 = 0; t0 < nseg; t0 += 64) {
         const int t = min(t0 + lane, nseg - 1);
-        dma16_to_lds(St + stream_s_seg_off(n0, N, K, nsteps, 0, t), sarea + t0 * 16);
+        dma16_to_lds_stream(St + stream_s_seg_off(n0, N, K, nsteps, 0, t), sarea + t0 * 16);
     }
 #pragma unroll
     for (int s = 1; s < DEPTH; ++s) issue(min(s, nsteps - 1), ring + s * kStepCodeBytes);
