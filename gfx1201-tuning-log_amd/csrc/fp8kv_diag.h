@@ -44,9 +44,24 @@ void fp8kv_h4mv_kslice_tune(int mode, int depth, int order, int workgroups);
  * Affects later launches and audits. */
 void fp8kv_h4mv_m1_tune(int mode, int depth, int workgroups);
 
+/* Tuning hook for the matvec's M = 2 .. 8 kernel (the M = 1 kernel's e4m3 hi + lo activations, one
+ * column pair per row): mode 0 = used at 2 <= M <= 8 when N / 16 >= 1024 tiles and every workgroup
+ * runs in one round at two workgroups per CU (the default; in practice M <= 4), 1 = whenever the
+ * shape allows it (2 <= M <= 8, K % 512 == 0),
+ * 2 = never; depth = LDS ring slots per wave (3; any other value: 2, the default); workgroups =
+ * workgroup count the planner aims for (0: default).  Affects later launches and audits. */
+void fp8kv_h4mv_mx_tune(int mode, int depth, int workgroups);
+
+/* Planner query of the matvec launch (host only, no GPU call): the kernel h4mv_launch would run
+ * for (N, K, M) under the current tuning hooks.  out[6] = {kernel (0 register path, 1 streaming,
+ * 2 K-slice, 3 M = 1, 4 M = 2 .. 8 hi / lo, 5 batched K-slice), grid, waves per workgroup, ring
+ * depth, dynamic LDS bytes, activation rows (kernels 3 and 4) / row tiles (1) / tiles per
+ * workgroup (2, 5)}.  Returns FP8KV_OK or an argument / shape status. */
+int fp8kv_h4mv_plan(int N, int K, int M, int* out);
+
 /* Tuning hook for sweeps of the decode attention launch: kernel variant index (0..6; any other
- * value, e.g. -1, selects the default, variant 4: 8 waves, chunks of 2 groups of 16 keys, 2 chunks
- * in flight per wave, K bytes requested before V bytes) and the workgroup count its split planner
+ * value, e.g. -1, selects the default, variant 5: 8 waves, chunks of 2 groups of 16 keys, 2 chunks
+ * in flight per wave, each group's K and V bytes requested together) and the workgroup count its split planner
  * aims for (0 = default 256).  Affects later launches. */
 void fp8kv_decode_tune(int variant, int target_wgs);
 

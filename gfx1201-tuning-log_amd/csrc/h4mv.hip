@@ -1035,6 +1035,189 @@ h4mv_m1_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
     store_tile<OutT, EPI>(acc, Out, tile, N, 1, r, q);
 }
 
+// ---------------------------------------------------------------------------------------------
+// M = 2 .. 8 on the block-scaled MFMA: the M = 1 kernel's scheme with one e4m3 hi / lo column
+// pair per activation row.  B of v_mfma_scale_f32_16x16x128_f8f6f4 has 16 columns, so MM = 8 rows
+// fill it (column 2m = hi of row m, 2m + 1 = lo); with MM = 2 or 4 the columns repeat the rows.
+// A step is still four MFMAs per wave, so the math per byte of codes does not grow with M; what
+// grows is the activation block the workgroup converts once (MM rows).  Each output column comes
+// out of the MFMA independently of the others, so row m's result equals the M = 1 kernel's for
+// that row alone, bit for bit.
+//   * LDS: MM rows of 2K + kMxRowPad bytes, then MM rows of block scale bytes, then the waves'
+//     rings and scale slices as in the M = 1 kernel.  Row m is copied in as bf16 (whole 1 KB
+//     copies; rows m >= M repeat row M - 1) and converted in place: thread t takes 16 values
+//     (32 bytes), the two threads of a 32-k block share their maximum with one DPP step, and the
+//     thread writes its 16 hi bytes over the first half of its own 32 bytes and its 16 lo bytes
+//     over the second.  A thread only ever rewrites bytes it alone read.
+//   * B fragment of lane (n, j) for MFMA u of step s: row m = (n / 2) mod MM, half n % 2, k =
+//     512 s + 128 u + 16 j .. + 15 and + 64: 16-byte units 32 s + 8 u + j and + 4 of the row, at
+//     byte 32 unit (+ 16 for lo).  Row stride = 32 mod 256, so lanes 0..15 of a read meet 16
+//     distinct 16-byte bank groups.
+//   * lane (n, q) ends with rows 4q .. 4q + 3 of column n; one DPP step adds column 2m + 1 to
+//     column 2m, and the even lanes store row m (m < M).
+// ---------------------------------------------------------------------------------------------
+constexpr int kMxRowPad = 32;
+
+__host__ __device__ inline int mx_row_bytes(int K) { return 2 * K + kMxRowPad; }
+// Block scale bytes of one row (m1_xe_pos order), padded so that rows start in different banks.
+__host__ __device__ inline int mx_xe_row_bytes(int K) { return (((K >> 5) + 15) & ~15) + 16; }
+__host__ __device__ inline int mx_x_bytes(int mm, int K) { return mm * (mx_row_bytes(K) + mx_xe_row_bytes(K)); }
+// Activation copy unit u (1 KB: 64 lanes x 16 B) of an MM-row block: row u / (K / 512), piece c.
+__host__ __device__ inline size_t mx_copy_src(int K, int M, int u, int lane)
+{
+    const int per_row = K >> 9, m = u / per_row, c = u % per_row;
+    const int mm = m < M ? m : M - 1;
+    return (size_t)mm * (size_t)K * 2 + (size_t)c * 1024 + 16u * (uint32_t)lane;
+}
+__host__ __device__ inline int mx_copy_dst(int K, int u, int lane)
+{
+    const int per_row = K >> 9, m = u / per_row, c = u % per_row;
+    return m * mx_row_bytes(K) + c * 1024 + 16 * lane;
+}
+
+template <int MM, int DEPTH, typename OutT, int EPI>
+__global__ void __launch_bounds__(64 * kM1MaxWaves)
+h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
+               const __bf16* __restrict__ X, OutT* __restrict__ Out, int N, int K, int M)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    const int T = (N + kRowsPerWG - 1) / kRowsPerWG;
+    const int nsteps = K >> 9;
+    const int rowb = mx_row_bytes(K);
+    const int xerow = mx_xe_row_bytes(K);
+
+    unsigned char* xa = smem;                                   // MM rows: bf16, then hi / lo
+    unsigned char* xe = smem + MM * rowb;                       // MM rows of B scale bytes
+    unsigned char* ring = smem + mx_x_bytes(MM, K) + wave * m1_wave_bytes(DEPTH, nsteps);
+    unsigned char* sarea = ring + DEPTH * kStepCodeBytes;
+
+    const int tile_w = blockIdx.x + wave * gridDim.x;
+    const bool has_tile = tile_w < T;                           // wave-uniform
+    const int tile = has_tile ? tile_w : blockIdx.x;
+    const int n0 = tile * kRowsPerWG;
+
+    // ---- the activation rows, the scale slice, then the ring: all copies straight to LDS -------
+    const unsigned char* xbytes = reinterpret_cast<const unsigned char*>(X);
+    const int nunits = MM * (K >> 9);
+    for (int u = wave; u < nunits; u += nwaves)
+        dma16_to_lds(xbytes + mx_copy_src(K, M, u, 0) + 16 * lane, xa + mx_copy_dst(K, u, 0));
+    uint32_t woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) woff[i] = stream_w_lane_off(n0, N, K, lane, i);
+    const uint8_t* wtile = W + (size_t)n0 * (size_t)(K >> 1);
+    auto issue = [&](int s, unsigned char* slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(wtile + (size_t)s * (kStepGroups * 16) + woff[i]),
+                                             (lds_void_t*)(slot + i * 1024), 16, 0, kDmaAux);
+    };
+    issue(0, ring);
+    const int nseg = 16 * nsteps;
+    for (int t0 = 0; t0 < nseg; t0 += 64) {
+        const int t = min(t0 + lane, nseg - 1);
+        dma16_to_lds_stream(St + stream_s_seg_off(n0, N, K, nsteps, 0, t), sarea + t0 * 16);
+    }
+#pragma unroll
+    for (int s = 1; s < DEPTH; ++s) issue(min(s, nsteps - 1), ring + s * kStepCodeBytes);
+    m1_wait_n<4 * DEPTH + kM1MaxScaleCopies>(4 * DEPTH + (nseg + 63) / 64);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");    // every wave's row pieces landed
+
+    // ---- activation rows -> e4m3 hi / lo in place, and block scales -----------------------------
+    const int units_per_row = K >> 4;                           // 32-byte units (16 values)
+    const int nconv = MM * units_per_row;                       // even: a block is units 2b, 2b + 1
+    for (int g0 = 0; g0 < nconv; g0 += nwaves * 64) {
+        const int gr = g0 + (int)threadIdx.x;
+        const bool live = gr < nconv;
+        const int g = live ? gr : nconv - 2 + (gr & 1);         // past the end: read, never write
+        const int m = g / units_per_row, p = g - m * units_per_row;
+        unsigned char* up = xa + m * rowb + 32 * p;
+        const u32x4_t xw0 = *reinterpret_cast<const u32x4_t*>(up);
+        const u32x4_t xw1 = *reinterpret_cast<const u32x4_t*>(up + 16);
+        float v[16];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            v[2 * c] = __uint_as_float(xw0[c] << 16);
+            v[2 * c + 1] = __uint_as_float(xw0[c] & 0xFFFF0000u);
+            v[8 + 2 * c] = __uint_as_float(xw1[c] << 16);
+            v[8 + 2 * c + 1] = __uint_as_float(xw1[c] & 0xFFFF0000u);
+        }
+        float amax = 0.f;                          // fmaxf drops NaN: NaN values stay out of the max
+#pragma unroll
+        for (int c = 0; c < 16; ++c) amax = fmaxf(amax, fabsf(v[c]));
+        amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, true)));
+        const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xFFu;
+        int be = 261 - (int)eb;                    // biased exponent of 2^e = 2^(7 - floor(log2 amax))
+        be = be < 1 ? 1 : (be > 253 ? 253 : be);
+        const float scale = __uint_as_float((uint32_t)be << 23);
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            float x[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[c] = v[4 * h + c] * scale;
+            uint32_t a = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+            a = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], (int)a, true);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, true);
+            uint32_t b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0] - h01[0], x[1] - h01[1], 0, false);
+            b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2] - h23[0], x[3] - h23[1], (int)b, true);
+            hw[h] = a;
+            lw[h] = b;
+        }
+        if (live) {
+            *reinterpret_cast<u32x4_t*>(up) = (u32x4_t){hw[0], hw[1], hw[2], hw[3]};
+            *reinterpret_cast<u32x4_t*>(up + 16) = (u32x4_t){lw[0], lw[1], lw[2], lw[3]};
+            if ((p & 1) == 0) xe[m * xerow + m1_xe_pos(p >> 1)] = (unsigned char)(eb == 255u ? 255 : 254 - be);
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (!has_tile) {
+        wait_vmcnt<0>();                           // its copies land before the wave leaves
+        return;
+    }
+
+    // ---- stream ------------------------------------------------------------------------------
+    int rdoff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rdoff[u] = stream_w_read_off(r, q, u);
+    const int mrow = (r >> 1) & (MM - 1);
+    const unsigned char* xcol = xa + mrow * rowb + 16 * (r & 1) + 32 * q;
+    const unsigned char* xecol = xe + mrow * xerow + 4 * q;
+    f32x4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < nsteps; ++s) {
+        unsigned char* sl = ring + (s % DEPTH) * kStepCodeBytes;
+        m1_wait<DEPTH - 1>(min(nsteps - 1 - s, DEPTH - 1));
+        const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(sarea + (r * nsteps + s) * 16);
+        u32x4_t wv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wv[u] = *reinterpret_cast<const u32x4_t*>(sl + rdoff[u]);
+        m1_v8i b[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const u32x4_t k0 = *reinterpret_cast<const u32x4_t*>(xcol + 1024 * s + 256 * u);
+            const u32x4_t k1 = *reinterpret_cast<const u32x4_t*>(xcol + 1024 * s + 256 * u + 128);
+            b[u] = (m1_v8i){(int)k0[0], (int)k0[1], (int)k0[2], (int)k0[3], (int)k1[0], (int)k1[1], (int)k1[2], (int)k1[3]};
+        }
+        const uint32_t sb = *reinterpret_cast<const uint32_t*>(xecol + 16 * s);
+        __builtin_amdgcn_s_waitcnt(0xC07F);                 // lgkmcnt(0): the slot is free again
+        if (s + DEPTH < nsteps) issue(s + DEPTH, sl);
+        c0 = m1_mfma<0>(wv[0], b[0], sv[0] >> (8 * q), sb, c0);
+        c1 = m1_mfma<1>(wv[1], b[1], sv[1] >> (8 * q), sb, c1);
+        c0 = m1_mfma<2>(wv[2], b[2], sv[2] >> (8 * q), sb, c0);
+        c1 = m1_mfma<3>(wv[3], b[3], sv[3] >> (8 * q), sb, c1);
+    }
+    f32x4_t acc = c0 + c1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)                                 // column 2m (hi) + column 2m + 1 (lo)
+        acc[i] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc[i]), 0xB1, 0xF, 0xF, true));
+    store_tile<OutT, EPI>(acc, Out, tile, N, M, (r & 1) ? kRowsPerWG : (r >> 1), q);
+}
+
 // Waves per tile: enough tiles x waves to cover the GPU, at most 16 per workgroup and at most one
 // per step.
 inline int stream_waves(int N, int K, int target_waves, int rt)
@@ -1345,6 +1528,75 @@ void launch_m1(const M1Plan& p, const void* W, const void* St, const void* Xb, v
 #undef FP8KV_M1
 }
 
+// M = 2 .. 8 planner (tunables: fp8kv_h4mv_mx_tune), the M = 1 planner's rule with the MM-row
+// activation block in LDS: mode 0 = used when the tiles alone fill the GPU (>= kM1MinTiles) and
+// every workgroup runs in one round with two workgroups per CU; 1 = whenever the shape allows it
+// (one workgroup per CU too); 2 = never.  Measured in one process against the bf16 kernels
+// (events / graph replay): cfg1 M = 2 11.0 / 11.9 against 12.0 / 13.0 us (streaming), M = 3
+// 11.9 / 12.8 against 12.5 / 13.3, M = 4 12.0 / 12.6 against 12.6 / 13.3 (K-slice), gate/up M = 4
+// 13.4 / 14.4 against 14.7 / 15.5.  With eight rows the block (66 KB at K = 4096) leaves room for
+// one workgroup per CU, which converts 32768 values before its first MFMA: cfg1 M = 8 14.4 against
+// 13.0 us and gate/up M = 8 15.6 against 15.3 us on the K-slice kernel, so M = 5 .. 8 stay there.
+thread_local int g_mx_mode = 0;
+thread_local int g_mx_depth = 0;
+thread_local int g_mx_wgs = 0;
+
+struct MxPlan {
+    int mm, tw, grid, depth;
+    size_t lds;
+};
+
+inline int mx_rows(int M) { return M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+
+inline bool mx_plan(int N, int K, int M, MxPlan& p)
+{
+    if (g_mx_mode == 2 || M < 2 || M > 8 || (K & 511) != 0 || (K >> 9) > kM1MaxSteps) return false;
+    const int T = (N + kRowsPerWG - 1) / kRowsPerWG;
+    if (g_mx_mode == 0 && T < kM1MinTiles) return false;
+    const int nsteps = K >> 9;
+    p.mm = mx_rows(M);
+    auto plan_for = [&](int wgs) {
+        const int G = std::min(T, wgs);
+        p.tw = std::min((T + G - 1) / G, kM1MaxWaves);
+        p.grid = (T + p.tw - 1) / p.tw;
+        p.lds = (size_t)mx_x_bytes(p.mm, K) + (size_t)p.tw * m1_wave_bytes(p.depth, nsteps);
+    };
+    for (p.depth = g_mx_depth == 3 ? 3 : 2; p.depth >= 2; --p.depth) {
+        if (g_mx_wgs > 0) {
+            plan_for(g_mx_wgs);
+            if (p.lds <= kLdsPerCU) return true;
+            continue;
+        }
+        plan_for(kM1Workgroups);
+        if (2 * p.lds <= kLdsPerCU && (g_mx_mode == 1 || p.grid <= kM1Workgroups)) return true;
+        if (g_mx_mode == 0) continue;
+        plan_for(kM1Workgroups / 2);
+        if (p.lds <= kLdsPerCU) return true;
+    }
+    return false;
+}
+
+template <typename OutT, int EPI = 0>
+void launch_mx(const MxPlan& p, const void* W, const void* St, const void* Xb, void* Out, int N, int K,
+               int M, hipStream_t s)
+{
+    const dim3 grid((unsigned)p.grid), block(64 * p.tw);
+#define FP8KV_MX(MM, D) \
+    launch_kernel(h4mv_mx_kernel<MM, D, OutT, EPI>, grid, block, (uint32_t)p.lds, s, \
+                  static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
+                  static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M)
+    if (p.depth == 3) {
+        if (p.mm == 2) FP8KV_MX(2, 3);
+        else if (p.mm == 4) FP8KV_MX(4, 3);
+        else FP8KV_MX(8, 3);
+    } else {
+        if (p.mm == 2) FP8KV_MX(2, 2);
+        else if (p.mm == 4) FP8KV_MX(4, 2);
+        else FP8KV_MX(8, 2);
+    }
+#undef FP8KV_MX
+}
+
 template <typename OutT>
 int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N, int K, int M,
                 void* stream)
@@ -1356,10 +1608,13 @@ int launch_h4mv(const void* W, const void* St, const void* Xb, void* Out, int N,
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     begin_launch();
     M1Plan mp;
+    MxPlan xp;
     KsPlan kp;
     StreamPlan p;
     if (aligned(St, 4) && m1_plan(N, K, M, mp)) {
         launch_m1<OutT>(mp, W, St, Xb, Out, N, K, s);
+    } else if (aligned(St, 4) && mx_plan(N, K, M, xp)) {
+        launch_mx<OutT>(xp, W, St, Xb, Out, N, K, M, s);
     } else if (aligned(St, 4) && kslice_plan(N, K, M, kp, true)) {
         launch_kslice<OutT>(kp, W, St, Xb, Out, N, K, M, s);
     } else if (aligned(St, 4) && stream_plan(N, K, M, p)) {
@@ -1389,6 +1644,13 @@ extern "C" int h4mv_silu_mul(const void* W, const void* St, const void* Xb, void
         begin_launch();
         if (mode == 0) launch_m1<__bf16, 1>(mp, W, St, Xb, Out, N, K, s);
         else launch_m1<__bf16, 2>(mp, W, St, Xb, Out, N, K, s);
+        return finish_launch();
+    }
+    MxPlan xp;
+    if (mx_plan(N, K, M, xp)) {
+        begin_launch();
+        if (mode == 0) launch_mx<__bf16, 1>(xp, W, St, Xb, Out, N, K, M, s);
+        else launch_mx<__bf16, 2>(xp, W, St, Xb, Out, N, K, M, s);
         return finish_launch();
     }
     KsPlan kp;
@@ -1642,6 +1904,106 @@ int audit_m1(int N, int K, const M1Plan& p)
     return 0;
 }
 
+// Audit of the M = 2 .. 8 kernel (same return convention): tile coverage, every activation /
+// code / scale byte read, every LDS byte written or read, the two units of a block in
+// neighbouring lanes of one pass, and every converted unit owned by one thread.
+int audit_mx(int N, int K, int M, const MxPlan& p)
+{
+    const int T = (N + kRowsPerWG - 1) / kRowsPerWG, G = p.grid, tw = p.tw, depth = p.depth, mm = p.mm;
+    if ((K & 511) || M < 2 || M > mm || mm > 8 || tw < 1 || tw > kM1MaxWaves || G < 1 || (long)G * tw < T ||
+        depth < 2 || depth > 3)
+        return 2;
+    const int nsteps = K >> 9, nthreads = 64 * tw, rowb = mx_row_bytes(K), xerow = mx_xe_row_bytes(K);
+    const size_t xb = (size_t)mx_x_bytes(mm, K), wb = (size_t)m1_wave_bytes(depth, nsteps);
+    if (xb + (size_t)tw * wb != p.lds || p.lds > kLdsPerCU) return 3;
+    if ((rowb & 255) != kMxRowPad || (xerow & 3)) return 3;
+    const size_t wbytes = (size_t)N * (size_t)(K >> 1), sbytes = (size_t)N * (size_t)(K >> 5);
+    const size_t xbytes = (size_t)M * (size_t)K * 2;
+    // the rows' copies: every LDS byte of the mm rows' first 2K bytes written once, sources in X
+    std::vector<unsigned char> lseen((size_t)mm * rowb, 0);
+    const int nunits = mm * (K >> 9);
+    for (int w = 0; w < tw; ++w)
+        for (int u = w; u < nunits; u += tw)
+            for (int lane = 0; lane < 64; ++lane) {
+                if (mx_copy_src(K, M, u, lane) + 16 > xbytes) return 4;
+                const int d = mx_copy_dst(K, u, lane);
+                if (d + 16 > mm * rowb) return 4;
+                for (int b = 0; b < 16; ++b) {
+                    if (lseen[(size_t)d + b]) return 4;
+                    lseen[(size_t)d + b] = 1;
+                }
+            }
+    for (int m = 0; m < mm; ++m)
+        for (int b = 0; b < 2 * K; ++b)
+            if (!lseen[(size_t)m * rowb + b]) return 4;
+    // conversion: units of a block in lanes 2i, 2i + 1 of one pass, each unit converted once,
+    // reads and writes inside the rows, scale bytes inside the scale rows
+    const int upr = K >> 4, nconv = mm * upr;
+    if (nconv & 1) return 5;
+    std::vector<unsigned char> useen((size_t)nconv, 0);
+    for (int g0 = 0; g0 < nconv; g0 += nthreads)
+        for (int t = 0; t < nthreads; ++t) {
+            const int gr = g0 + t;
+            const bool live = gr < nconv;
+            const int g = live ? gr : nconv - 2 + (gr & 1);
+            const int gp = (t & 1) ? g - 1 : g + 1;            // the DPP partner's unit
+            const int grp = g0 + (t ^ 1), gpp = grp < nconv ? grp : nconv - 2 + (grp & 1);
+            if (gp != gpp || (g >> 1) != (gp >> 1)) return 5;
+            const int m = g / upr, pp = g % upr;
+            if (m >= mm || (size_t)m * rowb + 32 * (size_t)pp + 32 > (size_t)m * rowb + 2 * (size_t)K) return 5;
+            if ((pp >> 1) >= (K >> 5) || m * xerow + m1_xe_pos(pp >> 1) + 1 > mm * xerow) return 5;
+            if (live) {
+                if (useen[(size_t)g]) return 5;
+                useen[(size_t)g] = 1;
+            }
+        }
+    for (int g = 0; g < nconv; ++g)
+        if (!useen[(size_t)g]) return 5;
+    std::vector<unsigned char> seen((size_t)T, 0);
+    for (int b = 0; b < G; ++b)
+        for (int w = 0; w < tw; ++w) {
+            const int tw_tile = b + w * G;
+            const bool has = tw_tile < T;
+            if (has) {
+                if (seen[(size_t)tw_tile]) return 6;
+                seen[(size_t)tw_tile] = 1;
+            }
+            const int n0 = (has ? tw_tile : b) * kRowsPerWG;
+            const size_t ring = xb + (size_t)w * wb, sarea = ring + (size_t)depth * kStepCodeBytes;
+            if (ring + wb > p.lds) return 7;
+            for (int lane = 0; lane < 64; ++lane) {
+                for (int t0 = 0; t0 < 16 * nsteps; t0 += 64) {        // scale slice copies
+                    const int t = std::min(t0 + lane, 16 * nsteps - 1);
+                    if (stream_s_seg_off(n0, N, K, nsteps, 0, t) + 16 > sbytes) return 8;
+                    if (sarea + 16 * (size_t)(t0 + lane) + 16 > ring + wb) return 8;
+                }
+                for (int s = 0; s < nsteps; ++s)                       // code copies
+                    for (int i = 0; i < 4; ++i) {
+                        const size_t g = (size_t)n0 * (K >> 1) + (size_t)s * 256 + stream_w_lane_off(n0, N, K, lane, i);
+                        if (g + 16 > wbytes) return 9;
+                        if ((size_t)(s % depth) * kStepCodeBytes + i * 1024 + 16 * lane + 16 > (size_t)depth * kStepCodeBytes) return 9;
+                    }
+                const int r = lane & 15, q = lane >> 4, mrow = (r >> 1) & (mm - 1);
+                for (int s = 0; s < nsteps; ++s) {                     // fragment reads
+                    if ((size_t)((r * nsteps + s) * 16 + 16) > (size_t)m1_scale_bytes(nsteps)) return 10;
+                    for (int u = 0; u < 4; ++u) {
+                        if (stream_w_read_off(r, q, u) + 16 > kStepCodeBytes) return 11;
+                        // unit 32 s + 8 u + q (k 512 s + 128 u + 16 q ..) and + 4 (k + 64 ..)
+                        const int unit = 32 * s + 8 * u + q;
+                        if (unit + 4 >= upr) return 12;
+                        const size_t off = (size_t)mrow * rowb + 32 * (size_t)(unit + 4) + 16 * (r & 1);
+                        if (off + 16 > (size_t)mrow * rowb + 2 * (size_t)K) return 12;
+                    }
+                    if ((size_t)mrow * xerow + 16 * (size_t)s + 4 * q + 4 > (size_t)mrow * xerow + (((K >> 5) + 15) & ~15))
+                        return 13;
+                }
+            }
+        }
+    for (int t = 0; t < T; ++t)
+        if (!seen[(size_t)t]) return 6;
+    return 0;
+}
+
 }}  // namespace fp8kv::h4mv_detail
 
 extern "C" int fp8kv_h4mv_audit(int N, int K, int M)
@@ -1650,6 +2012,8 @@ extern "C" int fp8kv_h4mv_audit(int N, int K, int M)
     if (N < 1 || K < 32 || M < 1 || M > 16 || (K & 31)) return 2;
     M1Plan mp;
     if (m1_plan(N, K, M, mp)) return audit_m1(N, K, mp);
+    MxPlan xp;
+    if (mx_plan(N, K, M, xp)) return audit_mx(N, K, M, xp);
     KsPlan kp;
     if (kslice_plan(N, K, M, kp, true)) return audit_kslice(N, K, M, kp);
     StreamPlan p;
@@ -1670,6 +2034,44 @@ extern "C" void fp8kv_h4mv_m1_tune(int mode, int depth, int workgroups)
     fp8kv::h4mv_detail::g_m1_mode = (mode == 1 || mode == 2) ? mode : 0;
     fp8kv::h4mv_detail::g_m1_depth = depth;
     fp8kv::h4mv_detail::g_m1_wgs = workgroups > 0 ? workgroups : 0;
+}
+
+extern "C" int fp8kv_h4mv_plan(int N, int K, int M, int* out)
+{
+    using namespace fp8kv::h4mv_detail;
+    if (!out) return FP8KV_ERR_ARG;
+    if (N < 1 || K < 32 || M < 1) return FP8KV_ERR_ARG;
+    if (M > 16 || (K & 31) != 0) return FP8KV_ERR_SHAPE;
+    for (int i = 0; i < 6; ++i) out[i] = 0;
+    M1Plan mp;
+    MxPlan xp;
+    KsPlan kp;
+    StreamPlan sp;
+    if (m1_plan(N, K, M, mp)) {
+        const int v[6] = {3, mp.grid, mp.tw, mp.depth, (int)mp.lds, 1};
+        for (int i = 0; i < 6; ++i) out[i] = v[i];
+    } else if (mx_plan(N, K, M, xp)) {
+        const int v[6] = {4, xp.grid, xp.tw, xp.depth, (int)xp.lds, xp.mm};
+        for (int i = 0; i < 6; ++i) out[i] = v[i];
+    } else if (kslice_plan(N, K, M, kp, true)) {
+        const int v[6] = {kp.batched ? 5 : 2, kp.grid, kp.nw, kp.depth, (int)kp.lds, kp.nt_max};
+        for (int i = 0; i < 6; ++i) out[i] = v[i];
+    } else if (stream_plan(N, K, M, sp)) {
+        const int v[6] = {1, (N + kRowsPerWG * sp.rt - 1) / (kRowsPerWG * sp.rt), sp.nw, sp.depth, (int)sp.lds, sp.rt};
+        for (int i = 0; i < 6; ++i) out[i] = v[i];
+    } else {
+        out[0] = 0;
+        out[1] = (N + kRowsPerWG - 1) / kRowsPerWG;
+        out[2] = 4;
+    }
+    return FP8KV_OK;
+}
+
+extern "C" void fp8kv_h4mv_mx_tune(int mode, int depth, int workgroups)
+{
+    fp8kv::h4mv_detail::g_mx_mode = (mode == 1 || mode == 2) ? mode : 0;
+    fp8kv::h4mv_detail::g_mx_depth = depth;
+    fp8kv::h4mv_detail::g_mx_wgs = workgroups > 0 ? workgroups : 0;
 }
 
 extern "C" void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode)

@@ -108,7 +108,8 @@ def test_fused_silu_epilogue_kslice(mode, depth):
     lib = _lib.load()
     try:
         lib.fp8kv_h4mv_kslice_tune(1, depth, 0, 0)
-        for N, K, M in ((512, 1024, 3), (8224, 2048, 8), (28672, 4096, 5)):
+        lib.fp8kv_h4mv_mx_tune(2, 0, 0)
+        for N, K, M in ((512, 1024, 3), (8224, 2048, 8), (28672, 4096, 5), (28672, 4096, 3)):
             c = workloads.w4_case(N, K, M, seed=N + M + depth)
             W, St, X = c["W"].to(DEV), c["St"].to(DEV), c["X"].to(DEV)
             wi, si = ops.interleave_gate_up(W, St)
@@ -118,6 +119,29 @@ def test_fused_silu_epilogue_kslice(mode, depth):
             assert torch.equal(fused, two), (N, K, M)
     finally:
         lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+        lib.fp8kv_h4mv_mx_tune(0, 0, 0)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("depth", [2, 3])
+def test_fused_silu_epilogue_mx(mode, depth):
+    """The fused epilogue on the M = 2 .. 8 hi / lo kernel forced through its tuning hook equals
+    the two-step path on the same kernel (one tile, several tiles per workgroup, cfg1's shape at
+    two, four and eight activation rows)."""
+    from fp8kv_amd import _lib
+    lib = _lib.load()
+    try:
+        lib.fp8kv_h4mv_mx_tune(1, depth, 0)
+        for N, K, M in ((16, 512, 2), (8224, 2048, 3), (28672, 4096, 4), (28672, 4096, 8), (37888, 3584, 7)):
+            c = workloads.w4_case(N, K, M, seed=N + M + depth)
+            W, St, X = c["W"].to(DEV), c["St"].to(DEV), c["X"].to(DEV)
+            wi, si = ops.interleave_gate_up(W, St)
+            fused = ops.h4mv_silu_mul(X, wi, si, mode=mode)
+            two = ops.silu_mul(ops.h4mv(X, W, St), mode=mode)
+            torch.cuda.synchronize()
+            assert torch.equal(fused, two), (N, K, M)
+    finally:
+        lib.fp8kv_h4mv_mx_tune(0, 0, 0)
 
 
 @pytest.mark.parametrize("mode", [0, 1])

@@ -253,11 +253,13 @@ def test_kslice_variants(depth, N, K, order):
     try:
         lib.fp8kv_h4mv_kslice_tune(1, depth, order, 0)
         lib.fp8kv_h4mv_m1_tune(2, 0, 0)                 # M = 1 on the K-slice kernel too
+        lib.fp8kv_h4mv_mx_tune(2, 0, 0)                 # and M = 3, 8
         for M in (1, 3, 8):
             _check(workloads.w4_case(N=N, K=K, M=M, seed=N + K + M + depth))
     finally:
         lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
         lib.fp8kv_h4mv_m1_tune(0, 0, 0)
+        lib.fp8kv_h4mv_mx_tune(0, 0, 0)
 
 
 @pytest.mark.parametrize("N,K,oracle", [(70000, 4096, True), (128167, 3584, False)])
@@ -297,16 +299,18 @@ def test_kslice_batched_variants(N, K, depth, order):
 
 
 def test_kslice_and_streaming_kernels_agree():
-    """Both LDS kernels on the same cfg1 inputs (K-slice by default, streaming forced): within
-    the fp32 rounding of their different accumulation orders."""
+    """Both bf16 LDS kernels on the same cfg1 inputs (K-slice with the hi / lo kernel off,
+    streaming forced): within the fp32 rounding of their different accumulation orders."""
     case = workloads.w4_case(N=28672, K=4096, M=8, seed=7)
     lib = _lib.load()
-    a = _run(case, out_dtype=torch.float32)
     try:
+        lib.fp8kv_h4mv_mx_tune(2, 0, 0)
+        a = _run(case, out_dtype=torch.float32)
         lib.fp8kv_h4mv_kslice_tune(2, 0, 0, 0)
         b = _run(case, out_dtype=torch.float32)
     finally:
         lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+        lib.fp8kv_h4mv_mx_tune(0, 0, 0)
     assert np.abs(a - b).max() <= 1e-5 * np.abs(a).max()
 
 
@@ -453,5 +457,127 @@ def test_m1_and_streaming_kernels_agree():
     case = workloads.w4_case(N=28672, K=4096, M=1, seed=7)
     a = _run(case, out_dtype=torch.float32)
     with _M1(2):
+        b = _run(case, out_dtype=torch.float32)
+    assert np.abs(a - b).max() <= 1e-5 * np.abs(a).max()
+
+
+# --- M = 2 .. 8 kernel: one e4m3 hi / lo column pair per activation row --------------------------
+
+class _MX:
+    """The M = 2 .. 8 hi / lo kernel forced (mode 1) or switched off (mode 2) for a block."""
+
+    def __init__(self, mode=1, depth=0, wgs=0):
+        self.args = (mode, depth, wgs)
+
+    def __enter__(self):
+        _lib.load().fp8kv_h4mv_mx_tune(*self.args)
+
+    def __exit__(self, *exc):
+        _lib.load().fp8kv_h4mv_mx_tune(0, 0, 0)
+
+
+def _plan(N, K, M):
+    out = (ctypes.c_int * 6)()
+    assert _lib.load().fp8kv_h4mv_plan(N, K, M, out) == 0
+    return list(out)
+
+
+@pytest.mark.parametrize("wgs", [0, 5, 150])
+@pytest.mark.parametrize("depth", [2, 3])
+@pytest.mark.parametrize("N,K", [(1, 512), (272, 1024), (250, 1536), (4096, 3584), (28672, 4096),
+                                 (37888, 3584), (100, 8192)])
+def test_mx_kernel_variants(depth, wgs, N, K):
+    """Both ring depths and three workgroup targets (the default; 5: several tiles per workgroup
+    and waves without a tile; 150) at M = 2, 3, 5 and 8 (two, four and eight activation rows in
+    LDS, rows past M repeating row M - 1): one K step, ragged N, cfg1, gate/up, 16 steps with all
+    eight rows; bf16 and fp32 outputs against the oracle.  With a workgroup target whose
+    workgroups would not fit the LDS the planner falls back to the K-slice kernel."""
+    with _MX(1, depth, wgs):
+        for M in (2, 3, 5, 8):
+            plan = _plan(N, K, M)
+            assert plan[0] == 4 or wgs > 0, (N, K, M, plan)
+            _check(workloads.w4_case(N=N, K=K, M=M, seed=N + K + M + depth + wgs))
+
+
+@pytest.mark.parametrize("N,K,M", [(28672, 4096, 8), (28672, 4096, 3), (37888, 3584, 8), (37888, 3584, 2),
+                                   (250, 1536, 7)])
+def test_mx_rows_equal_the_m1_kernel(N, K, M):
+    """Every output column of the MFMA is computed on its own, so row m of the M-row kernel is
+    bit for bit the M = 1 kernel's result for row m alone."""
+    case = workloads.w4_case(N=N, K=K, M=M, seed=N + M + 3)
+    with _MX(1), _M1(1):
+        assert _plan(N, K, M)[0] == 4 and _plan(N, K, 1)[0] == 3
+        y = _run(case, out_dtype=torch.float32)
+        for m in range(M):
+            one = _run(dict(case, X=case["X"][m:m + 1]), out_dtype=torch.float32)
+            assert np.array_equal(y[m:m + 1], one), m
+
+
+def test_mx_one_hot_probes_across_groups_and_rows():
+    """Distinct code per weight row, scale per (row, group) and value per activation row: every k
+    of a 512-k step at M = 8, exact."""
+    N, K, M = 37, 512, 8
+    rng = np.random.default_rng(6)
+    St = rng.integers(120, 135, (N, K // 32), dtype=np.uint8)
+    from oracle.formats import pack_e2m1
+    with _MX():
+        for k in [0, 1, 15, 16, 31, 32, 63, 64, 127, 128, 200, 255, 256, 480, 511]:
+            codes = np.zeros((N, K), dtype=np.uint8)
+            codes[:, k] = rng.integers(1, 16, N).astype(np.uint8)
+            X = np.zeros((M, K), dtype=np.float32)
+            X[:, k] = [-1.5, 2.0, 0.25, -3.0, 1.0, 0.75, -0.5, 6.0]
+            case = {"W": torch.from_numpy(pack_e2m1(codes)), "St": torch.from_numpy(St),
+                    "X": torch.from_numpy(X).to(torch.bfloat16)}
+            assert np.array_equal(_run(case), _oracle(case)), f"k={k}"
+
+
+def test_mx_every_bf16_value_splits_exactly():
+    """As for the M = 1 kernel, with a different block pattern in each of 8 rows: hi + lo is exact
+    for every value >= 2^-9 of its block's largest, so one-hot weight rows give the oracle's
+    products bit for bit."""
+    K, N, M = 512, 64, 8
+    rng = np.random.default_rng(9)
+    x = np.zeros((M, K), dtype=np.float32)
+    for m in range(M):
+        for b in range(K // 32):
+            top = 2.0 ** rng.integers(-100, 100)
+            mant = 1 + rng.integers(0, 128, 32) / 128.0
+            sgn = rng.choice([-1.0, 1.0], 32)
+            x[m, 32 * b: 32 * b + 32] = sgn * mant * top * 2.0 ** -np.minimum(np.arange(32), 9)
+            x[m, 32 * b] = top * 1.9921875
+    codes = np.zeros((N, K), dtype=np.uint8)
+    codes[np.arange(N), rng.choice(K, N, replace=False)] = 2      # e2m1 1.0
+    from oracle.formats import pack_e2m1
+    case = {"W": torch.from_numpy(pack_e2m1(codes)), "St": torch.full((N, K // 32), 127, dtype=torch.uint8),
+            "X": torch.from_numpy(x).to(torch.bfloat16)}
+    with _MX():
+        y = _run(case, out_dtype=torch.float32)
+    assert np.array_equal(y, _oracle(case).astype(np.float32))
+
+
+def test_mx_zero_nan_and_inf_rows():
+    """A zero row gives zeros; a NaN or an infinity in a row makes that row's outputs NaN (the
+    M = 1 kernel's rule: e4m3 has no infinity) and leaves the other rows as they are."""
+    case = workloads.w4_case(N=64, K=1024, M=4, seed=5)
+    with _MX():
+        ref = _run(case, out_dtype=torch.float32)
+        x = case["X"].clone()
+        x[1] = 0
+        x[2, 700] = float("nan")
+        x[3, 5] = float("-inf")
+        y = _run(dict(case, X=x), out_dtype=torch.float32)
+    assert np.array_equal(y[0], ref[0])
+    assert np.array_equal(y[1], np.zeros_like(y[1]))
+    assert np.isnan(y[2]).all() and np.isnan(y[3]).all()
+
+
+def test_mx_and_kslice_kernels_agree():
+    """cfg1 M = 4 on the hi / lo kernel (the default) and on the K-slice kernel: within the fp32
+    rounding of their accumulation orders."""
+    case = workloads.w4_case(N=28672, K=4096, M=4, seed=8)
+    assert _plan(28672, 4096, 4)[0] == 4
+    a = _run(case, out_dtype=torch.float32)
+    with _MX(2):
+        assert _plan(28672, 4096, 4)[0] == 2
         b = _run(case, out_dtype=torch.float32)
     assert np.abs(a - b).max() <= 1e-5 * np.abs(a).max()

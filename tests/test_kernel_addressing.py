@@ -62,6 +62,7 @@ def test_h4mv_kslice_in_bounds(lib, depth, order, wgs):
     rng = random.Random(depth)
     try:
         lib.fp8kv_h4mv_kslice_tune(1, depth, order, wgs)
+        lib.fp8kv_h4mv_mx_tune(2, 0, 0)                 # M = 3, 8 on the K-slice kernel too
         shapes = [(N, K) for N, K in CFG4_SHAPES if K <= 4096]
         shapes += [(16, 512), (4112, 1024), (8208, 2048), (65536, 512), (66048, 512)]
         # partial last tiles (N % 16 != 0): the lm_head vocabulary, the smallest N, random N
@@ -77,6 +78,7 @@ def test_h4mv_kslice_in_bounds(lib, depth, order, wgs):
                 assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
     finally:
         lib.fp8kv_h4mv_kslice_tune(0, 0, 0, 0)
+        lib.fp8kv_h4mv_mx_tune(0, 0, 0)
 
 
 @pytest.mark.parametrize("wgs", [0, 7, 300])
@@ -97,3 +99,53 @@ def test_h4mv_m1_in_bounds(lib, depth, wgs):
             assert lib.fp8kv_h4mv_audit(N, K, 1) == 0, (N, K)
     finally:
         lib.fp8kv_h4mv_m1_tune(0, 0, 0)
+
+
+@pytest.mark.parametrize("wgs", [0, 7, 300])
+@pytest.mark.parametrize("depth", [2, 3])
+def test_h4mv_mx_in_bounds(lib, depth, wgs):
+    """The M = 2 .. 8 hi / lo kernel forced on every shape it accepts, at two, four and eight
+    activation rows (M = 2, 3, 4, 5, 8): model shapes, ragged N, K from one step up, 1..16 tiles
+    per workgroup and waves without a tile.  Every tile covered once, every LDS byte of the rows
+    copied once, each 32-byte unit converted by one thread with its block partner in the
+    neighbouring lane, every fragment and scale read inside its row."""
+    import ctypes
+    rng = random.Random(depth + wgs + 1)
+    out = (ctypes.c_int * 6)()
+    try:
+        lib.fp8kv_h4mv_mx_tune(1, depth, wgs)
+        shapes = list(CFG4_SHAPES) + [(1, 512), (15, 512), (17, 1024), (4097, 2048), (250, 1536),
+                                      (100, 8192), (16 * 4096 + 3, 4096)]
+        for _ in range(30):
+            shapes.append((rng.randrange(1, 20000), 512 * rng.randrange(1, 17)))
+        used = 0
+        for N, K in shapes:
+            for M in (2, 3, 4, 5, 8):
+                assert lib.fp8kv_h4mv_audit(N, K, M) == 0, (N, K, M)
+                assert lib.fp8kv_h4mv_plan(N, K, M, out) == 0
+                used += out[0] == 4
+        assert used > len(shapes)
+    finally:
+        lib.fp8kv_h4mv_mx_tune(0, 0, 0)
+
+
+def test_h4mv_plan_picks_the_measured_kernels(lib):
+    """The default plans: M = 1 kernel for cfg1 and gate/up at M = 1, the hi / lo kernel at
+    M = 2 .. 4 (two workgroups per CU), the K-slice kernel at M = 5 .. 8 and for the lm_head
+    vocabulary, the streaming kernel for the short-N configs[4] linears."""
+    import ctypes
+    out = (ctypes.c_int * 6)()
+
+    def kernel(N, K, M):
+        assert lib.fp8kv_h4mv_plan(N, K, M, out) == 0
+        return out[0]
+    for N, K in ((28672, 4096), (37888, 3584)):
+        assert kernel(N, K, 1) == 3
+        assert [kernel(N, K, M) for M in (2, 3, 4)] == [4, 4, 4]
+        assert [kernel(N, K, M) for M in (5, 8)] == [2, 2]
+    assert kernel(28672, 4096, 4) == 4 and out[5] == 4 and out[1] == 448
+    assert [kernel(128167, 3584, M) for M in (3, 8)] == [5, 5]
+    for N, K in ((4096, 3584), (3584, 3072), (3584, 18944)):
+        assert [kernel(N, K, M) for M in (1, 4, 8)] == [1, 1, 1]
+    assert kernel(64, 96, 2) == 0
+    assert lib.fp8kv_h4mv_plan(64, 96, 17, out) != 0
