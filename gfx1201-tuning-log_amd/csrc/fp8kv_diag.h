@@ -46,11 +46,15 @@ void fp8kv_h4mv_m1_tune(int mode, int depth, int workgroups);
 
 /* Tuning hook for the matvec's M = 2 .. 8 kernel (the M = 1 kernel's e4m3 hi + lo activations, one
  * column pair per row): mode 0 = used at 2 <= M <= 8 when N / 16 >= 1024 tiles and every workgroup
- * runs in one round at two workgroups per CU (the default; in practice M <= 4), 1 = whenever the
- * shape allows it (2 <= M <= 8, K % 512 == 0),
+ * runs in one round (the default), 1 = whenever the shape allows it (2 <= M <= 8, K % 512 == 0),
  * 2 = never; depth = LDS ring slots per wave (3; any other value: 2, the default); workgroups =
  * workgroup count the planner aims for (0: default).  Affects later launches and audits. */
 void fp8kv_h4mv_mx_tune(int mode, int depth, int workgroups);
+
+/* Tuning hook for the M = 2 .. 8 kernel's activation conversion: 2^steps_log2 K steps per chunk
+ * (0..6; the first chunk is converted before the stream, each later one while the previous one
+ * streams); any other value restores the default.  Affects later launches and audits. */
+void fp8kv_h4mv_mx_chunk_tune(int steps_log2);
 
 /* Planner query of the matvec launch (host only, no GPU call): the kernel h4mv_launch would run
  * for (N, K, M) under the current tuning hooks.  out[6] = {kernel (0 register path, 1 streaming,

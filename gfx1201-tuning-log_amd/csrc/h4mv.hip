@@ -1045,10 +1045,13 @@ h4mv_m1_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
 // that row alone, bit for bit.
 //   * LDS: MM rows of 2K + kMxRowPad bytes, then MM rows of block scale bytes, then the waves'
 //     rings and scale slices as in the M = 1 kernel.  Row m is copied in as bf16 (whole 1 KB
-//     copies; rows m >= M repeat row M - 1) and converted in place: thread t takes 16 values
-//     (32 bytes), the two threads of a 32-k block share their maximum with one DPP step, and the
-//     thread writes its 16 hi bytes over the first half of its own 32 bytes and its 16 lo bytes
-//     over the second.  A thread only ever rewrites bytes it alone read.
+//     copies; rows m >= M repeat row M - 1) and converted in place (mx_convert_chunk): a thread
+//     takes 16 values (32 bytes), the two threads of a 32-k block share their maximum with one
+//     DPP step, and the thread writes its 16 hi bytes over the first half of its own 32 bytes and
+//     its 16 lo bytes over the second.  A thread only ever rewrites bytes it alone read.
+//   * The conversion runs cs steps of K at a time: chunk 0 before the stream starts, chunk
+//     j + 1 while the waves stream chunk j (its VALU work fills the stream's waits), one
+//     LDS-only barrier per chunk.  Waves without a tile convert and meet every barrier too.
 //   * B fragment of lane (n, j) for MFMA u of step s: row m = (n / 2) mod MM, half n % 2, k =
 //     512 s + 128 u + 16 j .. + 15 and + 64: 16-byte units 32 s + 8 u + j and + 4 of the row, at
 //     byte 32 unit (+ 16 for lo).  Row stride = 32 mod 256, so lanes 0..15 of a read meet 16
@@ -1075,10 +1078,78 @@ __host__ __device__ inline int mx_copy_dst(int K, int u, int lane)
     return m * mx_row_bytes(K) + c * 1024 + 16 * lane;
 }
 
+typedef short mx_pk16_t __attribute__((ext_vector_type(2)));
+typedef __bf16 mx_bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Converts chunk j of an MM-row activation block in place: steps cs j .. cs j + cs - 1 of every
+// row (cs a power of two; units past the row's end in the last chunk are skipped), U = 32 cs
+// 32-byte units of 16 values per row.  Thread i of the workgroup takes unit U j + i % U of row
+// i / U; the two units of a 32-k block sit in lanes 2i' and 2i' + 1, which share their maximum
+// with one DPP step.  A thread rewrites only the 32 bytes it alone read (a lane with no unit reads
+// unit 0 of row 0 and writes nothing); a wave whose lanes are all past the chunk skips the pass.
+template <int MM>
+__device__ __forceinline__ void mx_convert_chunk(unsigned char* xa, unsigned char* xe, int rowb, int xerow,
+                                                 int upr, int cs_log2, int j, int wave, int lane, int nthreads)
+{
+    const int ush = 5 + cs_log2;
+    const int U = 1 << ush;
+    const int total = MM * U;
+    for (int i0 = 0; i0 < total; i0 += nthreads) {
+        if (i0 + 64 * wave >= total) break;                    // wave-uniform
+        const int i = i0 + 64 * wave + lane;
+        const int m = i >> ush, p = U * j + (i & (U - 1));
+        const bool live = i < total && p < upr;                // a block's two units live or die together
+        unsigned char* up = xa + (live ? m * rowb + 32 * p : 0);
+        const u32x4_t xw0 = *reinterpret_cast<const u32x4_t*>(up);
+        const u32x4_t xw1 = *reinterpret_cast<const u32x4_t*>(up + 16);
+        float v[16];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            v[2 * c] = __uint_as_float(xw0[c] << 16);
+            v[2 * c + 1] = __uint_as_float(xw0[c] & 0xFFFF0000u);
+            v[8 + 2 * c] = __uint_as_float(xw1[c] << 16);
+            v[8 + 2 * c + 1] = __uint_as_float(xw1[c] & 0xFFFF0000u);
+        }
+        float amax = 0.f;                          // fmaxf drops NaN: NaN values stay out of the max
+#pragma unroll
+        for (int c = 0; c < 16; ++c) amax = fmaxf(amax, fabsf(v[c]));
+        amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, true)));
+        const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xFFu;
+        int be = 261 - (int)eb;                    // biased exponent of 2^e = 2^(7 - floor(log2 amax))
+        be = be < 1 ? 1 : (be > 253 ? 253 : be);
+        const float scale = __uint_as_float((uint32_t)be << 23);
+        const float rscale = __uint_as_float((uint32_t)(254 - be) << 23);     // 2^-e, exact
+        const uint32_t xd[8] = {xw0[0], xw0[1], xw0[2], xw0[3], xw1[0], xw1[1], xw1[2], xw1[3]};
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            // hi straight from the packed bf16 pairs: the scaled conversion rounds x / 2^-e = x 2^e
+            // once, as the unscaled conversion of the (exact) product does
+            mx_pk16_t t = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16((mx_pk16_t){0, 0},
+                                                                    __builtin_bit_cast(mx_bf16x2_t, xd[2 * h]), rscale, false);
+            t = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(t, __builtin_bit_cast(mx_bf16x2_t, xd[2 * h + 1]), rscale, true);
+            const uint32_t a = __builtin_bit_cast(uint32_t, t);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, true);
+            uint32_t b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fmaf(v[4 * h], scale, -h01[0]),
+                                                                   fmaf(v[4 * h + 1], scale, -h01[1]), 0, false);
+            b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fmaf(v[4 * h + 2], scale, -h23[0]),
+                                                          fmaf(v[4 * h + 3], scale, -h23[1]), (int)b, true);
+            hw[h] = a;
+            lw[h] = b;
+        }
+        if (live) {
+            *reinterpret_cast<u32x4_t*>(up) = (u32x4_t){hw[0], hw[1], hw[2], hw[3]};
+            *reinterpret_cast<u32x4_t*>(up + 16) = (u32x4_t){lw[0], lw[1], lw[2], lw[3]};
+            if ((p & 1) == 0) xe[m * xerow + m1_xe_pos(p >> 1)] = (unsigned char)(eb == 255u ? 255 : 254 - be);
+        }
+    }
+}
+
 template <int MM, int DEPTH, typename OutT, int EPI>
 __global__ void __launch_bounds__(64 * kM1MaxWaves)
 h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
-               const __bf16* __restrict__ X, OutT* __restrict__ Out, int N, int K, int M)
+               const __bf16* __restrict__ X, OutT* __restrict__ Out, int N, int K, int M, int cs_log2)
 {
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
@@ -1127,59 +1198,15 @@ h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
     m1_wait_n<4 * DEPTH + kM1MaxScaleCopies>(4 * DEPTH + (nseg + 63) / 64);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");    // every wave's row pieces landed
 
-    // ---- activation rows -> e4m3 hi / lo in place, and block scales -----------------------------
-    const int units_per_row = K >> 4;                           // 32-byte units (16 values)
-    const int nconv = MM * units_per_row;                       // even: a block is units 2b, 2b + 1
-    for (int g0 = 0; g0 < nconv; g0 += nwaves * 64) {
-        const int gr = g0 + (int)threadIdx.x;
-        const bool live = gr < nconv;
-        const int g = live ? gr : nconv - 2 + (gr & 1);         // past the end: read, never write
-        const int m = g / units_per_row, p = g - m * units_per_row;
-        unsigned char* up = xa + m * rowb + 32 * p;
-        const u32x4_t xw0 = *reinterpret_cast<const u32x4_t*>(up);
-        const u32x4_t xw1 = *reinterpret_cast<const u32x4_t*>(up + 16);
-        float v[16];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            v[2 * c] = __uint_as_float(xw0[c] << 16);
-            v[2 * c + 1] = __uint_as_float(xw0[c] & 0xFFFF0000u);
-            v[8 + 2 * c] = __uint_as_float(xw1[c] << 16);
-            v[8 + 2 * c + 1] = __uint_as_float(xw1[c] & 0xFFFF0000u);
-        }
-        float amax = 0.f;                          // fmaxf drops NaN: NaN values stay out of the max
-#pragma unroll
-        for (int c = 0; c < 16; ++c) amax = fmaxf(amax, fabsf(v[c]));
-        amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, true)));
-        const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xFFu;
-        int be = 261 - (int)eb;                    // biased exponent of 2^e = 2^(7 - floor(log2 amax))
-        be = be < 1 ? 1 : (be > 253 ? 253 : be);
-        const float scale = __uint_as_float((uint32_t)be << 23);
-        uint32_t hw[4], lw[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            float x[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) x[c] = v[4 * h + c] * scale;
-            uint32_t a = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
-            a = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], (int)a, true);
-            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, false);
-            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, true);
-            uint32_t b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[0] - h01[0], x[1] - h01[1], 0, false);
-            b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2] - h23[0], x[3] - h23[1], (int)b, true);
-            hw[h] = a;
-            lw[h] = b;
-        }
-        if (live) {
-            *reinterpret_cast<u32x4_t*>(up) = (u32x4_t){hw[0], hw[1], hw[2], hw[3]};
-            *reinterpret_cast<u32x4_t*>(up + 16) = (u32x4_t){lw[0], lw[1], lw[2], lw[3]};
-            if ((p & 1) == 0) xe[m * xerow + m1_xe_pos(p >> 1)] = (unsigned char)(eb == 255u ? 255 : 254 - be);
-        }
-    }
+    // ---- activation rows -> e4m3 hi / lo in place, cs = 2^cs_log2 steps at a time --------------
+    // Chunk 0 is converted before the stream starts; chunk j + 1 is converted while the waves
+    // stream chunk j, and an LDS-only barrier publishes it (the ring's copies stay in flight).
+    const int cs = 1 << cs_log2;
+    const int nchunks = (nsteps + cs - 1) >> cs_log2;
+    const int nthreads = 64 * nwaves;
+    const int upr = K >> 4;
+    mx_convert_chunk<MM>(xa, xe, rowb, xerow, upr, cs_log2, 0, wave, lane, nthreads);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (!has_tile) {
-        wait_vmcnt<0>();                           // its copies land before the wave leaves
-        return;
-    }
 
     // ---- stream ------------------------------------------------------------------------------
     int rdoff[4];
@@ -1189,27 +1216,38 @@ h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
     const unsigned char* xcol = xa + mrow * rowb + 16 * (r & 1) + 32 * q;
     const unsigned char* xecol = xe + mrow * xerow + 4 * q;
     f32x4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < nsteps; ++s) {
-        unsigned char* sl = ring + (s % DEPTH) * kStepCodeBytes;
-        m1_wait<DEPTH - 1>(min(nsteps - 1 - s, DEPTH - 1));
-        const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(sarea + (r * nsteps + s) * 16);
-        u32x4_t wv[4];
+    for (int j = 0; j < nchunks; ++j) {
+        if (j + 1 < nchunks) mx_convert_chunk<MM>(xa, xe, rowb, xerow, upr, cs_log2, j + 1, wave, lane, nthreads);
+        if (has_tile) {
+            const int s_end = min(nsteps, cs * (j + 1));
+            for (int s = cs * j; s < s_end; ++s) {
+                unsigned char* sl = ring + (s % DEPTH) * kStepCodeBytes;
+                m1_wait<DEPTH - 1>(min(nsteps - 1 - s, DEPTH - 1));
+                const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(sarea + (r * nsteps + s) * 16);
+                u32x4_t wv[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) wv[u] = *reinterpret_cast<const u32x4_t*>(sl + rdoff[u]);
-        m1_v8i b[4];
+                for (int u = 0; u < 4; ++u) wv[u] = *reinterpret_cast<const u32x4_t*>(sl + rdoff[u]);
+                m1_v8i b[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const u32x4_t k0 = *reinterpret_cast<const u32x4_t*>(xcol + 1024 * s + 256 * u);
-            const u32x4_t k1 = *reinterpret_cast<const u32x4_t*>(xcol + 1024 * s + 256 * u + 128);
-            b[u] = (m1_v8i){(int)k0[0], (int)k0[1], (int)k0[2], (int)k0[3], (int)k1[0], (int)k1[1], (int)k1[2], (int)k1[3]};
+                for (int u = 0; u < 4; ++u) {
+                    const u32x4_t k0 = *reinterpret_cast<const u32x4_t*>(xcol + 1024 * s + 256 * u);
+                    const u32x4_t k1 = *reinterpret_cast<const u32x4_t*>(xcol + 1024 * s + 256 * u + 128);
+                    b[u] = (m1_v8i){(int)k0[0], (int)k0[1], (int)k0[2], (int)k0[3], (int)k1[0], (int)k1[1], (int)k1[2], (int)k1[3]};
+                }
+                const uint32_t sb = *reinterpret_cast<const uint32_t*>(xecol + 16 * s);
+                __builtin_amdgcn_s_waitcnt(0xC07F);                 // lgkmcnt(0): the slot is free again
+                if (s + DEPTH < nsteps) issue(s + DEPTH, sl);
+                c0 = m1_mfma<0>(wv[0], b[0], sv[0] >> (8 * q), sb, c0);
+                c1 = m1_mfma<1>(wv[1], b[1], sv[1] >> (8 * q), sb, c1);
+                c0 = m1_mfma<2>(wv[2], b[2], sv[2] >> (8 * q), sb, c0);
+                c1 = m1_mfma<3>(wv[3], b[3], sv[3] >> (8 * q), sb, c1);
+            }
         }
-        const uint32_t sb = *reinterpret_cast<const uint32_t*>(xecol + 16 * s);
-        __builtin_amdgcn_s_waitcnt(0xC07F);                 // lgkmcnt(0): the slot is free again
-        if (s + DEPTH < nsteps) issue(s + DEPTH, sl);
-        c0 = m1_mfma<0>(wv[0], b[0], sv[0] >> (8 * q), sb, c0);
-        c1 = m1_mfma<1>(wv[1], b[1], sv[1] >> (8 * q), sb, c1);
-        c0 = m1_mfma<2>(wv[2], b[2], sv[2] >> (8 * q), sb, c0);
-        c1 = m1_mfma<3>(wv[3], b[3], sv[3] >> (8 * q), sb, c1);
+        if (j + 1 < nchunks) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    if (!has_tile) {
+        wait_vmcnt<0>();                           // its copies land before the wave leaves
+        return;
     }
     f32x4_t acc = c0 + c1;
 #pragma unroll
@@ -1530,21 +1568,38 @@ void launch_m1(const M1Plan& p, const void* W, const void* St, const void* Xb, v
 
 // M = 2 .. 8 planner (tunables: fp8kv_h4mv_mx_tune), the M = 1 planner's rule with the MM-row
 // activation block in LDS: mode 0 = used when the tiles alone fill the GPU (>= kM1MinTiles) and
-// every workgroup runs in one round with two workgroups per CU; 1 = whenever the shape allows it
-// (one workgroup per CU too); 2 = never.  Measured in one process against the bf16 kernels
-// (events / graph replay): cfg1 M = 2 11.0 / 11.9 against 12.0 / 13.0 us (streaming), M = 3
-// 11.9 / 12.8 against 12.5 / 13.3, M = 4 12.0 / 12.6 against 12.6 / 13.3 (K-slice), gate/up M = 4
-// 13.4 / 14.4 against 14.7 / 15.5.  With eight rows the block (66 KB at K = 4096) leaves room for
-// one workgroup per CU, which converts 32768 values before its first MFMA: cfg1 M = 8 14.4 against
-// 13.0 us and gate/up M = 8 15.6 against 15.3 us on the K-slice kernel, so M = 5 .. 8 stay there.
+// every workgroup runs in one round (two workgroups per CU where the LDS allows, else one);
+// 1 = whenever the shape allows it; 2 = never.  Measured in one process, two rounds, against the
+// bf16 kernels (events / graph replay): cfg1 M = 2 11.0-11.2 / 12.0-12.2 against 12.0 / 13.2-13.5
+// us (streaming), M = 4 11.8-11.9 / 12.6-13.2 against 12.6-12.7 / 13.5-13.8 (K-slice), M = 8
+// 12.9 / 13.7-14.0 against 13.1-13.2 / 14.0, gate/up M = 4 13.0-13.1 / 14.0-14.5 against 14.7 /
+// 15.3-15.7, M = 8 14.5 / 15.4 against 15.4 / 15.8-16.1; M = 5 12.8 against 12.6 us.  With eight
+// rows the block (66 KB at K = 4096) leaves room for one workgroup per CU, whose conversion of
+// 32768 values is spread over the stream in two-step chunks (mx_chunk_log2).
 thread_local int g_mx_mode = 0;
 thread_local int g_mx_depth = 0;
 thread_local int g_mx_wgs = 0;
 
+thread_local int g_mx_chunk = 0;             // log2 steps per conversion chunk + 1 (0: default)
+
 struct MxPlan {
-    int mm, tw, grid, depth;
+    int mm, tw, grid, depth, cs_log2;
     size_t lds;
 };
+
+// Steps per conversion chunk (log2).  Measured over 1, 2, 4 and all steps (one process, two
+// rounds): workgroups of up to four waves convert the whole block first (cfg1 M = 4: 11.9 us
+// against 12.3 in 2-step chunks, M = 2: 11.2 against 11.4), larger ones two steps at a time
+// while streaming (gate/up M = 4, 5 waves: 12.9 against 13.7; M = 8, 10 waves: 14.5 against
+// 15.9; cfg1 M = 8, 7 waves: 13.0 against 14.2).
+inline int mx_chunk_log2(int nsteps, int tw)
+{
+    if (g_mx_chunk > 0) return g_mx_chunk - 1;
+    if (tw > 4) return 1;
+    int l = 0;
+    while ((1 << l) < nsteps) ++l;
+    return l;
+}
 
 inline int mx_rows(int M) { return M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
@@ -1560,6 +1615,7 @@ inline bool mx_plan(int N, int K, int M, MxPlan& p)
         p.tw = std::min((T + G - 1) / G, kM1MaxWaves);
         p.grid = (T + p.tw - 1) / p.tw;
         p.lds = (size_t)mx_x_bytes(p.mm, K) + (size_t)p.tw * m1_wave_bytes(p.depth, nsteps);
+        p.cs_log2 = mx_chunk_log2(nsteps, p.tw);
     };
     for (p.depth = g_mx_depth == 3 ? 3 : 2; p.depth >= 2; --p.depth) {
         if (g_mx_wgs > 0) {
@@ -1569,9 +1625,8 @@ inline bool mx_plan(int N, int K, int M, MxPlan& p)
         }
         plan_for(kM1Workgroups);
         if (2 * p.lds <= kLdsPerCU && (g_mx_mode == 1 || p.grid <= kM1Workgroups)) return true;
-        if (g_mx_mode == 0) continue;
         plan_for(kM1Workgroups / 2);
-        if (p.lds <= kLdsPerCU) return true;
+        if (p.lds <= kLdsPerCU && (g_mx_mode == 1 || p.grid <= kM1Workgroups / 2)) return true;
     }
     return false;
 }
@@ -1584,7 +1639,7 @@ void launch_mx(const MxPlan& p, const void* W, const void* St, const void* Xb, v
 #define FP8KV_MX(MM, D) \
     launch_kernel(h4mv_mx_kernel<MM, D, OutT, EPI>, grid, block, (uint32_t)p.lds, s, \
                   static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(St), \
-                  static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M)
+                  static_cast<const __bf16*>(Xb), static_cast<OutT*>(Out), N, K, M, p.cs_log2)
     if (p.depth == 3) {
         if (p.mm == 2) FP8KV_MX(2, 3);
         else if (p.mm == 4) FP8KV_MX(4, 3);
@@ -1936,29 +1991,31 @@ int audit_mx(int N, int K, int M, const MxPlan& p)
     for (int m = 0; m < mm; ++m)
         for (int b = 0; b < 2 * K; ++b)
             if (!lseen[(size_t)m * rowb + b]) return 4;
-    // conversion: units of a block in lanes 2i, 2i + 1 of one pass, each unit converted once,
-    // reads and writes inside the rows, scale bytes inside the scale rows
-    const int upr = K >> 4, nconv = mm * upr;
-    if (nconv & 1) return 5;
-    std::vector<unsigned char> useen((size_t)nconv, 0);
-    for (int g0 = 0; g0 < nconv; g0 += nthreads)
-        for (int t = 0; t < nthreads; ++t) {
-            const int gr = g0 + t;
-            const bool live = gr < nconv;
-            const int g = live ? gr : nconv - 2 + (gr & 1);
-            const int gp = (t & 1) ? g - 1 : g + 1;            // the DPP partner's unit
-            const int grp = g0 + (t ^ 1), gpp = grp < nconv ? grp : nconv - 2 + (grp & 1);
-            if (gp != gpp || (g >> 1) != (gp >> 1)) return 5;
-            const int m = g / upr, pp = g % upr;
-            if (m >= mm || (size_t)m * rowb + 32 * (size_t)pp + 32 > (size_t)m * rowb + 2 * (size_t)K) return 5;
-            if ((pp >> 1) >= (K >> 5) || m * xerow + m1_xe_pos(pp >> 1) + 1 > mm * xerow) return 5;
-            if (live) {
-                if (useen[(size_t)g]) return 5;
-                useen[(size_t)g] = 1;
+    // conversion, chunk by chunk as mx_convert_chunk deals it: the units of a block in lanes
+    // 2i, 2i + 1 of one pass, each unit converted once, reads and writes inside the rows, scale
+    // bytes inside the scale rows
+    const int upr = K >> 4;
+    std::vector<unsigned char> useen((size_t)mm * upr, 0);
+    if (p.cs_log2 < 0 || p.cs_log2 > 6) return 5;
+    const int U = 32 << p.cs_log2, total = mm * U, nchunks = (nsteps + (1 << p.cs_log2) - 1) >> p.cs_log2;
+    for (int j = 0; j < nchunks; ++j) {
+        for (int i0 = 0; i0 < total; i0 += nthreads)
+            for (int t = 0; t < nthreads; ++t) {
+                if (i0 + 64 * (t / 64) >= total) continue;          // the wave skips the pass
+                const int i = i0 + t, ip = i ^ 1;
+                const int m = i / U, pp = U * j + i % U, mp = ip / U, ppp = U * j + ip % U;
+                const bool live = i < total && pp < upr, livep = ip < total && ppp < upr;
+                if (live != livep) return 5;                        // a block's halves live or die together
+                if (!live) continue;                                // reads unit 0 of row 0, writes nothing
+                if (m != mp || (pp >> 1) != (ppp >> 1)) return 5;   // the DPP partner holds the block's other half
+                if (m >= mm || 32 * pp + 32 > 2 * K) return 5;
+                if ((pp >> 1) >= (K >> 5) || m * xerow + m1_xe_pos(pp >> 1) + 1 > mm * xerow) return 5;
+                if (useen[(size_t)m * upr + pp]) return 5;
+                useen[(size_t)m * upr + pp] = 1;
             }
-        }
-    for (int g = 0; g < nconv; ++g)
-        if (!useen[(size_t)g]) return 5;
+    }
+    for (size_t g = 0; g < useen.size(); ++g)
+        if (!useen[g]) return 5;
     std::vector<unsigned char> seen((size_t)T, 0);
     for (int b = 0; b < G; ++b)
         for (int w = 0; w < tw; ++w) {
@@ -2072,6 +2129,11 @@ extern "C" void fp8kv_h4mv_mx_tune(int mode, int depth, int workgroups)
     fp8kv::h4mv_detail::g_mx_mode = (mode == 1 || mode == 2) ? mode : 0;
     fp8kv::h4mv_detail::g_mx_depth = depth;
     fp8kv::h4mv_detail::g_mx_wgs = workgroups > 0 ? workgroups : 0;
+}
+
+extern "C" void fp8kv_h4mv_mx_chunk_tune(int steps_log2)
+{
+    fp8kv::h4mv_detail::g_mx_chunk = (steps_log2 >= 0 && steps_log2 <= 6) ? steps_log2 + 1 : 0;
 }
 
 extern "C" void fp8kv_h4mv_tune(int target_waves, int depth, int row_tiles, int x_mode)

@@ -77,6 +77,7 @@ SIGNATURES: dict[str, tuple] = {
     "fp8kv_h4mv_kslice_tune": (None, [_c_i] * 4),
     "fp8kv_h4mv_m1_tune": (None, [_c_i] * 3),
     "fp8kv_h4mv_mx_tune": (None, [_c_i] * 3),
+    "fp8kv_h4mv_mx_chunk_tune": (None, [_c_i]),
     "fp8kv_h4mv_plan": (_c_i, [_c_i, _c_i, _c_i, _c_vp]),
     "fp8kv_decode_tune": (None, [_c_i] * 2),
     "fp8kv_prefill_tune": (None, [_c_i]),

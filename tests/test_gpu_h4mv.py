@@ -581,3 +581,24 @@ def test_mx_and_kslice_kernels_agree():
         assert _plan(28672, 4096, 4)[0] == 2
         b = _run(case, out_dtype=torch.float32)
     assert np.abs(a - b).max() <= 1e-5 * np.abs(a).max()
+
+
+@pytest.mark.parametrize("N,K,M", [(28672, 4096, 8), (37888, 3584, 4), (250, 1536, 3), (4097, 2048, 2),
+                                   (17, 3584, 5)])
+def test_mx_conversion_chunks_agree(N, K, M):
+    """The activation block converted 1, 2, 4, 8 or 64 steps at a time (the later chunks while the
+    earlier ones stream) gives the same result bit for bit, and it meets the oracle bar."""
+    case = workloads.w4_case(N=N, K=K, M=M, seed=N + K + M + 17)
+    lib = _lib.load()
+    outs = []
+    try:
+        with _MX(1):
+            for c in (0, 1, 2, 3, 6):
+                lib.fp8kv_h4mv_mx_chunk_tune(c)
+                assert _plan(N, K, M)[0] == 4
+                outs.append(_run(case, out_dtype=torch.float32))
+            _check(case)
+    finally:
+        lib.fp8kv_h4mv_mx_chunk_tune(-1)
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])

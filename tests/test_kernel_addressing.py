@@ -131,8 +131,9 @@ def test_h4mv_mx_in_bounds(lib, depth, wgs):
 
 def test_h4mv_plan_picks_the_measured_kernels(lib):
     """The default plans: M = 1 kernel for cfg1 and gate/up at M = 1, the hi / lo kernel at
-    M = 2 .. 4 (two workgroups per CU), the K-slice kernel at M = 5 .. 8 and for the lm_head
-    vocabulary, the streaming kernel for the short-N configs[4] linears."""
+    M = 2 .. 8 (one round of workgroups; conversion chunks of two steps for workgroups of more
+    than four waves), the K-slice kernel for the lm_head vocabulary, the streaming kernel for the
+    short-N configs[4] linears."""
     import ctypes
     out = (ctypes.c_int * 6)()
 
@@ -141,9 +142,9 @@ def test_h4mv_plan_picks_the_measured_kernels(lib):
         return out[0]
     for N, K in ((28672, 4096), (37888, 3584)):
         assert kernel(N, K, 1) == 3
-        assert [kernel(N, K, M) for M in (2, 3, 4)] == [4, 4, 4]
-        assert [kernel(N, K, M) for M in (5, 8)] == [2, 2]
-    assert kernel(28672, 4096, 4) == 4 and out[5] == 4 and out[1] == 448
+        assert [kernel(N, K, M) for M in (2, 3, 4, 5, 8)] == [4, 4, 4, 4, 4]
+    assert kernel(28672, 4096, 4) == 4 and out[5] == 4 and out[1] == 448 and out[2] == 4
+    assert kernel(28672, 4096, 8) == 4 and out[5] == 8 and out[1] == 256 and out[2] == 7
     assert [kernel(128167, 3584, M) for M in (3, 8)] == [5, 5]
     for N, K in ((4096, 3584), (3584, 3072), (3584, 18944)):
         assert [kernel(N, K, M) for M in (1, 4, 8)] == [1, 1, 1]
