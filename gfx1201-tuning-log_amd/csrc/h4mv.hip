@@ -27,6 +27,7 @@
 #include "fp8kv_status.h"
 #include "fp8kv_diag.h"
 #include <algorithm>
+#include <utility>
 #include <vector>
 
 namespace fp8kv {
@@ -1065,18 +1066,51 @@ __host__ __device__ inline int mx_row_bytes(int K) { return 2 * K + kMxRowPad; }
 // Block scale bytes of one row (m1_xe_pos order), padded so that rows start in different banks.
 __host__ __device__ inline int mx_xe_row_bytes(int K) { return (((K >> 5) + 15) & ~15) + 16; }
 __host__ __device__ inline int mx_x_bytes(int mm, int K) { return mm * (mx_row_bytes(K) + mx_xe_row_bytes(K)); }
-// Activation copy unit u (1 KB: 64 lanes x 16 B) of an MM-row block: row u / (K / 512), piece c.
-__host__ __device__ inline size_t mx_copy_src(int K, int M, int u, int lane)
+// Activation copy unit u (1 KB: 64 lanes x 16 B, one row's 512 values of one step) of an MM-row
+// block, step-major: step u / MM, row u % MM; unit u is copied by wave u % nwaves.
+__host__ __device__ inline size_t mx_copy_src(int K, int M, int mm, int u, int lane)
 {
-    const int per_row = K >> 9, m = u / per_row, c = u % per_row;
-    const int mm = m < M ? m : M - 1;
-    return (size_t)mm * (size_t)K * 2 + (size_t)c * 1024 + 16u * (uint32_t)lane;
+    const int st = u / mm, m = u % mm;
+    const int mc = m < M ? m : M - 1;
+    return (size_t)mc * (size_t)K * 2 + (size_t)st * 1024 + 16u * (uint32_t)lane;
 }
-__host__ __device__ inline int mx_copy_dst(int K, int u, int lane)
+__host__ __device__ inline int mx_copy_dst(int K, int mm, int u, int lane)
 {
-    const int per_row = K >> 9, m = u / per_row, c = u % per_row;
-    return m * mx_row_bytes(K) + c * 1024 + 16 * lane;
+    const int st = u / mm, m = u % mm;
+    return m * mx_row_bytes(K) + st * 1024 + 16 * lane;
 }
+// Units of [a, b) that wave w copies when units are dealt round-robin over nw waves.
+__host__ __device__ inline int mx_units_of(int a, int b, int w, int nw)
+{
+    return b <= a ? 0 : (b - w + nw - 1) / nw - (a - w + nw - 1) / nw;
+}
+// Copies a wave has issued after its last activation copy of chunk j (steps cs j .. cs j + cs - 1)
+// when it waits for that chunk: its copies of later chunks, the ring's first slots and the scale
+// slice (all issued up front, after the activation copies), and, for a wave with a tile, the ring
+// refills issued while streaming the steps before step cs (j - 1).  Waiting until at most that many
+// are outstanding means the wave's copies of chunk j have landed (vmcnt retires in issue order).
+__host__ __device__ inline int mx_after_chunk(int mm, int nsteps, int cs, int depth, int nscale, int j,
+                                              int w, int nw, bool streams)
+{
+    const int end = mm * (cs * (j + 1) < nsteps ? cs * (j + 1) : nsteps);
+    const int streamed = streams && cs * (j - 1) > 0 ? cs * (j - 1) : 0;      // steps consumed so far
+    const int refills = streamed < nsteps - depth ? streamed : (nsteps - depth > 0 ? nsteps - depth : 0);
+    return mx_units_of(end, mm * nsteps, w, nw) + 4 * depth + nscale + 4 * refills;
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform 0 <= n (counts above 63 wait for 63: stricter).
+template <int LO, int HI>
+__device__ __forceinline__ void mx_wait_range(int n)
+{
+    if constexpr (HI - LO <= 1) {
+        wait_vmcnt<LO>();
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        if (n >= MID) mx_wait_range<MID, HI>(n);
+        else mx_wait_range<LO, MID>(n);
+    }
+}
+__device__ __forceinline__ void mx_wait(int n) { mx_wait_range<0, 64>(n < 63 ? n : 63); }
 
 typedef short mx_pk16_t __attribute__((ext_vector_type(2)));
 typedef __bf16 mx_bf16x2_t __attribute__((ext_vector_type(2)));
@@ -1172,11 +1206,14 @@ h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
     const int tile = has_tile ? tile_w : blockIdx.x;
     const int n0 = tile * kRowsPerWG;
 
-    // ---- the activation rows, the scale slice, then the ring: all copies straight to LDS -------
+    // ---- the activation rows (step-major), the scale slice, then the ring: all copies straight
+    // to LDS.  Chunk j of the rows is waited for just before its conversion.
+    const int cs = 1 << cs_log2;
+    const int nchunks = (nsteps + cs - 1) >> cs_log2;
     const unsigned char* xbytes = reinterpret_cast<const unsigned char*>(X);
-    const int nunits = MM * (K >> 9);
+    const int nunits = MM * nsteps;
     for (int u = wave; u < nunits; u += nwaves)
-        dma16_to_lds(xbytes + mx_copy_src(K, M, u, 0) + 16 * lane, xa + mx_copy_dst(K, u, 0));
+        dma16_to_lds(xbytes + mx_copy_src(K, M, MM, u, 0) + 16 * lane, xa + mx_copy_dst(K, MM, u, 0));
     uint32_t woff[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) woff[i] = stream_w_lane_off(n0, N, K, lane, i);
@@ -1195,18 +1232,18 @@ h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
     }
 #pragma unroll
     for (int s = 1; s < DEPTH; ++s) issue(min(s, nsteps - 1), ring + s * kStepCodeBytes);
-    m1_wait_n<4 * DEPTH + kM1MaxScaleCopies>(4 * DEPTH + (nseg + 63) / 64);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");    // every wave's row pieces landed
+    const int nscale = (nseg + 63) / 64;
+    mx_wait(mx_after_chunk(MM, nsteps, cs, DEPTH, nscale, 0, wave, nwaves, has_tile));
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");    // every wave's chunk-0 pieces landed
 
     // ---- activation rows -> e4m3 hi / lo in place, cs = 2^cs_log2 steps at a time --------------
-    // Chunk 0 is converted before the stream starts; chunk j + 1 is converted while the waves
-    // stream chunk j, and an LDS-only barrier publishes it (the ring's copies stay in flight).
-    const int cs = 1 << cs_log2;
-    const int nchunks = (nsteps + cs - 1) >> cs_log2;
+    // Chunk 0 is converted while the later chunks' copies are still landing; chunk j + 1 is
+    // converted while the waves stream chunk j, after a barrier that publishes chunk j's
+    // conversion and follows every wave's wait for its own copies of chunk j + 1 (the LDS-only
+    // barrier leaves the ring in flight).
     const int nthreads = 64 * nwaves;
     const int upr = K >> 4;
     mx_convert_chunk<MM>(xa, xe, rowb, xerow, upr, cs_log2, 0, wave, lane, nthreads);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // ---- stream ------------------------------------------------------------------------------
     int rdoff[4];
@@ -1217,6 +1254,8 @@ h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
     const unsigned char* xecol = xe + mrow * xerow + 4 * q;
     f32x4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < nchunks; ++j) {
+        if (j + 1 < nchunks) mx_wait(mx_after_chunk(MM, nsteps, cs, DEPTH, nscale, j + 1, wave, nwaves, has_tile));
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (j + 1 < nchunks) mx_convert_chunk<MM>(xa, xe, rowb, xerow, upr, cs_log2, j + 1, wave, lane, nthreads);
         if (has_tile) {
             const int s_end = min(nsteps, cs * (j + 1));
@@ -1243,7 +1282,6 @@ h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
                 c1 = m1_mfma<3>(wv[3], b[3], sv[3] >> (8 * q), sb, c1);
             }
         }
-        if (j + 1 < nchunks) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
     if (!has_tile) {
         wait_vmcnt<0>();                           // its copies land before the wave leaves
@@ -1976,12 +2014,12 @@ int audit_mx(int N, int K, int M, const MxPlan& p)
     const size_t xbytes = (size_t)M * (size_t)K * 2;
     // the rows' copies: every LDS byte of the mm rows' first 2K bytes written once, sources in X
     std::vector<unsigned char> lseen((size_t)mm * rowb, 0);
-    const int nunits = mm * (K >> 9);
+    const int nunits = mm * nsteps;
     for (int w = 0; w < tw; ++w)
         for (int u = w; u < nunits; u += tw)
             for (int lane = 0; lane < 64; ++lane) {
-                if (mx_copy_src(K, M, u, lane) + 16 > xbytes) return 4;
-                const int d = mx_copy_dst(K, u, lane);
+                if (mx_copy_src(K, M, mm, u, lane) + 16 > xbytes) return 4;
+                const int d = mx_copy_dst(K, mm, u, lane);
                 if (d + 16 > mm * rowb) return 4;
                 for (int b = 0; b < 16; ++b) {
                     if (lseen[(size_t)d + b]) return 4;
@@ -2016,6 +2054,42 @@ int audit_mx(int N, int K, int M, const MxPlan& p)
     }
     for (size_t g = 0; g < useen.size(); ++g)
         if (!useen[g]) return 5;
+    // vmcnt: replay each wave's copies in issue order and check that every wait the kernel makes
+    // (same count formulas) leaves outstanding only copies younger than the ones the next use needs
+    {
+        const int cs = 1 << p.cs_log2, nchunks = (nsteps + cs - 1) / cs, nscale = (16 * nsteps + 63) / 64;
+        for (int w = 0; w < tw; ++w)
+            for (int has = 0; has < 2; ++has) {
+                // op kinds: 0 = activation unit (id = chunk), 1 = ring step (id = step), 2 = scale
+                std::vector<std::pair<int, int>> ops;
+                for (int u = w; u < nunits; u += tw) ops.push_back({0, (u / mm) / cs});
+                for (int i = 0; i < 4; ++i) ops.push_back({1, 0});
+                for (int k = 0; k < nscale; ++k) ops.push_back({2, 0});
+                for (int d = 1; d < depth; ++d)
+                    for (int i = 0; i < 4; ++i) ops.push_back({1, std::min(d, nsteps - 1)});
+                auto landed_ok = [&](int n, auto need) {
+                    for (int i = (int)ops.size() - std::min(n, 63); i < (int)ops.size(); ++i)
+                        if (need(ops[(size_t)i])) return false;
+                    return true;
+                };
+                auto chunk_need = [](int c) { return [c](std::pair<int, int> o) { return o.first == 0 && o.second == c; }; };
+                if (!landed_ok(mx_after_chunk(mm, nsteps, cs, depth, nscale, 0, w, tw, has != 0), chunk_need(0)))
+                    return 14;
+                for (int j = 0; j < nchunks; ++j) {
+                    if (j + 1 < nchunks &&
+                        !landed_ok(mx_after_chunk(mm, nsteps, cs, depth, nscale, j + 1, w, tw, has != 0), chunk_need(j + 1)))
+                        return 14;
+                    if (!has) continue;
+                    for (int st = cs * j; st < std::min(nsteps, cs * (j + 1)); ++st) {
+                        if (!landed_ok(4 * std::min(nsteps - 1 - st, depth - 1), [&](std::pair<int, int> o) {
+                                return (o.first == 1 && o.second == st) || (st == 0 && o.first == 2); }))
+                            return 14;
+                        if (st + depth < nsteps)
+                            for (int i = 0; i < 4; ++i) ops.push_back({1, st + depth});
+                    }
+                }
+            }
+    }
     std::vector<unsigned char> seen((size_t)T, 0);
     for (int b = 0; b < G; ++b)
         for (int w = 0; w < tw; ++w) {
