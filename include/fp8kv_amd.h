@@ -50,11 +50,12 @@ const char* fp8kv_last_hip_error_string(void);
  * Same symbol, same signature, same argument meaning.  Differences: M up to 16 (the reference runs
  * M > 8 silently as M = 8), bf16 rounding is nearest-even (the reference rounds half up), and a
  * rejected call launches nothing and records its status for fp8kv_last_status().
- * Non-finite activations depend on M: NaN in X gives NaN outputs at every M (as the reference).
- * An infinity in X gives +-inf (NaN where its weight is zero) for M >= 2, as the reference does,
- * but NaN in every output of the row at M = 1 on shapes of at least 1024 row tiles with
- * K % 512 == 0 (there the row is split into e4m3 parts, which have no infinity, and its 32-k
- * block takes the NaN scale).
+ * Non-finite activations: NaN in X gives NaN outputs of its row (as the reference).  An infinity
+ * in X gives NaN in every output of its row on the block-scaled kernels, which run 1 <= M <= 8 on
+ * shapes of at least 1024 row tiles with K % 512 == 0 whose workgroups fit one round (cfg1, the
+ * configs[4] gate/up shape); there the row is split into e4m3 parts, which have no infinity, and
+ * its 32-k block takes the NaN scale.  Everywhere else it gives +-inf (NaN where its weight is
+ * zero), as the reference does.  fp8kv_h4mv_plan (fp8kv_diag.h) reports which kernel a shape uses.
  */
 void h4mv_launch(const void* W, const void* St, const void* Xb, void* Out,
                  int N, int K, int M, void* stream);
