@@ -1053,6 +1053,8 @@ h4mv_m1_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
 //   * The conversion runs cs steps of K at a time: chunk 0 before the stream starts, chunk
 //     j + 1 while the waves stream chunk j (its VALU work fills the stream's waits), one
 //     LDS-only barrier per chunk.  Waves without a tile convert and meet every barrier too.
+//   * Only the M rows in use are converted; the columns of rows M .. MM - 1 read the unconverted
+//     copies and are never stored (each MFMA output column depends on its own B column only).
 //   * B fragment of lane (n, j) for MFMA u of step s: row m = (n / 2) mod MM, half n % 2, k =
 //     512 s + 128 u + 16 j .. + 15 and + 64: 16-byte units 32 s + 8 u + j and + 4 of the row, at
 //     byte 32 unit (+ 16 for lo).  Row stride = 32 mod 256, so lanes 0..15 of a read meet 16
@@ -1115,19 +1117,21 @@ __device__ __forceinline__ void mx_wait(int n) { mx_wait_range<0, 64>(n < 63 ? n
 typedef short mx_pk16_t __attribute__((ext_vector_type(2)));
 typedef __bf16 mx_bf16x2_t __attribute__((ext_vector_type(2)));
 
-// Converts chunk j of an MM-row activation block in place: steps cs j .. cs j + cs - 1 of every
-// row (cs a power of two; units past the row's end in the last chunk are skipped), U = 32 cs
+// Converts chunk j of an MM-row activation block in place: steps cs j .. cs j + cs - 1 of its
+// first `rows` rows (the M rows in use: the block's rows past M are never stored, so they stay
+// as copied), cs a power of two (units past the row's end in the last chunk are skipped), U = 32 cs
 // 32-byte units of 16 values per row.  Thread i of the workgroup takes unit U j + i % U of row
 // i / U; the two units of a 32-k block sit in lanes 2i' and 2i' + 1, which share their maximum
 // with one DPP step.  A thread rewrites only the 32 bytes it alone read (a lane with no unit reads
 // unit 0 of row 0 and writes nothing); a wave whose lanes are all past the chunk skips the pass.
 template <int MM>
 __device__ __forceinline__ void mx_convert_chunk(unsigned char* xa, unsigned char* xe, int rowb, int xerow,
-                                                 int upr, int cs_log2, int j, int wave, int lane, int nthreads)
+                                                 int upr, int cs_log2, int j, int rows, int wave, int lane,
+                                                 int nthreads)
 {
     const int ush = 5 + cs_log2;
     const int U = 1 << ush;
-    const int total = MM * U;
+    const int total = rows * U;
     for (int i0 = 0; i0 < total; i0 += nthreads) {
         if (i0 + 64 * wave >= total) break;                    // wave-uniform
         const int i = i0 + 64 * wave + lane;
@@ -1243,7 +1247,7 @@ h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
     // barrier leaves the ring in flight).
     const int nthreads = 64 * nwaves;
     const int upr = K >> 4;
-    mx_convert_chunk<MM>(xa, xe, rowb, xerow, upr, cs_log2, 0, wave, lane, nthreads);
+    mx_convert_chunk<MM>(xa, xe, rowb, xerow, upr, cs_log2, 0, M, wave, lane, nthreads);
 
     // ---- stream ------------------------------------------------------------------------------
     int rdoff[4];
@@ -1256,7 +1260,7 @@ h4mv_mx_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ St,
     for (int j = 0; j < nchunks; ++j) {
         if (j + 1 < nchunks) mx_wait(mx_after_chunk(MM, nsteps, cs, DEPTH, nscale, j + 1, wave, nwaves, has_tile));
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (j + 1 < nchunks) mx_convert_chunk<MM>(xa, xe, rowb, xerow, upr, cs_log2, j + 1, wave, lane, nthreads);
+        if (j + 1 < nchunks) mx_convert_chunk<MM>(xa, xe, rowb, xerow, upr, cs_log2, j + 1, M, wave, lane, nthreads);
         if (has_tile) {
             const int s_end = min(nsteps, cs * (j + 1));
             for (int s = cs * j; s < s_end; ++s) {
@@ -1611,7 +1615,7 @@ void launch_m1(const M1Plan& p, const void* W, const void* St, const void* Xb, v
 // bf16 kernels (events / graph replay): cfg1 M = 2 11.0-11.2 / 12.0-12.2 against 12.0 / 13.2-13.5
 // us (streaming), M = 4 11.8-11.9 / 12.6-13.2 against 12.6-12.7 / 13.5-13.8 (K-slice), M = 8
 // 12.9 / 13.7-14.0 against 13.1-13.2 / 14.0, gate/up M = 4 13.0-13.1 / 14.0-14.5 against 14.7 /
-// 15.3-15.7, M = 8 14.5 / 15.4 against 15.4 / 15.8-16.1; M = 5 12.8 against 12.6 us.  With eight
+// 15.3-15.7, M = 8 14.5 / 15.4 against 15.4 / 15.8-16.1; M = 5 12.1 against 12.6 us.  With eight
 // rows the block (66 KB at K = 4096) leaves room for one workgroup per CU, whose conversion of
 // 32768 values is spread over the stream in two-step chunks (mx_chunk_log2).
 thread_local int g_mx_mode = 0;
@@ -2033,9 +2037,9 @@ int audit_mx(int N, int K, int M, const MxPlan& p)
     // 2i, 2i + 1 of one pass, each unit converted once, reads and writes inside the rows, scale
     // bytes inside the scale rows
     const int upr = K >> 4;
-    std::vector<unsigned char> useen((size_t)mm * upr, 0);
+    std::vector<unsigned char> useen((size_t)M * upr, 0);
     if (p.cs_log2 < 0 || p.cs_log2 > 6) return 5;
-    const int U = 32 << p.cs_log2, total = mm * U, nchunks = (nsteps + (1 << p.cs_log2) - 1) >> p.cs_log2;
+    const int U = 32 << p.cs_log2, total = M * U, nchunks = (nsteps + (1 << p.cs_log2) - 1) >> p.cs_log2;
     for (int j = 0; j < nchunks; ++j) {
         for (int i0 = 0; i0 < total; i0 += nthreads)
             for (int t = 0; t < nthreads; ++t) {
@@ -2046,7 +2050,7 @@ int audit_mx(int N, int K, int M, const MxPlan& p)
                 if (live != livep) return 5;                        // a block's halves live or die together
                 if (!live) continue;                                // reads unit 0 of row 0, writes nothing
                 if (m != mp || (pp >> 1) != (ppp >> 1)) return 5;   // the DPP partner holds the block's other half
-                if (m >= mm || 32 * pp + 32 > 2 * K) return 5;
+                if (m >= M || 32 * pp + 32 > 2 * K) return 5;
                 if ((pp >> 1) >= (K >> 5) || m * xerow + m1_xe_pos(pp >> 1) + 1 > mm * xerow) return 5;
                 if (useen[(size_t)m * upr + pp]) return 5;
                 useen[(size_t)m * upr + pp] = 1;
