@@ -573,9 +573,10 @@ def bench_stream_read(nbytes: int, steps: int, warmup: int):
         events[:] = [None, None]
 
     wall, per = time_launches(launch, n_sets, steps, warmup, arm=arm)
+    gms = time_graph(launch, n_sets, steps, warmup)      # no events armed: plain launches
     del bufs
     torch.cuda.empty_cache()
-    r = _summary(wall, per, nbytes)
+    r = _with_graph(_summary(wall, per, nbytes), gms, nbytes)
     r["rotation_sets"] = n_sets
     return r
 
@@ -875,6 +876,8 @@ def main():
     if ref_w4 is not None and m1 is not None:
         line["roofline"]["read_reference_GBps"] = ref_w4["GBps_kernel"]
         line["roofline"]["frac_of_read_reference"] = round(m1["GBps_kernel"] / ref_w4["GBps_kernel"], 4)
+        line["roofline"]["read_reference_GBps_graph"] = ref_w4["GBps_graph"]
+        line["roofline"]["frac_graph_of_read_reference"] = round(m1["GBps_graph"] / ref_w4["GBps_graph"], 4)
     if "lm_head_topk_vocab128167_M1_k64" in legs:
         lm = legs["lm_head_topk_vocab128167_M1_k64"]
         line["roofline_lm_head_M1"] = {"bound": "hbm", "achieved": lm["GBps_kernel"], "peak": HBM_PEAK_GBS,
@@ -897,6 +900,8 @@ def main():
         if ref_dec is not None:
             line["roofline_decode_b8_4k"]["read_reference_GBps"] = ref_dec["GBps_kernel"]
             line["roofline_decode_b8_4k"]["frac_of_read_reference"] = round(dec["GBps_kernel"] / ref_dec["GBps_kernel"], 4)
+            line["roofline_decode_b8_4k"]["read_reference_GBps_graph"] = ref_dec["GBps_graph"]
+            line["roofline_decode_b8_4k"]["frac_graph_of_read_reference"] = round(dec["GBps_graph"] / ref_dec["GBps_graph"], 4)
     print(json.dumps(line))
 
 

@@ -56,10 +56,16 @@ extern "C" int fp8kv_stream_read(const void* src, size_t bytes, void* sink, void
     if (blocks > kMaxBlocks) return FP8KV_ERR_SHAPE;
     const int per = (int)((n16 + blocks * kThreads - 1) / (blocks * kThreads));
     (void)hipGetLastError();
-    // hipExtLaunchKernel stamps the events (either may be NULL) at the dispatch's own start and end
-    hipExtLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
-                          reinterpret_cast<hipStream_t>(stream), static_cast<hipEvent_t>(start_event),
-                          static_cast<hipEvent_t>(stop_event), 0, static_cast<const u32x4_t*>(src), n16,
-                          per, static_cast<uint32_t*>(sink));
+    if (!start_event && !stop_event) {               // a plain launch (also inside a graph capture)
+        hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
+                           reinterpret_cast<hipStream_t>(stream), static_cast<const u32x4_t*>(src), n16, per,
+                           static_cast<uint32_t*>(sink));
+    } else {
+        // hipExtLaunchKernel stamps the events (either may be NULL) at the dispatch's own start and end
+        hipExtLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
+                              reinterpret_cast<hipStream_t>(stream), static_cast<hipEvent_t>(start_event),
+                              static_cast<hipEvent_t>(stop_event), 0, static_cast<const u32x4_t*>(src), n16,
+                              per, static_cast<uint32_t*>(sink));
+    }
     return hipGetLastError() == hipSuccess ? FP8KV_OK : FP8KV_ERR_LAUNCH;
 }
