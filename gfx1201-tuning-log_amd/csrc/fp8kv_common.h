@@ -104,6 +104,20 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// s_waitcnt vmcnt(n) for a wave-uniform n known only at run time (n in [LO, HI), by bisection;
+// n >= 63 waits for 63).
+template <int LO, int HI>
+__device__ __forceinline__ void wait_vmcnt_range(int n) {
+    if constexpr (HI - LO <= 1) {
+        wait_vmcnt<LO>();
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        if (n >= MID) wait_vmcnt_range<MID, HI>(n);
+        else wait_vmcnt_range<LO, MID>(n);
+    }
+}
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) { wait_vmcnt_range<0, 64>(n < 63 ? n : 63); }
+
 // Non-temporal 16-byte global load: weight and KV streams are read exactly once per launch.
 __device__ __forceinline__ u32x4_t load_nt_16(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));

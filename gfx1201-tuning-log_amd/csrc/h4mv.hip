@@ -1101,18 +1101,7 @@ __host__ __device__ inline int mx_after_chunk(int mm, int nsteps, int cs, int de
 }
 
 // s_waitcnt vmcnt(n) for a wave-uniform 0 <= n (counts above 63 wait for 63: stricter).
-template <int LO, int HI>
-__device__ __forceinline__ void mx_wait_range(int n)
-{
-    if constexpr (HI - LO <= 1) {
-        wait_vmcnt<LO>();
-    } else {
-        constexpr int MID = (LO + HI) / 2;
-        if (n >= MID) mx_wait_range<MID, HI>(n);
-        else mx_wait_range<LO, MID>(n);
-    }
-}
-__device__ __forceinline__ void mx_wait(int n) { mx_wait_range<0, 64>(n < 63 ? n : 63); }
+__device__ __forceinline__ void mx_wait(int n) { wait_vmcnt_dyn(n); }
 
 typedef short mx_pk16_t __attribute__((ext_vector_type(2)));
 typedef __bf16 mx_bf16x2_t __attribute__((ext_vector_type(2)));

@@ -471,6 +471,15 @@ struct BigGeom {
     static_assert(NW_W % NW == 0 && NW_X % NW == 0, "copy kinds must split evenly over the waves");
     static_assert(TN % 4 == 0 && TM % 4 == 0, "tiles come in groups of four (one scale VGPR)");
     static_assert((S - 1) * DPW < 64, "vmcnt range");
+    // Grouped scales (K % 512 == 0): one 16-byte copy per lane brings a row's scale bytes of four
+    // steps into a two-slot scale ring behind the operand ring (weight rows, then in MXFP8 mode the
+    // token rows; 16 bytes per row).
+    static constexpr int OPER = W_BYTES + X_BYTES;
+    static constexpr int sg_rows(bool tok) { return tok ? BN : BN + BM; }
+    static constexpr int dpw_sg(bool tok) { return (sg_rows(tok) / 64 + NW - 1) / NW; }
+    static constexpr int lds_gs(bool tok) { return S * OPER + 2 * 16 * sg_rows(tok); }
+    static_assert(lds_gs(false) <= 160 * 1024, "LDS");
+    static_assert((S - 1) * (NW_W + NW_X) / NW + 2 * dpw_sg(false) < 64, "vmcnt range");
 };
 
 template <int TN, int TM>
@@ -512,12 +521,18 @@ __device__ __forceinline__ void big_compute(const BigFrags<TN, TM>& f, f32x4_t (
     big_mfmas<TN, TM>(f, sa, sb, acc, std::make_integer_sequence<int, TN * TM>{});
 }
 
-// TOK: per-token mode, as in gemm_lds_body.
-template <int WN, int WM, int TN, int TM, int S, bool TOK = false>
+// TOK: per-token mode, as in gemm_lds_body.  GS: grouped scales (BigGeom; K % 512 == 0): the
+// scale bytes of steps 4g .. 4g + 3 are copied with step 4g's operands into slot g % 2 of the scale
+// ring, a quarter of the per-step scale copies, each lane 16 bytes instead of 4.
+template <int WN, int WM, int TN, int TM, int S, bool TOK = false, bool GS = false>
 __global__ void __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_big_kernel(Params P)
 {
     using G = BigGeom<WN, WM, TN, TM, S>;
+    constexpr int STAGE = GS ? G::OPER : G::STAGE;
+    constexpr int DPW = GS ? (G::NW_W + G::NW_X) / G::NW : G::DPW;      // copies per wave and step
+    constexpr int SG_ROWS = G::sg_rows(TOK), DPW_SG = G::dpw_sg(TOK);     // GS: copies per group
+    constexpr int SG_BASE = S * G::OPER;
     extern __shared__ __align__(16) unsigned char smem[];
     int nb, mb;
     if (!tile_of(P, blockIdx.x, nb, mb)) return;
@@ -533,11 +548,11 @@ gemm_big_kernel(Params P)
     const uint8_t* const xtile = P.Xq + (int64_t)M0 * P.K;
     const uint8_t* const swtile = P.St + (int64_t)N0 * ks;
     const uint8_t* const sxtile = TOK ? swtile : P.Sx + (int64_t)M0 * ks;
-    uint32_t loff[G::DPW];
-    int ldsoff[G::DPW];
-    bool from_w[G::DPW];
+    uint32_t loff[DPW];
+    int ldsoff[DPW];
+    bool from_w[DPW];
 #pragma unroll
-    for (int c = 0; c < G::DPW; ++c) {
+    for (int c = 0; c < DPW; ++c) {
         const int d = c * G::NW + wave;
         from_w[c] = false;
         if (c < G::NW_W / G::NW) {
@@ -571,12 +586,33 @@ gemm_big_kernel(Params P)
             }
         }
     }
+    // GS scale copies: copy e of a group covers rows 64 e .. 64 e + 63 of the group's rows (weight
+    // rows, then token rows), lane = row, 16 bytes (four steps) each; padding copies repeat the last.
+    uint32_t sg_loff[GS ? DPW_SG : 1];
+    int sg_lds[GS ? DPW_SG : 1];
+    bool sg_w[GS ? DPW_SG : 1];
+#pragma unroll
+    for (int c = 0; c < (GS ? DPW_SG : 0); ++c) {
+        int e = c * G::NW + wave;
+        if (e >= SG_ROWS / 64) e = SG_ROWS / 64 - 1;
+        sg_w[c] = e < G::BN / 64;
+        if (sg_w[c]) {
+            int n = 64 * e + lane;
+            n = N0 + n < P.N ? n : P.N - 1 - N0;
+            sg_loff[c] = (uint32_t)n * (uint32_t)ks;
+        } else {
+            int m = 64 * e - G::BN + lane;
+            m = M0 + m < P.M ? m : P.M - 1 - M0;
+            sg_loff[c] = (uint32_t)m * (uint32_t)ks;
+        }
+        sg_lds[c] = SG_BASE + 1024 * e;
+    }
     auto issue = [&](int step) {
-        unsigned char* stage = smem + (step % S) * G::STAGE;
+        unsigned char* stage = smem + (step % S) * STAGE;
         const uint8_t* wb = wtile + (int64_t)step * 64;
         const uint8_t* xb = xtile + (int64_t)step * 128;
 #pragma unroll
-        for (int c = 0; c < G::DPW; ++c) {
+        for (int c = 0; c < DPW; ++c) {
             if (c < G::NW_W / G::NW) {
                 dma16_to_lds(wb + loff[c], stage + ldsoff[c]);
             } else if (c < (G::NW_W + G::NW_X) / G::NW) {
@@ -586,23 +622,35 @@ gemm_big_kernel(Params P)
                 dma4_to_lds(sbase + loff[c], stage + ldsoff[c]);
             }
         }
+        if constexpr (GS) {
+            if ((step & 3) == 0) {                     // wave-uniform
+                unsigned char* slot = smem + ((step >> 2) & 1) * (16 * SG_ROWS);
+#pragma unroll
+                for (int c = 0; c < DPW_SG; ++c)
+                    dma16_to_lds((sg_w[c] ? swtile : sxtile) + (int64_t)step * 4 + sg_loff[c], slot + sg_lds[c]);
+            }
+        }
     };
     const int abase = (wn * 16 * TN + r) * 64 + 16 * j;
     const int bbase = G::W_BYTES + (wm * 16 * TM + r) * 64 + 16 * j;
-    const int sabase = G::W_BYTES + G::X_BYTES + (wn * 16 * TN + r) * 4;
-    const int sbbase = G::W_BYTES + G::X_BYTES + G::SW_BYTES + (wm * 16 * TM + r) * 4;
+    const int sabase = GS ? SG_BASE + (wn * 16 * TN + r) * 16 : G::W_BYTES + G::X_BYTES + (wn * 16 * TN + r) * 4;
+    const int sbbase = GS ? SG_BASE + (G::BN + wm * 16 * TM + r) * 16
+                          : G::W_BYTES + G::X_BYTES + G::SW_BYTES + (wm * 16 * TM + r) * 4;
+    constexpr int SROW = GS ? 256 : 64;              // bytes between the scale dwords of tiles i and i + 1
     auto read = [&](BigFrags<TN, TM>& f, int step) {
-        const unsigned char* stage = smem + (step % S) * G::STAGE;
+        const unsigned char* stage = smem + (step % S) * STAGE;
+        const unsigned char* sst = GS ? smem + ((step >> 2) & 1) * (16 * SG_ROWS) + 4 * (step & 3) : stage;
 #pragma unroll
         for (int i = 0; i < TN; ++i) {
             f.a[i] = *reinterpret_cast<const u32x4_t*>(stage + abase + 1024 * i);
-            f.sa[i] = *reinterpret_cast<const uint32_t*>(stage + sabase + 64 * i);
+            f.sa[i] = *reinterpret_cast<const uint32_t*>(sst + sabase + SROW * i);
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             f.b[i] = concat8(*reinterpret_cast<const u32x4_t*>(stage + bbase + 1024 * i),
                              *reinterpret_cast<const u32x4_t*>(stage + bbase + 1024 * i + G::BM * 64));
-            f.sb[i] = *reinterpret_cast<const uint32_t*>(stage + sbbase + 64 * i);
+            if constexpr (!TOK) f.sb[i] = *reinterpret_cast<const uint32_t*>(sst + sbbase + SROW * i);
+            else f.sb[i] = 0u;
         }
     };
 
@@ -612,13 +660,20 @@ gemm_big_kernel(Params P)
 #pragma unroll
         for (int b = 0; b < TM; ++b) acc[a][b] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 
-    // ring protocol as in gemm_lds_body (wait for step q, barrier, refill the retired buffer, read)
+    // ring protocol as in gemm_lds_body (wait for step q, barrier, refill the retired buffer, read);
+    // under GS the steps issued after q carry DPW_SG more copies each when they start a group
     auto sync_read = [&](BigFrags<TN, TM>& f, int q) {
         const int left = nsteps - 1 - q;
         const int ahead = left < S - 2 ? left : S - 2;
-        if (ahead >= 2) wait_vmcnt<2 * G::DPW>();
-        else if (ahead == 1) wait_vmcnt<G::DPW>();
-        else wait_vmcnt<0>();
+        if constexpr (GS) {
+            int later = ahead * DPW;
+            for (int t = q + 1; t <= q + ahead; ++t) later += (t & 3) == 0 ? DPW_SG : 0;
+            wait_vmcnt_dyn(later);
+        } else {
+            if (ahead >= 2) wait_vmcnt<2 * DPW>();
+            else if (ahead == 1) wait_vmcnt<DPW>();
+            else wait_vmcnt<0>();
+        }
         lds_barrier_all();
         if (q + S - 1 < nsteps) issue(q + S - 1);
         read(f, q);
@@ -865,8 +920,12 @@ int launch_gemm(Params& P, int variant, bool tok, hipStream_t st)
     P.nblk = (P.N + BN - 1) / BN;
     P.mblk = (P.M + BM - 1) / BM;
     if ((int64_t)P.nblk * P.mblk > 0x7FFFFFFF - kXcds) return FP8KV_ERR_SHAPE;
-    const int lds = variant == 6 ? BigGeom<2, 2, 8, 4, 2>::LDS : variant == 7 ? BigGeom<2, 2, 4, 8, 2>::LDS
-                  : variant == 8 ? BigGeom<2, 4, 8, 4, 3>::LDS : variant == 1 ? 0
+    // the big-tile kernels copy each row's scales of four steps at once when K % 512 == 0
+    const bool gs = P.K % 512 == 0;
+    const int lds = variant == 6 ? (gs ? BigGeom<2, 2, 8, 4, 2>::lds_gs(tok) : BigGeom<2, 2, 8, 4, 2>::LDS)
+                  : variant == 7 ? (gs ? BigGeom<2, 2, 4, 8, 2>::lds_gs(tok) : BigGeom<2, 2, 4, 8, 2>::LDS)
+                  : variant == 8 ? (gs ? BigGeom<2, 4, 8, 4, 3>::lds_gs(tok) : BigGeom<2, 4, 8, 4, 3>::LDS)
+                  : variant == 1 ? 0
                   : variant == 0 ? LdsGeom<2, 2, 4>::LDS : variant == 2 || variant == 4 ? LdsGeom<2, 2, 3>::LDS
                   : variant == 3 ? LdsGeom<2, 2, 5>::LDS : LdsGeom<2, 2, 2>::LDS;
     const int gm = pick_split(P, BM, lds, !tok);
@@ -876,9 +935,10 @@ int launch_gemm(Params& P, int variant, bool tok, hipStream_t st)
     const int64_t grid = per_xcd * kXcds;
     begin_launch();
     if (tok) {
-        if (variant == 6)
-            launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2, true>, dim3((unsigned)grid), dim3(256),
-                          BigGeom<2, 2, 8, 4, 2>::LDS, st, P);
+        if (variant == 6 && gs)
+            launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2, true, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
+        else if (variant == 6)
+            launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
         else
             launch_kernel(gemm_lds2_kernel<2, 2, 2, true>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 2>::LDS,
                           st, P);
@@ -898,16 +958,22 @@ int launch_gemm(Params& P, int variant, bool tok, hipStream_t st)
             launch_kernel(gemm_lds2_kernel<2, 2, 3>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 3>::LDS, st, P);
             break;
         case 6:
-            launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2>, dim3((unsigned)grid), dim3(256),
-                          BigGeom<2, 2, 8, 4, 2>::LDS, st, P);
+            if (gs)
+                launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2, false, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
+            else
+                launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2>, dim3((unsigned)grid), dim3(256), lds, st, P);
             break;
         case 7:
-            launch_kernel(gemm_big_kernel<2, 2, 4, 8, 2>, dim3((unsigned)grid), dim3(256),
-                          BigGeom<2, 2, 4, 8, 2>::LDS, st, P);
+            if (gs)
+                launch_kernel(gemm_big_kernel<2, 2, 4, 8, 2, false, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
+            else
+                launch_kernel(gemm_big_kernel<2, 2, 4, 8, 2>, dim3((unsigned)grid), dim3(256), lds, st, P);
             break;
         case 8:
-            launch_kernel(gemm_big_kernel<2, 4, 8, 4, 3>, dim3((unsigned)grid), dim3(512),
-                          BigGeom<2, 4, 8, 4, 3>::LDS, st, P);
+            if (gs)
+                launch_kernel(gemm_big_kernel<2, 4, 8, 4, 3, false, true>, dim3((unsigned)grid), dim3(512), lds, st, P);
+            else
+                launch_kernel(gemm_big_kernel<2, 4, 8, 4, 3>, dim3((unsigned)grid), dim3(512), lds, st, P);
             break;
         default:                                          // 5
             launch_kernel(gemm_lds2_kernel<2, 2, 2>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 2>::LDS, st, P);
