@@ -230,7 +230,8 @@ gemm_kernel(Params P)
 // DMA (global_load_lds; every wave issues the same number of copies per step, so vmcnt counts
 // are exact), S steps in flight in an LDS ring.  After one barrier per step, each wave reads the
 // next step's fragments into registers (ds_read_b128: every read covers one contiguous KB) while
-// its MFMAs work on the current step.
+// its MFMAs work on the current step.  With K % 512 == 0 the scale bytes of four steps come in one
+// 16-byte copy per row instead (GS), into a two-slot scale ring behind the operand ring.
 template <int DPW>
 __device__ __forceinline__ void wait_stages_ahead(int ahead)
 {
@@ -258,6 +259,13 @@ struct LdsGeom {
     static constexpr int LDS = S * STAGE;
     static_assert(NDMA % NW == 0, "copies must split evenly over the waves");
     static_assert(3 * DPW < 64, "vmcnt range");
+    // grouped scales, as in BigGeom (a scale slot is refilled four steps after its last read, so
+    // S <= 5)
+    static constexpr int OPER = W_BYTES + X_BYTES;
+    static constexpr int sg_rows(bool tok) { return tok ? BN : BN + BM; }
+    static constexpr int dpw_sg(bool tok) { return (sg_rows(tok) / 64 + NW - 1) / NW; }
+    static constexpr int lds_gs(bool tok) { return S * OPER + 2 * 16 * sg_rows(tok); }
+    static_assert(S <= 5 && lds_gs(false) <= 160 * 1024, "grouped scales");
 };
 
 // DB: fragments double-buffered in registers (one workgroup per CU) or single-buffered with two
@@ -266,10 +274,15 @@ struct LdsGeom {
 // TOK: per-token mode (activation block scales fixed at 2^0, each output row multiplied by
 // P.tok_scale[m]); the activation-scale copies then read weight-scale rows of the tile (clamped
 // into the operand) so that every wave still issues the same copies and the waits stay exact.
-template <int WN, int WM, int S, bool DB, bool TOK>
+// GS: grouped scale copies (K % 512 == 0), as in gemm_big_kernel.
+template <int WN, int WM, int S, bool DB, bool TOK, bool GS>
 __device__ __forceinline__ void gemm_lds_body(const Params& P)
 {
     using G = LdsGeom<WN, WM, S>;
+    constexpr int STAGE = GS ? G::OPER : G::STAGE;
+    constexpr int DPW = GS ? (G::NW_W + G::NW_X) / G::NW : G::DPW;      // copies per wave and step
+    constexpr int SG_ROWS = G::sg_rows(TOK), DPW_SG = G::dpw_sg(TOK);     // GS: copies per group
+    constexpr int SG_BASE = S * G::OPER;
     extern __shared__ __align__(16) unsigned char smem[];
     int nb, mb;
     if (!tile_of(P, blockIdx.x, nb, mb)) return;
@@ -291,10 +304,10 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
     const uint8_t* const xtile = P.Xq + (int64_t)M0 * P.K;
     const uint8_t* const swtile = P.St + (int64_t)N0 * ks;
     const uint8_t* const sxtile = TOK ? swtile : P.Sx + (int64_t)M0 * ks;
-    uint32_t loff[G::DPW];
-    int ldsoff[G::DPW];
+    uint32_t loff[DPW];
+    int ldsoff[DPW];
 #pragma unroll
-    for (int c = 0; c < G::DPW; ++c) {
+    for (int c = 0; c < DPW; ++c) {
         const int d = c * G::NW + wave;
         if (c < G::NW_W / G::NW) {                           // weight codes: rows 16 d .. 16 d + 15
             int n = 16 * d + (lane >> 2);
@@ -325,12 +338,33 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
             }
         }
     }
+    // GS scale copies: copy e of a group covers rows 64 e .. 64 e + 63 of the group's rows (weight
+    // rows, then token rows), lane = row, 16 bytes (four steps) each; padding copies repeat the last.
+    uint32_t sg_loff[GS ? DPW_SG : 1];
+    int sg_lds[GS ? DPW_SG : 1];
+    bool sg_w[GS ? DPW_SG : 1];
+#pragma unroll
+    for (int c = 0; c < (GS ? DPW_SG : 0); ++c) {
+        int e = c * G::NW + wave;
+        if (e >= SG_ROWS / 64) e = SG_ROWS / 64 - 1;
+        sg_w[c] = e < G::BN / 64;
+        if (sg_w[c]) {
+            int n = 64 * e + lane;
+            n = N0 + n < P.N ? n : P.N - 1 - N0;
+            sg_loff[c] = (uint32_t)n * (uint32_t)ks;
+        } else {
+            int m = 64 * e - G::BN + lane;
+            m = M0 + m < P.M ? m : P.M - 1 - M0;
+            sg_loff[c] = (uint32_t)m * (uint32_t)ks;
+        }
+        sg_lds[c] = SG_BASE + 1024 * e;
+    }
     auto issue = [&](int step) {
-        unsigned char* stage = smem + (step % S) * G::STAGE;
+        unsigned char* stage = smem + (step % S) * STAGE;
         const uint8_t* wb = wtile + (int64_t)step * 64;
         const uint8_t* xb = xtile + (int64_t)step * 128;
 #pragma unroll
-        for (int c = 0; c < G::DPW; ++c) {
+        for (int c = 0; c < DPW; ++c) {
             if (c < G::NW_W / G::NW) {
                 dma16_to_lds(wb + loff[c], stage + ldsoff[c]);
             } else if (c < (G::NW_W + G::NW_X) / G::NW) {
@@ -341,25 +375,37 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
                 dma4_to_lds(sbase + loff[c], stage + ldsoff[c]);
             }
         }
+        if constexpr (GS) {
+            if ((step & 3) == 0) {                     // wave-uniform
+                unsigned char* slot = smem + ((step >> 2) & 1) * (16 * SG_ROWS);
+#pragma unroll
+                for (int c = 0; c < DPW_SG; ++c)
+                    dma16_to_lds((sg_w[c] ? swtile : sxtile) + (int64_t)step * 4 + sg_loff[c], slot + sg_lds[c]);
+            }
+        }
     };
     // fragment reads: one lane base per kind, tiles at constant offsets from it
     const int abase = (wn * 64 + r) * 64 + 16 * j;
     const int bbase = G::W_BYTES + (wm * 64 + r) * 64 + 16 * j;
-    const int sabase = G::W_BYTES + G::X_BYTES + (wn * 64 + r) * 4;
-    const int sbbase = G::W_BYTES + G::X_BYTES + G::SW_BYTES + (wm * 64 + r) * 4;
+    const int sabase = GS ? SG_BASE + (wn * 64 + r) * 16 : G::W_BYTES + G::X_BYTES + (wn * 64 + r) * 4;
+    const int sbbase = GS ? SG_BASE + (G::BN + wm * 64 + r) * 16
+                          : G::W_BYTES + G::X_BYTES + G::SW_BYTES + (wm * 64 + r) * 4;
+    constexpr int SROW = GS ? 256 : 64;              // bytes between the scale dwords of tiles i and i + 1
     auto read = [&](Frags& f, int step) {
-        const unsigned char* stage = smem + (step % S) * G::STAGE;
+        const unsigned char* stage = smem + (step % S) * STAGE;
+        const unsigned char* sst = GS ? smem + ((step >> 2) & 1) * (16 * SG_ROWS) + 4 * (step & 3) : stage;
         const unsigned char* pa = stage + abase;
         const unsigned char* pb = stage + bbase;
-        const unsigned char* psa = stage + sabase;
-        const unsigned char* psb = stage + sbbase;
+        const unsigned char* psa = sst + sabase;
+        const unsigned char* psb = sst + sbbase;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             f.a[i] = *reinterpret_cast<const u32x4_t*>(pa + 1024 * i);
             f.b[i] = concat8(*reinterpret_cast<const u32x4_t*>(pb + 1024 * i),
                              *reinterpret_cast<const u32x4_t*>(pb + 1024 * i + G::BM * 64));
-            f.sa[i] = *reinterpret_cast<const uint32_t*>(psa + 64 * i);
-            f.sb[i] = *reinterpret_cast<const uint32_t*>(psb + 64 * i);
+            f.sa[i] = *reinterpret_cast<const uint32_t*>(psa + SROW * i);
+            if constexpr (!TOK || !GS) f.sb[i] = *reinterpret_cast<const uint32_t*>(psb + SROW * i);
+            else f.sb[i] = 0u;
         }
     };
 
@@ -375,7 +421,14 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
     // barrier), step q + S - 1 is copied into that buffer, and step q's fragments are read.
     auto sync_read = [&](Frags& f, int q) {
         const int left = nsteps - 1 - q;
-        wait_stages_ahead<G::DPW>(left < S - 2 ? left : S - 2);
+        const int ahead = left < S - 2 ? left : S - 2;
+        if constexpr (GS) {                           // later steps that start a group carry DPW_SG more
+            int later = ahead * DPW;
+            for (int t = q + 1; t <= q + ahead; ++t) later += (t & 3) == 0 ? DPW_SG : 0;
+            wait_vmcnt_dyn(later);
+        } else {
+            wait_stages_ahead<DPW>(ahead);
+        }
         lds_barrier_all();
         if (q + S - 1 < nsteps) issue(q + S - 1);
         read(f, q);
@@ -435,18 +488,18 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
     }
 }
 
-template <int WN, int WM, int S>
+template <int WN, int WM, int S, bool GS = false>
 __global__ void __launch_bounds__(64 * WN * WM)
 gemm_lds_kernel(Params P)
 {
-    gemm_lds_body<WN, WM, S, true, false>(P);
+    gemm_lds_body<WN, WM, S, true, false, GS>(P);
 }
 
-template <int WN, int WM, int S, bool TOK = false>
+template <int WN, int WM, int S, bool TOK = false, bool GS = false>
 __global__ void __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_lds2_kernel(Params P)
 {
-    gemm_lds_body<WN, WM, S, false, TOK>(P);
+    gemm_lds_body<WN, WM, S, false, TOK, GS>(P);
 }
 
 // ---- larger wave tiles -------------------------------------------------------------------------
@@ -926,8 +979,10 @@ int launch_gemm(Params& P, int variant, bool tok, hipStream_t st)
                   : variant == 7 ? (gs ? BigGeom<2, 2, 4, 8, 2>::lds_gs(tok) : BigGeom<2, 2, 4, 8, 2>::LDS)
                   : variant == 8 ? (gs ? BigGeom<2, 4, 8, 4, 3>::lds_gs(tok) : BigGeom<2, 4, 8, 4, 3>::LDS)
                   : variant == 1 ? 0
-                  : variant == 0 ? LdsGeom<2, 2, 4>::LDS : variant == 2 || variant == 4 ? LdsGeom<2, 2, 3>::LDS
-                  : variant == 3 ? LdsGeom<2, 2, 5>::LDS : LdsGeom<2, 2, 2>::LDS;
+                  : variant == 0 ? (gs ? LdsGeom<2, 2, 4>::lds_gs(tok) : LdsGeom<2, 2, 4>::LDS)
+                  : variant == 2 || variant == 4 ? (gs ? LdsGeom<2, 2, 3>::lds_gs(tok) : LdsGeom<2, 2, 3>::LDS)
+                  : variant == 3 ? (gs ? LdsGeom<2, 2, 5>::lds_gs(tok) : LdsGeom<2, 2, 5>::LDS)
+                  : (gs ? LdsGeom<2, 2, 2>::lds_gs(tok) : LdsGeom<2, 2, 2>::LDS);
     const int gm = pick_split(P, BM, lds, !tok);
     P.gm = gm;
     P.gn = kXcds / gm;
@@ -939,9 +994,10 @@ int launch_gemm(Params& P, int variant, bool tok, hipStream_t st)
             launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2, true, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
         else if (variant == 6)
             launch_kernel(gemm_big_kernel<2, 2, 8, 4, 2, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
+        else if (gs)
+            launch_kernel(gemm_lds2_kernel<2, 2, 2, true, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
         else
-            launch_kernel(gemm_lds2_kernel<2, 2, 2, true>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 2>::LDS,
-                          st, P);
+            launch_kernel(gemm_lds2_kernel<2, 2, 2, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
         return finish_launch();
     }
     switch (variant) {
@@ -949,13 +1005,16 @@ int launch_gemm(Params& P, int variant, bool tok, hipStream_t st)
             launch_kernel(gemm_kernel, dim3((unsigned)grid), dim3(256), 0, st, P);
             break;
         case 2:
-            launch_kernel(gemm_lds_kernel<2, 2, 3>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 3>::LDS, st, P);
+            if (gs) launch_kernel(gemm_lds_kernel<2, 2, 3, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
+            else launch_kernel(gemm_lds_kernel<2, 2, 3>, dim3((unsigned)grid), dim3(256), lds, st, P);
             break;
         case 3:
-            launch_kernel(gemm_lds_kernel<2, 2, 5>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 5>::LDS, st, P);
+            if (gs) launch_kernel(gemm_lds_kernel<2, 2, 5, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
+            else launch_kernel(gemm_lds_kernel<2, 2, 5>, dim3((unsigned)grid), dim3(256), lds, st, P);
             break;
         case 4:
-            launch_kernel(gemm_lds2_kernel<2, 2, 3>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 3>::LDS, st, P);
+            if (gs) launch_kernel(gemm_lds2_kernel<2, 2, 3, false, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
+            else launch_kernel(gemm_lds2_kernel<2, 2, 3>, dim3((unsigned)grid), dim3(256), lds, st, P);
             break;
         case 6:
             if (gs)
@@ -976,10 +1035,12 @@ int launch_gemm(Params& P, int variant, bool tok, hipStream_t st)
                 launch_kernel(gemm_big_kernel<2, 4, 8, 4, 3>, dim3((unsigned)grid), dim3(512), lds, st, P);
             break;
         default:                                          // 5
-            launch_kernel(gemm_lds2_kernel<2, 2, 2>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 2>::LDS, st, P);
+            if (gs) launch_kernel(gemm_lds2_kernel<2, 2, 2, false, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
+            else launch_kernel(gemm_lds2_kernel<2, 2, 2>, dim3((unsigned)grid), dim3(256), lds, st, P);
             break;
         case 0:
-            launch_kernel(gemm_lds_kernel<2, 2, 4>, dim3((unsigned)grid), dim3(256), LdsGeom<2, 2, 4>::LDS, st, P);
+            if (gs) launch_kernel(gemm_lds_kernel<2, 2, 4, true>, dim3((unsigned)grid), dim3(256), lds, st, P);
+            else launch_kernel(gemm_lds_kernel<2, 2, 4>, dim3((unsigned)grid), dim3(256), lds, st, P);
             break;
     }
     return finish_launch();
