@@ -973,8 +973,9 @@ int launch_gemm(Params& P, int variant, bool tok, hipStream_t st)
     P.nblk = (P.N + BN - 1) / BN;
     P.mblk = (P.M + BM - 1) / BM;
     if ((int64_t)P.nblk * P.mblk > 0x7FFFFFFF - kXcds) return FP8KV_ERR_SHAPE;
-    // the big-tile kernels copy each row's scales of four steps at once when K % 512 == 0
-    const bool gs = P.K % 512 == 0;
+    // each row's scales of four steps in one 16-byte copy when K % 512 == 0 (rows 16-byte aligned)
+    // and the scale operands start 16-byte aligned; the entry points only require 4
+    const bool gs = P.K % 512 == 0 && aligned(P.St, 16) && (tok || aligned(P.Sx, 16));
     const int lds = variant == 6 ? (gs ? BigGeom<2, 2, 8, 4, 2>::lds_gs(tok) : BigGeom<2, 2, 8, 4, 2>::LDS)
                   : variant == 7 ? (gs ? BigGeom<2, 2, 4, 8, 2>::lds_gs(tok) : BigGeom<2, 2, 4, 8, 2>::LDS)
                   : variant == 8 ? (gs ? BigGeom<2, 4, 8, 4, 3>::lds_gs(tok) : BigGeom<2, 4, 8, 4, 3>::LDS)

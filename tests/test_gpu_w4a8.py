@@ -75,6 +75,32 @@ def test_gemm_parity(N, K, M, variant, order):
     assert matvec.bf16_excess_error(got, ref) < 1e-4
 
 
+@pytest.mark.parametrize("variant", [-1, 5, 6, 8])
+def test_gemm_scales_only_4_byte_aligned(variant):
+    """Scale operands that start 4 bytes past a 16-byte boundary (the entry point requires 4): the
+    kernels that copy four steps' scales per lane at once (K % 512 == 0) must fall back to per-step
+    copies and still meet the bar."""
+    N, K, M = 512, 3584, 200
+    lib = _lib.load()
+    c, rc, rs = _gemm_case(N, K, M, seed=77)
+
+    def offset_view(a):
+        buf = torch.zeros(a.size + 16, dtype=torch.uint8, device=DEV)
+        v = buf[4:4 + a.size].view(a.shape)
+        v.copy_(torch.from_numpy(np.ascontiguousarray(a)).to(DEV))
+        assert v.data_ptr() % 16 == 4
+        return v
+
+    try:
+        lib.fp8kv_gemm_tune(variant, 0)
+        out = ops.h4a8_gemm(torch.from_numpy(rc).to(DEV), offset_view(rs), c["W"].to(DEV), offset_view(c["St"].numpy()))
+        torch.cuda.synchronize()
+    finally:
+        lib.fp8kv_gemm_tune(-1, 0)
+    ref = w4a8.gemm(c["W"].numpy(), c["St"].numpy(), rc, rs)
+    assert matvec.bf16_excess_error(out.float().cpu().numpy(), ref) < 1e-4
+
+
 def test_end_to_end_against_w4a16_product():
     N, K, M = 1024, 3584, 64
     c = workloads.w4_case(N, K, M, seed=21)
