@@ -131,6 +131,38 @@ def test_gemm_repeats_bitwise(variant, act):
     assert matvec.bf16_excess_error(outs[0].float().cpu().numpy(), ref) < 1e-4
 
 
+def _random_shapes(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        K = 128 * int(rng.integers(1, 48))                 # half of them K % 512 == 0 on average
+        if rng.random() < 0.5:
+            K = 512 * max(1, K // 512)
+        N = 4 * int(rng.integers(1, 1200))
+        M = int(rng.integers(1, 700))
+        out.append((N, K, M))
+    return out
+
+
+@pytest.mark.parametrize("N,K,M", _random_shapes(12, 2026))
+@pytest.mark.parametrize("act", ["mx", "token"])
+def test_gemm_random_shapes(N, K, M, act):
+    """Seeded random shapes through the default planner (every tile size, ring, XCD split and the
+    grouped scale copies where K % 512 == 0), against the oracle."""
+    if act == "token":
+        c, rc, rs = _token_case(N, K, M, seed=N + K + M)
+        out = ops.h4a8_gemm_token(torch.from_numpy(rc).to(DEV), torch.from_numpy(rs).to(DEV), c["W"].to(DEV),
+                                  c["St"].to(DEV))
+        ref = w4a8.gemm_token(c["W"].numpy(), c["St"].numpy(), rc, rs)
+    else:
+        c, rc, rs = _gemm_case(N, K, M, seed=N + K + M)
+        out = ops.h4a8_gemm(torch.from_numpy(rc).to(DEV), torch.from_numpy(rs).to(DEV), c["W"].to(DEV),
+                            c["St"].to(DEV))
+        ref = w4a8.gemm(c["W"].numpy(), c["St"].numpy(), rc, rs)
+    torch.cuda.synchronize()
+    assert matvec.bf16_excess_error(out.float().cpu().numpy(), ref) < 1e-4
+
+
 def test_end_to_end_against_w4a16_product():
     N, K, M = 1024, 3584, 64
     c = workloads.w4_case(N, K, M, seed=21)
