@@ -38,12 +38,15 @@ HIPCC_FLAGS = [
 
 # Per-file code-generation options.  The block-scaled MFMA accumulates in place only in its VGPR
 # form; left to choose, the compiler keeps the GEMM accumulators in VGPRs and copies them into
-# AGPRs around every MFMA.  Kernel-argument preloading (gfx950: the first 16 SGPRs of the leading
+# AGPRs around every MFMA.  The GEMM is also scheduled with the iterative ILP strategy (measured
+# at the configs[4] linears, M = 2048: gate/up 298-299 -> 274-275 us on MXFP8 activations and
+# 283-284 -> 264 us per-token, the four linears together -4%; the attention kernels were slower
+# or unchanged with it).  Kernel-argument preloading (gfx950: the first 16 SGPRs of the leading
 # scalar arguments are loaded before the wave starts) removes one dependent round trip from the
 # start of the matvec and decode kernels (measured: matvec cfg1 M = 1 11.35 -> 11.12 us, M = 8
 # 12.85 -> 12.40 us).  Arguments passed as a struct are not preloaded.
 FILE_FLAGS = {
-    "w4a8_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "w4a8_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "h4mv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
     "decode_attn.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
     "prefill_bf16kv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
