@@ -40,8 +40,8 @@ HIPCC_FLAGS = [
 # form; left to choose, the compiler keeps the GEMM accumulators in VGPRs and copies them into
 # AGPRs around every MFMA.  The GEMM is also scheduled with the iterative ILP strategy (measured
 # at the configs[4] linears, M = 2048: gate/up 298-299 -> 274-275 us on MXFP8 activations and
-# 283-284 -> 264 us per-token, the four linears together -4%; the attention kernels were slower
-# or unchanged with it).  Kernel-argument preloading (gfx950: the first 16 SGPRs of the leading
+# 283-284 -> 264 us per-token, the four linears together -4%; the attention and matvec kernels
+# were slower or unchanged with it).  Kernel-argument preloading (gfx950: the first 16 SGPRs of the leading
 # scalar arguments are loaded before the wave starts) removes one dependent round trip from the
 # start of the matvec and decode kernels (measured: matvec cfg1 M = 1 11.35 -> 11.12 us, M = 8
 # 12.85 -> 12.40 us).  Arguments passed as a struct are not preloaded.
