@@ -46,16 +46,21 @@ constexpr int kXcds = 8;
 // 8: 8 waves of 8 x 4 tiles (256 x 256 per workgroup, 3-step ring, 150 KB of LDS).  Measured on
 // the configs[4] linears at M = 2048: 6 ~1.22-1.69 PFLOP/s, 5 ~1.27-1.41, 8 ~0.88-1.67 (only
 // gate/up fills the GPU), 7 ~1.05-1.27, 4 ~1.33, 0 ~1.01, 1 ~0.40.
-// Default (-1): variant 6 (the 8 x 4 wave tile, 256 x 128 per workgroup) when its grid has at
-// least 256 tiles or K >= 8192, else variant 5 (measured at the configs[4] linears, M = 2048:
-// gate/up 1.41 -> 1.66 PFLOP/s and down 1.41 -> 1.47 with variant 6, o 1.27 -> 1.22).
+// Default (-1): variant 6 (the 8 x 4 wave tile, 256 x 128 per workgroup) when its grid has more
+// tiles than the GPU has CUs, else variant 5 (128 x 128, twice the workgroups).  With one
+// workgroup per CU, variant 6 has one wave per SIMD and nothing hides its waits.  Measured at
+// M = 2048 (MXFP8, us per launch, variant 5 against 6): 224 tiles of 256 x 128 (down, K = 18944)
+// 150 against 184, 256 tiles (qkv) 36 against 45, 384 tiles 58-59 against 56-57, 512 tiles 68
+// against 60, 1024 tiles 131 against 116, gate/up (2368 tiles) 323 against 285.
 constexpr int kDefaultVariant = -1;
 thread_local int g_gemm_variant = kDefaultVariant;
+constexpr int64_t kGemmCus = 256;
 
 inline int default_variant(int N, int K, int M)
 {
+    (void)K;
     const int64_t tiles6 = (int64_t)((N + 255) / 256) * ((M + 127) / 128);
-    return (tiles6 >= 256 || K >= 8192) ? 6 : 5;
+    return tiles6 > kGemmCus ? 6 : 5;
 }
 
 inline int pick_variant(int N, int K, int M) { return g_gemm_variant >= 0 ? g_gemm_variant : default_variant(N, K, M); }
