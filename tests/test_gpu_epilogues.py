@@ -30,8 +30,12 @@ def _rows(M, H, seed, scale=3.0):
 
 
 @pytest.mark.parametrize("mode", [0, 1])
-@pytest.mark.parametrize("M,H", [(1, 3584), (8, 3584), (300, 4096), (5, 16384), (3, 8), (2, 5120), (7, 2056)])
+@pytest.mark.parametrize("M,H", [(1, 3584), (8, 3584), (300, 4096), (5, 16384), (3, 8), (2, 5120), (7, 2056),
+                                 (2048, 3584), (1537, 1032)])
 def test_rmsnorm_parity(mode, M, H):
+    """The output is rounded twice, bf16(bf16(z * r) * w), so a last-bit difference in r (rsqrt and
+    the order of the sum of squares) that moves bf16(z * r) by one step can end two steps away;
+    at millions of elements that happens a few times in a million."""
     x, res, w = _rows(M, H, 1), _rows(M, H, 2, 5.0), _rows(1, H, 3, 1.0)[0]
     xd, rd, wd = x.to(DEV), res.to(DEV), w.to(DEV)
     out = ops.fused_add_rmsnorm(xd, rd, wd, 1e-6, mode=mode)
@@ -39,7 +43,8 @@ def test_rmsnorm_parity(mode, M, H):
     r_out, r_res = ep.fused_add_rmsnorm(x.float().numpy(), res.float().numpy(), w.float().numpy(), 1e-6, mode)
     assert np.array_equal(rd.cpu().float().numpy(), r_res)
     d = _steps_apart(out, r_out)
-    assert d.max() <= 1 and (d == 0).mean() >= 0.99, (d.max(), (d == 0).mean())
+    assert d.max() <= 2 and (d > 1).mean() < 1e-4 and (d == 0).mean() >= 0.99, \
+        (d.max(), (d > 1).mean(), (d == 0).mean())
 
 
 def test_rmsnorm_strided_rows_in_place():
