@@ -249,6 +249,60 @@ __device__ __forceinline__ void wait_stages_ahead(int ahead)
 
 __device__ __forceinline__ void lds_barrier_all() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Grouped scale copies (GS, K % 512 == 0, scale rows 16-byte aligned): copy c of a wave covers
+// rows 64 e .. 64 e + 63 (e = c * NW + wave) of the group's rows - the BN weight rows, then in
+// MXFP8 mode the token rows - lane = row, 16 bytes each: the row's scale bytes of four steps.
+// Padding copies repeat the last.  The bytes of steps 4g .. 4g + 3 are copied with step 4g's
+// operands into slot g % 2 of a two-slot ring at byte BASE of the LDS (16 bytes per row).
+template <int DPW_SG>
+struct ScaleGroups {
+    uint32_t loff[DPW_SG];
+    int lds[DPW_SG];
+    bool w[DPW_SG];
+
+    template <int NW, int BN, int ROWS, int BASE>
+    __device__ __forceinline__ void setup(const Params& P, int wave, int lane, int N0, int M0, int ks)
+    {
+#pragma unroll
+        for (int c = 0; c < DPW_SG; ++c) {
+            int e = c * NW + wave;
+            if (e >= ROWS / 64) e = ROWS / 64 - 1;
+            w[c] = e < BN / 64;
+            if (w[c]) {
+                int n = 64 * e + lane;
+                n = N0 + n < P.N ? n : P.N - 1 - N0;
+                loff[c] = (uint32_t)n * (uint32_t)ks;
+            } else {
+                int m = 64 * e - BN + lane;
+                m = M0 + m < P.M ? m : P.M - 1 - M0;
+                loff[c] = (uint32_t)m * (uint32_t)ks;
+            }
+            lds[c] = BASE + 1024 * e;
+        }
+    }
+
+    // The group copies that go out with step `step`'s operands (none unless step % 4 == 0).
+    template <int ROWS>
+    __device__ __forceinline__ void issue(int step, unsigned char* smem, const uint8_t* swtile,
+                                          const uint8_t* sxtile) const
+    {
+        if ((step & 3) != 0) return;                   // wave-uniform
+        unsigned char* slot = smem + ((step >> 2) & 1) * (16 * ROWS);
+#pragma unroll
+        for (int c = 0; c < DPW_SG; ++c)
+            dma16_to_lds((w[c] ? swtile : sxtile) + (int64_t)step * 4 + loff[c], slot + lds[c]);
+    }
+};
+
+// Copies issued after step q's under GS: `ahead` steps of dpw operand copies each, plus dpw_sg
+// group copies with every one of them that starts a group.
+__device__ __forceinline__ int scale_group_later(int q, int ahead, int dpw, int dpw_sg)
+{
+    int later = ahead * dpw;
+    for (int t = q + 1; t <= q + ahead; ++t) later += (t & 3) == 0 ? dpw_sg : 0;
+    return later;
+}
+
 template <int WN, int WM, int S>
 struct LdsGeom {
     static constexpr int NW = WN * WM;
@@ -343,27 +397,8 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
             }
         }
     }
-    // GS scale copies: copy e of a group covers rows 64 e .. 64 e + 63 of the group's rows (weight
-    // rows, then token rows), lane = row, 16 bytes (four steps) each; padding copies repeat the last.
-    uint32_t sg_loff[GS ? DPW_SG : 1];
-    int sg_lds[GS ? DPW_SG : 1];
-    bool sg_w[GS ? DPW_SG : 1];
-#pragma unroll
-    for (int c = 0; c < (GS ? DPW_SG : 0); ++c) {
-        int e = c * G::NW + wave;
-        if (e >= SG_ROWS / 64) e = SG_ROWS / 64 - 1;
-        sg_w[c] = e < G::BN / 64;
-        if (sg_w[c]) {
-            int n = 64 * e + lane;
-            n = N0 + n < P.N ? n : P.N - 1 - N0;
-            sg_loff[c] = (uint32_t)n * (uint32_t)ks;
-        } else {
-            int m = 64 * e - G::BN + lane;
-            m = M0 + m < P.M ? m : P.M - 1 - M0;
-            sg_loff[c] = (uint32_t)m * (uint32_t)ks;
-        }
-        sg_lds[c] = SG_BASE + 1024 * e;
-    }
+    ScaleGroups<GS ? DPW_SG : 1> sg;
+    if constexpr (GS) sg.template setup<G::NW, G::BN, SG_ROWS, SG_BASE>(P, wave, lane, N0, M0, ks);
     auto issue = [&](int step) {
         unsigned char* stage = smem + (step % S) * STAGE;
         const uint8_t* wb = wtile + (int64_t)step * 64;
@@ -380,14 +415,7 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
                 dma4_to_lds(sbase + loff[c], stage + ldsoff[c]);
             }
         }
-        if constexpr (GS) {
-            if ((step & 3) == 0) {                     // wave-uniform
-                unsigned char* slot = smem + ((step >> 2) & 1) * (16 * SG_ROWS);
-#pragma unroll
-                for (int c = 0; c < DPW_SG; ++c)
-                    dma16_to_lds((sg_w[c] ? swtile : sxtile) + (int64_t)step * 4 + sg_loff[c], slot + sg_lds[c]);
-            }
-        }
+        if constexpr (GS) sg.template issue<SG_ROWS>(step, smem, swtile, sxtile);
     };
     // fragment reads: one lane base per kind, tiles at constant offsets from it
     const int abase = (wn * 64 + r) * 64 + 16 * j;
@@ -427,10 +455,8 @@ __device__ __forceinline__ void gemm_lds_body(const Params& P)
     auto sync_read = [&](Frags& f, int q) {
         const int left = nsteps - 1 - q;
         const int ahead = left < S - 2 ? left : S - 2;
-        if constexpr (GS) {                           // later steps that start a group carry DPW_SG more
-            int later = ahead * DPW;
-            for (int t = q + 1; t <= q + ahead; ++t) later += (t & 3) == 0 ? DPW_SG : 0;
-            wait_vmcnt_dyn(later);
+        if constexpr (GS) {
+            wait_vmcnt_dyn(scale_group_later(q, ahead, DPW, DPW_SG));
         } else {
             wait_stages_ahead<DPW>(ahead);
         }
@@ -644,27 +670,8 @@ gemm_big_kernel(Params P)
             }
         }
     }
-    // GS scale copies: copy e of a group covers rows 64 e .. 64 e + 63 of the group's rows (weight
-    // rows, then token rows), lane = row, 16 bytes (four steps) each; padding copies repeat the last.
-    uint32_t sg_loff[GS ? DPW_SG : 1];
-    int sg_lds[GS ? DPW_SG : 1];
-    bool sg_w[GS ? DPW_SG : 1];
-#pragma unroll
-    for (int c = 0; c < (GS ? DPW_SG : 0); ++c) {
-        int e = c * G::NW + wave;
-        if (e >= SG_ROWS / 64) e = SG_ROWS / 64 - 1;
-        sg_w[c] = e < G::BN / 64;
-        if (sg_w[c]) {
-            int n = 64 * e + lane;
-            n = N0 + n < P.N ? n : P.N - 1 - N0;
-            sg_loff[c] = (uint32_t)n * (uint32_t)ks;
-        } else {
-            int m = 64 * e - G::BN + lane;
-            m = M0 + m < P.M ? m : P.M - 1 - M0;
-            sg_loff[c] = (uint32_t)m * (uint32_t)ks;
-        }
-        sg_lds[c] = SG_BASE + 1024 * e;
-    }
+    ScaleGroups<GS ? DPW_SG : 1> sg;
+    if constexpr (GS) sg.template setup<G::NW, G::BN, SG_ROWS, SG_BASE>(P, wave, lane, N0, M0, ks);
     auto issue = [&](int step) {
         unsigned char* stage = smem + (step % S) * STAGE;
         const uint8_t* wb = wtile + (int64_t)step * 64;
@@ -680,14 +687,7 @@ gemm_big_kernel(Params P)
                 dma4_to_lds(sbase + loff[c], stage + ldsoff[c]);
             }
         }
-        if constexpr (GS) {
-            if ((step & 3) == 0) {                     // wave-uniform
-                unsigned char* slot = smem + ((step >> 2) & 1) * (16 * SG_ROWS);
-#pragma unroll
-                for (int c = 0; c < DPW_SG; ++c)
-                    dma16_to_lds((sg_w[c] ? swtile : sxtile) + (int64_t)step * 4 + sg_loff[c], slot + sg_lds[c]);
-            }
-        }
+        if constexpr (GS) sg.template issue<SG_ROWS>(step, smem, swtile, sxtile);
     };
     const int abase = (wn * 16 * TN + r) * 64 + 16 * j;
     const int bbase = G::W_BYTES + (wm * 16 * TM + r) * 64 + 16 * j;
@@ -724,9 +724,7 @@ gemm_big_kernel(Params P)
         const int left = nsteps - 1 - q;
         const int ahead = left < S - 2 ? left : S - 2;
         if constexpr (GS) {
-            int later = ahead * DPW;
-            for (int t = q + 1; t <= q + ahead; ++t) later += (t & 3) == 0 ? DPW_SG : 0;
-            wait_vmcnt_dyn(later);
+            wait_vmcnt_dyn(scale_group_later(q, ahead, DPW, DPW_SG));
         } else {
             if (ahead >= 2) wait_vmcnt<2 * DPW>();
             else if (ahead == 1) wait_vmcnt<DPW>();
