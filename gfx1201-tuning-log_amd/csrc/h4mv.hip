@@ -844,6 +844,7 @@ h4mv_kslice_batched_kernel(const uint8_t* __restrict__ W, const uint8_t* __restr
 constexpr int kM1MaxWaves = 16;
 constexpr int kM1Workgroups = 512;             // two workgroups per CU when their LDS allows it
 constexpr int kM1MinTiles = 1024;              // default: when the tiles alone fill the GPU
+constexpr int kM1RoundWaves = 4;               // waves per workgroup when one round cannot hold the tiles
 constexpr int kM1MaxSteps = 64;                // K <= 32768
 constexpr int kM1MaxScaleCopies = kM1MaxSteps / 4;   // 16 nsteps / 64 copies of the scale slice
 
@@ -1579,6 +1580,19 @@ inline bool m1_plan(int N, int K, int M, M1Plan& p)
         if (2 * p.lds <= kLdsPerCU) return true;
         plan_for(kM1Workgroups / 2);
         if (p.lds <= kLdsPerCU) return true;
+    }
+    // More tiles than one round holds at any wave count the LDS allows (the lm_head vocabulary:
+    // 8011 tiles at K = 3584 would need 16 waves and 178 KB): workgroups of kM1RoundWaves waves,
+    // two per CU, over several rounds.  Measured at N = 128167, K = 3584 (one process, two rounds,
+    // events / graph replay): 4 waves 38.6-39.0 / 38.9-39.5 us against 39.7-40.3 / 40.5-41.7 on
+    // the streaming kernel; 2 waves 38.7-38.8 / 39.0-39.5, 3 waves 38.7-39.1 / 39.3-39.6, 5 and 6
+    // waves 39.2-40.1 / 40.1-40.6, 1 wave 42.0-42.8, ring depth 3 the same or slower.
+    if (g_m1_wgs == 0) {
+        p.depth = 2;
+        p.tw = std::min(kM1RoundWaves, T);
+        p.grid = (T + p.tw - 1) / p.tw;
+        p.lds = (size_t)m1_x_bytes(K) + 2 * (size_t)K + (size_t)p.tw * m1_wave_bytes(p.depth, nsteps);
+        if (2 * p.lds <= kLdsPerCU) return true;
     }
     return false;
 }

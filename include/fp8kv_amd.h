@@ -51,11 +51,12 @@ const char* fp8kv_last_hip_error_string(void);
  * M > 8 silently as M = 8), bf16 rounding is nearest-even (the reference rounds half up), and a
  * rejected call launches nothing and records its status for fp8kv_last_status().
  * Non-finite activations: NaN in X gives NaN outputs of its row (as the reference).  An infinity
- * in X gives NaN in every output of its row on the block-scaled kernels, which run 1 <= M <= 8 on
- * shapes of at least 1024 row tiles with K % 512 == 0 whose workgroups fit one round (cfg1, the
- * configs[4] gate/up shape); there the row is split into e4m3 parts, which have no infinity, and
- * its 32-k block takes the NaN scale.  Everywhere else it gives +-inf (NaN where its weight is
- * zero), as the reference does.  fp8kv_h4mv_plan (fp8kv_diag.h) reports which kernel a shape uses.
+ * in X gives NaN in every output of its row on the block-scaled kernels, which run on shapes of at
+ * least 1024 row tiles with K % 512 == 0: at M = 1 (cfg1, the configs[4] gate/up shape, the
+ * lm_head vocabulary), and at 2 <= M <= 8 where the workgroups fit one round (cfg1, gate/up);
+ * there the row is split into e4m3 parts, which have no infinity, and its 32-k block takes the NaN
+ * scale.  Everywhere else it gives +-inf (NaN where its weight is zero), as the reference does.
+ * fp8kv_h4mv_plan (fp8kv_diag.h) reports which kernel a shape uses.
  */
 void h4mv_launch(const void* W, const void* St, const void* Xb, void* Out,
                  int N, int K, int M, void* stream);

@@ -130,7 +130,7 @@ def test_h4mv_mx_in_bounds(lib, depth, wgs):
 
 
 def test_h4mv_plan_picks_the_measured_kernels(lib):
-    """The default plans: M = 1 kernel for cfg1 and gate/up at M = 1, the hi / lo kernel at
+    """The default plans: M = 1 kernel for cfg1, gate/up and the lm_head vocabulary at M = 1, the hi / lo kernel at
     M = 2 .. 8 (one round of workgroups; conversion chunks of two steps for workgroups of more
     than four waves), the K-slice kernel for the lm_head vocabulary, the streaming kernel for the
     short-N configs[4] linears."""
@@ -146,6 +146,10 @@ def test_h4mv_plan_picks_the_measured_kernels(lib):
     assert kernel(28672, 4096, 4) == 4 and out[5] == 4 and out[1] == 448 and out[2] == 4
     assert kernel(28672, 4096, 8) == 4 and out[5] == 8 and out[1] == 256 and out[2] == 7
     assert [kernel(128167, 3584, M) for M in (3, 8)] == [5, 5]
+    # M = 1 at the lm_head vocabulary: more tiles than one round holds at any wave count the LDS
+    # allows, so 4-wave workgroups over several rounds
+    assert kernel(128167, 3584, 1) == 3 and out[1] == 2003 and out[2] == 4 and out[3] == 2
+    assert lib.fp8kv_h4mv_audit(128167, 3584, 1) == 0
     for N, K in ((4096, 3584), (3584, 3072), (3584, 18944)):
         assert [kernel(N, K, M) for M in (1, 4, 8)] == [1, 1, 1]
     assert kernel(64, 96, 2) == 0
