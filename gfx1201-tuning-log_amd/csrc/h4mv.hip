@@ -1673,6 +1673,20 @@ inline bool mx_plan(int N, int K, int M, MxPlan& p)
         plan_for(kM1Workgroups / 2);
         if (p.lds <= kLdsPerCU && (g_mx_mode == 1 || p.grid <= kM1Workgroups / 2)) return true;
     }
+    // Two activation rows and more tiles than one round holds (the lm_head vocabulary): workgroups
+    // of kM1RoundWaves waves over several rounds, as at M = 1.  Measured at N = 128167, K = 3584
+    // (one process, two rounds, events / graph replay): M = 2 38.6-38.8 / 39.2-39.6 us against
+    // 40.3-41.9 / 40.8-41.9 on the streaming kernel; at M = 4 the same form ties with the batched
+    // K-slice kernel (41.7-42.6 against 41.6-42.1) and at M = 8 it is slower (67.7-68.0 against
+    // 43.6-44.8: every workgroup converts all eight rows), so those keep the K-slice kernels.
+    if (g_mx_wgs == 0 && p.mm == 2) {
+        p.depth = 2;
+        p.tw = std::min(kM1RoundWaves, T);
+        p.grid = (T + p.tw - 1) / p.tw;
+        p.lds = (size_t)mx_x_bytes(p.mm, K) + (size_t)p.tw * m1_wave_bytes(p.depth, nsteps);
+        p.cs_log2 = mx_chunk_log2(nsteps, p.tw);
+        if (2 * p.lds <= kLdsPerCU) return true;
+    }
     return false;
 }
 

@@ -43,7 +43,7 @@ def _case_topk(N, K, M, k, seed):
     return vals, idx, rv, ri
 
 
-@pytest.mark.parametrize("M,k", [(1, 1), (1, 64), (4, 8), (8, 50)])
+@pytest.mark.parametrize("M,k", [(1, 1), (1, 64), (2, 64), (4, 8), (8, 50)])
 def test_vocab_topk(M, k):
     """The reference model's lm_head: vocab 128167 (not a multiple of 16), hidden 3584."""
     _case_topk(128167, 3584, M, k, seed=600 + M + k)

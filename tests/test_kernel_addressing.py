@@ -150,6 +150,9 @@ def test_h4mv_plan_picks_the_measured_kernels(lib):
     # allows, so 4-wave workgroups over several rounds
     assert kernel(128167, 3584, 1) == 3 and out[1] == 2003 and out[2] == 4 and out[3] == 2
     assert lib.fp8kv_h4mv_audit(128167, 3584, 1) == 0
+    # ... and the same form of the hi / lo kernel at M = 2 (two rows in LDS)
+    assert kernel(128167, 3584, 2) == 4 and out[1] == 2003 and out[2] == 4 and out[5] == 2
+    assert lib.fp8kv_h4mv_audit(128167, 3584, 2) == 0
     for N, K in ((4096, 3584), (3584, 3072), (3584, 18944)):
         assert [kernel(N, K, M) for M in (1, 4, 8)] == [1, 1, 1]
     assert kernel(64, 96, 2) == 0
