@@ -42,6 +42,13 @@ __device__ __forceinline__ float load_coherent(const float* p)
 {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Two adjacent floats (8-byte aligned) in one device-coherent 8-byte load.
+__device__ __forceinline__ f32x2_t load_coherent2(const float* p)
+{
+    const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_bit_cast(f32x2_t, v);
+}
 
 // MFMA A fragments of O^T = V^T . P^T for one 32-token group from lane (c, p)'s V bytes:
 // vr[j] = bytes d = 8c .. 8c+7 of the group's k-slot j token (two e4m3 dwords).  The 8 x 8 byte

@@ -34,6 +34,9 @@
 //     partial record and resets the ticket to zero, so no memset is needed between calls.
 //     Records are written and read with device-coherent (agent-scope) accesses, which need no
 //     cache-wide write-back or invalidate.  The tickets of different pairs lie 256 bytes apart.
+//     The merging workgroup loads its records straight into registers (a wave's (m, l) pairs of
+//     every split in one 8-byte load per lane, read across the wave with readlane) and merges
+//     with independent per-split terms: no LDS round trip and no barrier after the loads.
 #include "fp8kv_common.h"
 #include "fp8kv_status.h"
 #include "fp8kv_diag.h"
@@ -73,7 +76,7 @@ struct Params {
     const int32_t* bt;
     const float* k_scale;
     const float* v_scale;
-    float* part;            // [records][gqa * (D + 2)]: o (gqa x D), m (gqa), l (gqa)
+    float* part;            // [records][gqa * (D + 2)]: o (gqa x D), then (m, l) of each head
     uint32_t* counters;     // [kMaxPairs] tickets, indexed by ticket_slot(pair)
     int64_t q_stride, o_stride, bt_stride;
     int64_t sk0, sk1, sk2, sv0, sv1, sv2;
@@ -93,66 +96,54 @@ __host__ __device__ inline void split_span(int seqlen, int nsplit, int sp, int& 
     hi = seqlen < lo + span ? seqlen : lo + span;
 }
 
-// Final merge of up to SMAX split records in one round trip: every o value a thread needs (its
-// elements tid + T j of every split) and every split's m and l (to LDS) are requested together
-// with straight-line loads (split indices past nsplit repeat the last split and are not used), so
-// the only wait is the barrier's.  Each element then weighs split s by exp2(m_s - max_s m_s).
-// wm / wl: LDS for [nsplit][gqa] m and l.
+// Final merge of up to SMAX split records in one round trip, with no LDS and no barrier.  Every o
+// value a thread needs (its elements tid + T j of every split) and its head's (m, l) pairs are
+// requested together with straight-line loads (split indices past nsplit repeat the last split).
+// The 64 elements of a wave belong to one head (E and T are multiples of 128 and 64), so lane s
+// loads split s's (m, l) pair of that head and the wave reads all of them with readlane; each
+// element then weighs split s by exp2(m_s - max_s m_s), every split term independent of the others.
 template <int SMAX, int T>
-__device__ __forceinline__ void merge_all(const Params& P, const float* recs, int rf, int E, int gqa,
-                                          float* wm, float* wl, int tid, float vs, int64_t out_row)
+__device__ __forceinline__ void merge_regs(const Params& P, const float* recs, int rf, int E, int tid, float vs,
+                                           int64_t out_row)
 {
+    static_assert(SMAX <= 64, "one (m, l) pair per lane");
     const int ns = P.nsplit;
-    const int NSG = ns * gqa;
+    const int lane = tid & 63;
+    const int sl = lane < ns ? lane : ns - 1;
     for (int e0 = 0; e0 < E; e0 += 2 * T) {
         float ov[2][SMAX];
+        f32x2_t ml[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             int e = e0 + tid + T * j;
             e = e < E ? e : E - 1;
+            const int h = e / kD;
 #pragma unroll
             for (int s = 0; s < SMAX; ++s)
                 ov[j][s] = load_coherent(recs + (int64_t)(s < ns ? s : ns - 1) * rf + e);
+            ml[j] = load_coherent2(recs + (int64_t)sl * rf + E + 2 * h);
         }
-        if (e0 == 0) {
-            // Every m and l value goes into registers first (unconditional loads, index clamped),
-            // then to LDS: one wait covers them and the o values above.  Storing each value as it
-            // arrives put a vmcnt(0) between the m and the l loads, a second round trip.
-            constexpr int NI = (SMAX * kMaxGqa + T - 1) / T;
-            float mv[NI], lv[NI];
-#pragma unroll
-            for (int k = 0; k < NI; ++k) {
-                const int i = tid + k * T;
-                const int ic = i < NSG ? i : NSG - 1;
-                const int s = ic / gqa, h = ic - s * gqa;
-                mv[k] = load_coherent(recs + (int64_t)s * rf + E + h);
-                lv[k] = load_coherent(recs + (int64_t)s * rf + E + gqa + h);
-            }
-#pragma unroll
-            for (int k = 0; k < NI; ++k) {
-                const int i = tid + k * T;
-                if (i < NSG) {
-                    wm[i] = mv[k];
-                    wl[i] = lv[k];
-                }
-            }
-        }
-        __syncthreads();
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int e = e0 + tid + T * j;
-            if (e >= E) continue;
-            const int h = e / kD;
+            if (e >= E) continue;                      // wave-uniform
+            float ms[SMAX], ls[SMAX];
+#pragma unroll
+            for (int s = 0; s < SMAX; ++s) {
+                ms[s] = s < ns ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[j][0]), s)) : neg_inf();
+                ls[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[j][1]), s));
+            }
             float m = neg_inf();
-            for (int s = 0; s < ns; ++s) m = fmaxf(m, wm[s * gqa + h]);
+#pragma unroll
+            for (int s = 0; s < SMAX; ++s) m = fmaxf(m, ms[s]);
             const float mu = m == neg_inf() ? 0.f : m;
             float acc = 0.f, l = 0.f;
 #pragma unroll
             for (int s = 0; s < SMAX; ++s) {
                 if (s < ns) {
-                    const float f = __builtin_amdgcn_exp2f(wm[s * gqa + h] - mu);
+                    const float f = __builtin_amdgcn_exp2f(ms[s] - mu);
                     acc += f * ov[j][s];
-                    l += f * wl[s * gqa + h];
+                    l += f * ls[s];
                 }
             }
             const float r = l > 0.f ? acc * vs / l : 0.f;
@@ -297,22 +288,47 @@ __device__ __forceinline__ void decode_body(const int32_t* __restrict__ seq_lens
 
     const int E = gqa * kD;
     const int64_t pair = (int64_t)seq * P.hkv + kh;
+    // Each thread merges elements e0 + tid and e0 + tid + T over the W waves' partial states, every
+    // LDS read of both elements issued before any use (index clamped; the 64 elements of a wave
+    // share one head, so the (m, l) reads are broadcasts).
+    auto merge_waves = [&](int e, float& acc, float& mx, float& l) {
+        const int h = e / kD, d = e % kD;
+        float mw[W], lw[W], ow[W];
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            mw[w] = lds_ml[w][h][0];
+            lw[w] = lds_ml[w][h][1];
+            ow[w] = lds_o[w][h][d];
+        }
+        float m = neg_inf();
+#pragma unroll
+        for (int w = 0; w < W; ++w) m = fmaxf(m, mw[w]);
+        const float mu = m == neg_inf() ? 0.f : m;
+        acc = 0.f;
+        l = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float f = __builtin_amdgcn_exp2f(mw[w] - mu);
+            acc += f * ow[w];
+            l += f * lw[w];
+        }
+        mx = m;
+    };
     if (P.nsplit == 1) {
-        for (int e = tid; e < E; e += T) {
-            const int h = e / kD, d = e % kD;
-            float m = neg_inf();
+        for (int e0 = 0; e0 < E; e0 += 2 * T) {
+            float acc[2], m[2], l[2];
 #pragma unroll
-            for (int w = 0; w < W; ++w) m = fmaxf(m, lds_ml[w][h][0]);
-            const float mu = m == neg_inf() ? 0.f : m;
-            float acc = 0.f, l = 0.f;
-#pragma unroll
-            for (int w = 0; w < W; ++w) {
-                const float f = __builtin_amdgcn_exp2f(lds_ml[w][h][0] - mu);
-                acc += f * lds_o[w][h][d];
-                l += f * lds_ml[w][h][1];
+            for (int j = 0; j < 2; ++j) {
+                const int e = e0 + tid + T * j;
+                merge_waves(e < E ? e : E - 1, acc[j], m[j], l[j]);
             }
-            const float r = l > 0.f ? acc * vs / l : 0.f;
-            P.out[(int64_t)qtok * P.o_stride + (int64_t)(kh * gqa + h) * kD + d] = (__bf16)r;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int e = e0 + tid + T * j;
+                if (e >= E) continue;
+                const float r = l[j] > 0.f ? acc[j] * vs / l[j] : 0.f;
+                P.out[(int64_t)qtok * P.o_stride + (int64_t)(kh * gqa) * kD + e] = (__bf16)r;
+            }
         }
         return;
     }
@@ -320,23 +336,22 @@ __device__ __forceinline__ void decode_body(const int32_t* __restrict__ seq_lens
     // ---- this split's partial record -------------------------------------------------------------
     const int rf = record_floats(gqa);
     float* rec = P.part + (pair * P.nsplit + sp) * rf;
-    for (int e = tid; e < E; e += T) {
-        const int h = e / kD, d = e % kD;
-        float m = neg_inf();
+    for (int e0 = 0; e0 < E; e0 += 2 * T) {
+        float acc[2], m[2], l[2];
 #pragma unroll
-        for (int w = 0; w < W; ++w) m = fmaxf(m, lds_ml[w][h][0]);
-        const float mu = m == neg_inf() ? 0.f : m;
-        float acc = 0.f, l = 0.f;
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-            const float f = __builtin_amdgcn_exp2f(lds_ml[w][h][0] - mu);
-            acc += f * lds_o[w][h][d];
-            l += f * lds_ml[w][h][1];
+        for (int j = 0; j < 2; ++j) {
+            const int e = e0 + tid + T * j;
+            merge_waves(e < E ? e : E - 1, acc[j], m[j], l[j]);
         }
-        store_coherent(rec + e, acc);
-        if (d == 0) {
-            store_coherent(rec + E + h, m);
-            store_coherent(rec + E + gqa + h, l);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int e = e0 + tid + T * j;
+            if (e >= E) continue;
+            store_coherent(rec + e, acc[j]);
+            if (e % kD == 0) {
+                store_coherent(rec + E + 2 * (e / kD), m[j]);
+                store_coherent(rec + E + 2 * (e / kD) + 1, l[j]);
+            }
         }
     }
 
@@ -357,14 +372,16 @@ __device__ __forceinline__ void decode_body(const int32_t* __restrict__ seq_lens
     const float* recs_all = P.part + pair * P.nsplit * rf;
     const int64_t out_row = (int64_t)qtok * P.o_stride + (int64_t)(kh * gqa) * kD;
     if (P.nsplit <= 32) {
-        float* wm_all = &lds_o[0][0][0];
-        float* wl_all = wm_all + 32 * kMaxGqa;
-        if (P.nsplit <= 8)
-            merge_all<8, T>(P, recs_all, rf, E, gqa, wm_all, wl_all, tid, vs, out_row);
+        if (P.nsplit <= 2)
+            merge_regs<2, T>(P, recs_all, rf, E, tid, vs, out_row);
+        else if (P.nsplit <= 4)
+            merge_regs<4, T>(P, recs_all, rf, E, tid, vs, out_row);
+        else if (P.nsplit <= 8)
+            merge_regs<8, T>(P, recs_all, rf, E, tid, vs, out_row);
         else if (P.nsplit <= 16)
-            merge_all<16, T>(P, recs_all, rf, E, gqa, wm_all, wl_all, tid, vs, out_row);
+            merge_regs<16, T>(P, recs_all, rf, E, tid, vs, out_row);
         else
-            merge_all<32, T>(P, recs_all, rf, E, gqa, wm_all, wl_all, tid, vs, out_row);
+            merge_regs<32, T>(P, recs_all, rf, E, tid, vs, out_row);
         if (tid == 0)
             __hip_atomic_store(P.counters + ticket_slot(pair), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
@@ -394,8 +411,8 @@ __device__ __forceinline__ void decode_body(const int32_t* __restrict__ seq_lens
         if (s0 == 0) {
             for (int i = tid; i < NSG; i += T) {
                 const int s2 = i / gqa, h = i % gqa;
-                wm[i] = load_coherent(recs + (int64_t)s2 * rf + E + h);
-                wm[NSG + i] = load_coherent(recs + (int64_t)s2 * rf + E + gqa + h);
+                wm[i] = load_coherent(recs + (int64_t)s2 * rf + E + 2 * h);
+                wm[NSG + i] = load_coherent(recs + (int64_t)s2 * rf + E + 2 * h + 1);
             }
             __syncthreads();
         }
