@@ -42,6 +42,12 @@ __device__ __forceinline__ float load_coherent(const float* p)
 {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Two adjacent floats (8-byte aligned) in one device-coherent 8-byte store.
+__device__ __forceinline__ void store_coherent2(float* p, float a, float b)
+{
+    const uint64_t v = __builtin_bit_cast(uint64_t, (f32x2_t){a, b});
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 // Two adjacent floats (8-byte aligned) in one device-coherent 8-byte load.
 __device__ __forceinline__ f32x2_t load_coherent2(const float* p)
 {

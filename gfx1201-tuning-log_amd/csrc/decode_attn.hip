@@ -36,7 +36,8 @@
 //     cache-wide write-back or invalidate.  The tickets of different pairs lie 256 bytes apart.
 //     The merging workgroup loads its records straight into registers (a wave's (m, l) pairs of
 //     every split in one 8-byte load per lane, read across the wave with readlane) and merges
-//     with independent per-split terms: no LDS round trip and no barrier after the loads.
+//     with independent per-split terms: no LDS round trip and no barrier after the loads.  Both
+//     merges give each thread adjacent elements of one head, so one set of exp2 factors serves them.
 #include "fp8kv_common.h"
 #include "fp8kv_status.h"
 #include "fp8kv_diag.h"
@@ -96,59 +97,54 @@ __host__ __device__ inline void split_span(int seqlen, int nsplit, int sp, int& 
     hi = seqlen < lo + span ? seqlen : lo + span;
 }
 
-// Final merge of up to SMAX split records in one round trip, with no LDS and no barrier.  Every o
-// value a thread needs (its elements tid + T j of every split) and its head's (m, l) pairs are
-// requested together with straight-line loads (split indices past nsplit repeat the last split).
-// The 64 elements of a wave belong to one head (E and T are multiples of 128 and 64), so lane s
-// loads split s's (m, l) pair of that head and the wave reads all of them with readlane; each
-// element then weighs split s by exp2(m_s - max_s m_s), every split term independent of the others.
+// Final merge of up to SMAX split records in one round trip, with no LDS and no barrier.  Thread t
+// takes the two adjacent elements 2t, 2t + 1 (+ 2T per pass), so the 128 elements of a wave are one
+// head.  Each split's two o values (one 8-byte load) and, in lane s, split s's (m, l) pair of the
+// wave's head are requested together with straight-line loads (split indices past nsplit repeat
+// the last split); the wave reads the pairs with readlane, computes the factors exp2(m_s - max m)
+// once for both elements, and adds every split's term independently of the others.
 template <int SMAX, int T>
 __device__ __forceinline__ void merge_regs(const Params& P, const float* recs, int rf, int E, int tid, float vs,
-                                           int64_t out_row)
+                                            int64_t out_row)
 {
     static_assert(SMAX <= 64, "one (m, l) pair per lane");
     const int ns = P.nsplit;
     const int lane = tid & 63;
     const int sl = lane < ns ? lane : ns - 1;
     for (int e0 = 0; e0 < E; e0 += 2 * T) {
-        float ov[2][SMAX];
-        f32x2_t ml[2];
+        int e = e0 + 2 * tid;
+        const bool live = e < E;                       // wave-uniform
+        e = live ? e : E - 2;
+        const int h = e / kD;
+        f32x2_t ov[SMAX];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            int e = e0 + tid + T * j;
-            e = e < E ? e : E - 1;
-            const int h = e / kD;
+        for (int s = 0; s < SMAX; ++s) ov[s] = load_coherent2(recs + (int64_t)(s < ns ? s : ns - 1) * rf + e);
+        const f32x2_t ml = load_coherent2(recs + (int64_t)sl * rf + E + 2 * h);
+        if (!live) continue;
+        float ms[SMAX], ls[SMAX];
 #pragma unroll
-            for (int s = 0; s < SMAX; ++s)
-                ov[j][s] = load_coherent(recs + (int64_t)(s < ns ? s : ns - 1) * rf + e);
-            ml[j] = load_coherent2(recs + (int64_t)sl * rf + E + 2 * h);
+        for (int s = 0; s < SMAX; ++s) {
+            ms[s] = s < ns ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[0]), s)) : neg_inf();
+            ls[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[1]), s));
         }
+        float m = neg_inf();
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int e = e0 + tid + T * j;
-            if (e >= E) continue;                      // wave-uniform
-            float ms[SMAX], ls[SMAX];
+        for (int s = 0; s < SMAX; ++s) m = fmaxf(m, ms[s]);
+        const float mu = m == neg_inf() ? 0.f : m;
+        float a0 = 0.f, a1 = 0.f, l = 0.f;
 #pragma unroll
-            for (int s = 0; s < SMAX; ++s) {
-                ms[s] = s < ns ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[j][0]), s)) : neg_inf();
-                ls[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[j][1]), s));
+        for (int s = 0; s < SMAX; ++s) {
+            if (s < ns) {
+                const float f = __builtin_amdgcn_exp2f(ms[s] - mu);
+                a0 += f * ov[s][0];
+                a1 += f * ov[s][1];
+                l += f * ls[s];
             }
-            float m = neg_inf();
-#pragma unroll
-            for (int s = 0; s < SMAX; ++s) m = fmaxf(m, ms[s]);
-            const float mu = m == neg_inf() ? 0.f : m;
-            float acc = 0.f, l = 0.f;
-#pragma unroll
-            for (int s = 0; s < SMAX; ++s) {
-                if (s < ns) {
-                    const float f = __builtin_amdgcn_exp2f(ms[s] - mu);
-                    acc += f * ov[j][s];
-                    l += f * ls[s];
-                }
-            }
-            const float r = l > 0.f ? acc * vs / l : 0.f;
-            P.out[out_row + e] = (__bf16)r;
         }
+        const float r0 = l > 0.f ? a0 * vs / l : 0.f;
+        const float r1 = l > 0.f ? a1 * vs / l : 0.f;
+        P.out[out_row + e] = (__bf16)r0;
+        P.out[out_row + e + 1] = (__bf16)r1;
     }
 }
 
@@ -288,46 +284,45 @@ __device__ __forceinline__ void decode_body(const int32_t* __restrict__ seq_lens
 
     const int E = gqa * kD;
     const int64_t pair = (int64_t)seq * P.hkv + kh;
-    // Each thread merges elements e0 + tid and e0 + tid + T over the W waves' partial states, every
-    // LDS read of both elements issued before any use (index clamped; the 64 elements of a wave
-    // share one head, so the (m, l) reads are broadcasts).
-    auto merge_waves = [&](int e, float& acc, float& mx, float& l) {
+    // Each thread merges four adjacent elements of one head over the W waves' partial states: every
+    // LDS read goes out before any use (the o values of each wave in one 16-byte read, the (m, l)
+    // reads are broadcasts), and the W factors exp2(m_w - max m) serve all four elements.
+    auto merge_waves = [&](int e, f32x4_t& acc, float& mx, float& l) {
         const int h = e / kD, d = e % kD;
-        float mw[W], lw[W], ow[W];
+        float mw[W], lw[W];
+        f32x4_t ow[W];
 #pragma unroll
         for (int w = 0; w < W; ++w) {
             mw[w] = lds_ml[w][h][0];
             lw[w] = lds_ml[w][h][1];
-            ow[w] = lds_o[w][h][d];
+            ow[w] = *reinterpret_cast<const f32x4_t*>(&lds_o[w][h][d]);
         }
         float m = neg_inf();
 #pragma unroll
         for (int w = 0; w < W; ++w) m = fmaxf(m, mw[w]);
         const float mu = m == neg_inf() ? 0.f : m;
-        acc = 0.f;
+        acc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
         l = 0.f;
 #pragma unroll
         for (int w = 0; w < W; ++w) {
             const float f = __builtin_amdgcn_exp2f(mw[w] - mu);
-            acc += f * ow[w];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += f * ow[w][i];
             l += f * lw[w];
         }
         mx = m;
     };
     if (P.nsplit == 1) {
-        for (int e0 = 0; e0 < E; e0 += 2 * T) {
-            float acc[2], m[2], l[2];
+        for (int e0 = 0; e0 < E; e0 += 4 * T) {
+            const int e = e0 + 4 * tid;
+            if (e >= E) break;
+            f32x4_t acc;
+            float m, l;
+            merge_waves(e, acc, m, l);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int e = e0 + tid + T * j;
-                merge_waves(e < E ? e : E - 1, acc[j], m[j], l[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int e = e0 + tid + T * j;
-                if (e >= E) continue;
-                const float r = l[j] > 0.f ? acc[j] * vs / l[j] : 0.f;
-                P.out[(int64_t)qtok * P.o_stride + (int64_t)(kh * gqa) * kD + e] = (__bf16)r;
+            for (int i = 0; i < 4; ++i) {
+                const float r = l > 0.f ? acc[i] * vs / l : 0.f;
+                P.out[(int64_t)qtok * P.o_stride + (int64_t)(kh * gqa) * kD + e + i] = (__bf16)r;
             }
         }
         return;
@@ -336,23 +331,15 @@ __device__ __forceinline__ void decode_body(const int32_t* __restrict__ seq_lens
     // ---- this split's partial record -------------------------------------------------------------
     const int rf = record_floats(gqa);
     float* rec = P.part + (pair * P.nsplit + sp) * rf;
-    for (int e0 = 0; e0 < E; e0 += 2 * T) {
-        float acc[2], m[2], l[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int e = e0 + tid + T * j;
-            merge_waves(e < E ? e : E - 1, acc[j], m[j], l[j]);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int e = e0 + tid + T * j;
-            if (e >= E) continue;
-            store_coherent(rec + e, acc[j]);
-            if (e % kD == 0) {
-                store_coherent(rec + E + 2 * (e / kD), m[j]);
-                store_coherent(rec + E + 2 * (e / kD) + 1, l[j]);
-            }
-        }
+    for (int e0 = 0; e0 < E; e0 += 4 * T) {
+        const int e = e0 + 4 * tid;
+        if (e >= E) break;
+        f32x4_t acc;
+        float m, l;
+        merge_waves(e, acc, m, l);
+        store_coherent2(rec + e, acc[0], acc[1]);
+        store_coherent2(rec + e + 2, acc[2], acc[3]);
+        if (e % kD == 0) store_coherent2(rec + E + 2 * (e / kD), m, l);
     }
 
     // ---- ticket: the last split of this (sequence, kv head) merges --------------------------------
