@@ -48,6 +48,13 @@ __device__ __forceinline__ void store_coherent2(float* p, float a, float b)
     const uint64_t v = __builtin_bit_cast(uint64_t, (f32x2_t){a, b});
     __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Four adjacent floats (16-byte aligned) in one device-coherent 16-byte store (global_store_dwordx4
+// with the agent-scope sc1 bit; HIP's atomic stores stop at 8 bytes).  The caller waits for it
+// with s_waitcnt vmcnt like any other store.
+__device__ __forceinline__ void store_coherent4(float* p, f32x4_t v)
+{
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
 // Two adjacent floats (8-byte aligned) in one device-coherent 8-byte load.
 __device__ __forceinline__ f32x2_t load_coherent2(const float* p)
 {

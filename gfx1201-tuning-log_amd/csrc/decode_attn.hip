@@ -77,7 +77,7 @@ struct Params {
     const int32_t* bt;
     const float* k_scale;
     const float* v_scale;
-    float* part;            // [records][gqa * (D + 2)]: o (gqa x D), then (m, l) of each head
+    float* part;            // [records][record_floats(gqa)]: o (gqa x D), then (m, l) of each head
     uint32_t* counters;     // [kMaxPairs] tickets, indexed by ticket_slot(pair)
     int64_t q_stride, o_stride, bt_stride;
     int64_t sk0, sk1, sk2, sv0, sv1, sv2;
@@ -85,7 +85,9 @@ struct Params {
     int hkv, gqa, pblk, pshift, nsplit;
 };
 
-__host__ __device__ inline int record_floats(int gqa) { return gqa * (kD + 2); }
+// Floats per split record, rounded up to a multiple of four so that every record starts 16-byte
+// aligned (the workgroup merge stores four adjacent values per lane at once).
+__host__ __device__ inline int record_floats(int gqa) { return (gqa * (kD + 2) + 3) & ~3; }
 
 // Token span [lo, hi) of split `sp`: cdiv(seq_len, nsplit) rounded up to 16 tokens, so every
 // 16-token group of a span lies in one cache block when block_size % 16 == 0.
@@ -337,8 +339,7 @@ __device__ __forceinline__ void decode_body(const int32_t* __restrict__ seq_lens
         f32x4_t acc;
         float m, l;
         merge_waves(e, acc, m, l);
-        store_coherent2(rec + e, acc[0], acc[1]);
-        store_coherent2(rec + e + 2, acc[2], acc[3]);
+        store_coherent4(rec + e, acc);
         if (e % kD == 0) store_coherent2(rec + E + 2 * (e / kD), m, l);
     }
 
