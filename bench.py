@@ -42,7 +42,7 @@ ROTATE_BYTES = 1 << 30         # >= 4x the 256 MB MALL
 # (FETCH_SIZE, then WRITE_SIZE, scaled by what they read for a 256 MiB copy; commands and tables in
 # the profile named beside each).  Static: properties of the kernels as built when profiled, not
 # measured by this run (counters need the profiler).
-MEASURED_TRAFFIC = {"w4_gemv_M1": 62580498, "decode_b8_4k": 35959748, "prefill_cfg3": 33881267}
+MEASURED_TRAFFIC = {"w4_gemv_M1": 62580498, "decode_b8_4k": 35862723, "prefill_cfg3": 33881267}
 TRAFFIC_SOURCE = {
     "w4_gemv_M1": "static: profiles/h4mv_m1_mx_kernels_cfg1.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
     "decode_b8_4k": "static: profiles/decode_kernel_b8_4k.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
