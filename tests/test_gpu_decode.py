@@ -81,7 +81,7 @@ def test_b8_at_4k():
     _check(c)
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 2), (32, 2), (6, 1)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 2), (32, 2), (6, 1), (15, 5), (20, 4)])
 def test_other_head_geometries(hq, hkv):
     """(32, 8) is the reference's own geometry (vllm-fp8kv/fp8kv_v3.py:144); GQA 1 .. 16."""
     c = workloads.decode_case([777, 2048, 5], HQ=hq, HKV=hkv, seed=4)
