@@ -34,10 +34,6 @@ __device__ __forceinline__ uint32_t bf16x2_bits(bf16x2_t v) { return __builtin_b
 // Device-coherent (agent-scope) accesses for the cross-workgroup partial records: they bypass the
 // per-XCD L2 state that ordinary accesses may hit, so no cache-wide write-back or invalidate is
 // needed to hand records from one workgroup to another.
-__device__ __forceinline__ void store_coherent(float* p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ float load_coherent(const float* p)
 {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
